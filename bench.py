@@ -1,0 +1,172 @@
+"""Benchmark of the paged KV-cache hot path on one MI355X.
+
+Workload ("C2"): Llama-3-8B-shaped decode step on one
+layer — 32 query heads, 8 KV heads, head_dim 128, fp16, block_size 16, 64
+sequences with context U[512,4096], block tables drawn from a randomly permuted
+pool of 1.1x the needed blocks, Q/K/V = 0.3 N(0,1) (synthetic, seed 1).
+
+One step = KV append of one token per sequence (vkv_reshape_and_cache)
+followed by paged decode over ctx+1 keys (vkv_paged_decode), both through the
+C ABI on torch's current stream, inputs resident in HBM.
+
+Printed (rank 0, one JSON line): metric/value = decode KV bytes per step / step
+time (GB/s); roofline = the decode operation alone (its partition and merge
+kernels) timed with HIP events on the launch stream; cpu_baseline = the CPU
+oracle's decode on a sample of the same sequences.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (os.path.join(ROOT, "vllm-cpp_amd", "python"), ROOT):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E bandwidth
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(kc, vc, q, lay, cfg, num_seqs=8):
+    """CPU oracle decode (oracle/kv_oracle.c, a C restatement of the reference
+    kernel) on the first num_seqs sequences, threads = host cores (<= 16)."""
+    import numpy as np
+    import torch
+    from oracle import oracle
+    bs = cfg.block_size
+    idx = list(range(num_seqs))
+    ctx = lay.context_lens[idx]
+    nblk = (ctx + bs - 1) // bs
+    ids = np.concatenate([lay.block_tables[s, :n] for s, n in zip(idx, nblk)])
+    kk = kc[torch.from_numpy(ids).long().to(kc.device)].cpu().numpy().view(np.uint16)
+    vv = vc[torch.from_numpy(ids).long().to(vc.device)].cpu().numpy().view(np.uint16)
+    tables = np.zeros((num_seqs, int(nblk.max())), np.int32)
+    off = 0
+    for i, n in enumerate(nblk):
+        tables[i, :n] = np.arange(off, off + n)
+        off += int(n)
+    qn = q[idx].float().cpu().numpy()
+    threads = max(1, min(16, os.cpu_count() or 1))
+    oracle.paged_decode(qn[:1], kk, vv, tables[:1], np.minimum(ctx[:1], 16), cfg.scale, nthreads=1)  # tables init
+    t0 = time.perf_counter()
+    oracle.paged_decode(qn, kk, vv, tables, ctx, cfg.scale, nthreads=threads)
+    dt = time.perf_counter() - t0
+    sample_bytes = int(ctx.astype(np.int64).sum()) * cfg.num_kv_heads * cfg.head_dim * 2 * 2
+    return {"value": round(sample_bytes / dt / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"oracle decode of {num_seqs} of the {cfg.num_seqs} C2 sequences "
+                      f"({int(ctx.sum())} KV tokens, fp16 KV, fp32 math) in {dt:.2f} s on {threads} threads"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle timing")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (the paged KV path "
+              "shards by sequence or KV head with no cross-GPU exchange); run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+    import vllm_kv_amd as vkv
+    from vllm_kv_amd import workloads
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    cfg = workloads.config2()
+    lay = cfg.layout
+    S, H, Hkv, D, bs = cfg.num_seqs, cfg.num_heads, cfg.num_kv_heads, cfg.head_dim, cfg.block_size
+    g = torch.Generator(device=dev).manual_seed(cfg.seed)
+    shape = (lay.num_blocks, bs, Hkv, D)
+    kc = (torch.randn(shape, generator=g, device=dev) * cfg.sigma).half()
+    vc = (torch.randn(shape, generator=g, device=dev) * cfg.sigma).half()
+    q = (torch.randn((S, H, D), generator=g, device=dev) * cfg.sigma).half()
+    nk = (torch.randn((S, Hkv, D), generator=g, device=dev) * cfg.sigma).half()
+    nv = (torch.randn((S, Hkv, D), generator=g, device=dev) * cfg.sigma).half()
+    slots = torch.from_numpy(lay.slots(cfg.prev_lens, np.arange(S))).to(dev)
+    bt = torch.from_numpy(lay.block_tables).to(dev)
+    cl = torch.from_numpy(lay.context_lens).to(dev)
+    out = torch.empty((S, H, D), dtype=torch.float16, device=dev)
+    ws = torch.empty(vkv.decode_workspace_size(out, q, kc, vc, bt, cl, cfg.scale) // 4 + 4,
+                     dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream()
+
+    def append():
+        vkv.reshape_and_cache(nk, nv, kc, vc, slots, stream=stream)
+
+    def decode():
+        vkv.paged_decode(out, q, kc, vc, bt, cl, cfg.scale, workspace=ws, stream=stream)
+
+    def step():
+        append()
+        decode()
+
+    def timed(fn, n):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(n):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n  # ms
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    log(f"[bench] warmup done: {args.warmup} steps, pool {lay.num_blocks} blocks "
+        f"({2 * kc.numel() * 2 / 1e9:.2f} GB K+V)")
+    ms_step = timed(step, args.steps)
+    log(f"[bench] timed {args.steps} steps: {ms_step * 1e3:.1f} us/step")
+    ms_decode = timed(decode, args.steps)
+    ms_append = timed(append, args.steps)
+    log(f"[bench] decode {ms_decode * 1e3:.1f} us, append {ms_append * 1e3:.1f} us")
+
+    kv_bytes = cfg.kv_bytes(2)
+    value = kv_bytes / (ms_step * 1e-3) / 1e9
+    achieved = kv_bytes / (ms_decode * 1e-3) / 1e9
+    append_bytes = S * Hkv * D * 2 * 2 * 2 + S * 4
+    result = {
+        "metric": "paged-decode KV GB/s (% of HBM peak) @Llama-3-8B shape; decode tokens/s/GPU",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": "C2: Llama-3-8B-shaped paged decode, one layer, H32/Hkv8/D128 fp16, bs16, "
+                               "B=64, ctx U[512,4096], append 1 token + decode per step",
+                   "global_batch": S, "context_tokens": int(lay.context_lens.sum()), "seed": cfg.seed},
+        "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
+        "decode_tokens_per_s": round(S / (ms_step * 1e-3), 1),
+        "decode_tokens_per_s_32_layers": round(S / (32 * ms_step * 1e-3), 1),
+        "decode_us": round(ms_decode * 1e3, 2),
+        "append_us": round(ms_append * 1e3, 2),
+        "append_gbs": round(append_bytes / (ms_append * 1e-3) / 1e9, 2),
+        "kv_bytes_per_call": kv_bytes,
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "paged decode (partition + merge kernels), event-timed on the launch stream"},
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(kc, vc, q, lay, cfg)
+        log(f"[bench] cpu baseline: {result['cpu_baseline']['sample']}")
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

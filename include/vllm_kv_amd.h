@@ -1,0 +1,239 @@
+/*
+ * vllm_kv_amd.h — C ABI of the MI355X (gfx950) paged KV-cache hot path.
+ *
+ * Every entry point takes plain pointers, sizes and a HIP stream, launches
+ * hand-written HIP kernels on that stream and returns immediately (no host
+ * synchronisation, no hidden allocation except where stated).  All device
+ * pointers are owned by the caller.
+ *
+ * Status codes: 0 = success; > 0 = a hipError_t from the runtime;
+ * < 0 = an argument error detected on the host before any launch
+ * (see VKV_ERR_*).  vkv_last_error() returns a message for the last failing
+ * call made on the calling thread.
+ *
+ * KV cache layout (the reference's, src/memory/kv_cache.cpp:27-51):
+ *   key_cache / value_cache of one layer: [num_blocks][block_size][num_kv_heads][head_dim]
+ *   slot id s = physical_block * block_size + offset_in_block; the K/V vector of
+ *   (slot s, kv head h) starts at element (s * num_kv_heads + h) * head_dim.
+ * FP8 caches add one fp32 scale per (slot, kv head):
+ *   key_scales / value_scales of one layer: [num_blocks][block_size][num_kv_heads]
+ */
+#ifndef VLLM_KV_AMD_H
+#define VLLM_KV_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Same type as hipStream_t (struct ihipStream_t*); NULL is the null stream. */
+typedef struct ihipStream_t* vkv_stream_t;
+
+/* Element types. */
+enum {
+    VKV_DTYPE_F32 = 0,      /* IEEE binary32 */
+    VKV_DTYPE_F16 = 1,      /* IEEE binary16 */
+    VKV_DTYPE_FP8_E4M3 = 2  /* OCP 8-bit e4m3fn (bias 7, max 448, no inf); cache only */
+};
+
+/* Host-side argument errors (negative so they never collide with hipError_t). */
+enum {
+    VKV_OK = 0,
+    VKV_ERR_NULL = -1,        /* a required pointer is NULL */
+    VKV_ERR_SHAPE = -2,       /* a size is out of range or inconsistent */
+    VKV_ERR_UNSUPPORTED = -3, /* dtype / head_dim / group size combination not built */
+    VKV_ERR_WORKSPACE = -4,   /* caller workspace too small */
+    VKV_ERR_ALIGN = -5,       /* pointer or stride not aligned as required */
+    VKV_ERR_DEVICE = -6       /* no usable gfx950 device / kernel image */
+};
+
+/* Message describing the last failing call on this thread ("" if none). */
+const char* vkv_last_error(void);
+
+/* ABI version: bumped whenever a struct below changes layout. */
+int vkv_abi_version(void);
+
+/* -------------------------------------------------------------------------
+ * KV append (reshape_and_cache).
+ *
+ * Replaces the per-token pair of cudaMemcpyAsync calls of the reference's
+ * AttentionLayer::forward (src/layers/attention.cpp:84-102) with one launch:
+ * token t's K and V rows (num_kv_heads * head_dim elements) are written to
+ * slot slot_mapping[t]; slot_mapping[t] < 0 skips the token (padding) and so
+ * does a slot >= num_blocks * block_size.  The reference computes the slot as
+ * block_table[pos / block_size] * block_size + pos % block_size;
+ * vkv_slot_mapping_host() builds exactly that on the host.
+ *
+ * cache_dtype F32 requires src F32 (bit copy); F16 takes F16 (bit copy) or
+ * F32 (round to nearest even); FP8_E4M3 takes F16 or F32 and quantises per
+ * (token, kv head): amax = max|x| over head_dim, scale = amax / 448 (IEEE
+ * fp32 division, 1.0 when amax == 0), q = e4m3fn_rne_saturate(x / scale),
+ * scale stored to key_scales/value_scales[slot][kv_head].
+ * ------------------------------------------------------------------------- */
+typedef struct vkv_append_params {
+    const void* key;            /* [num_tokens, num_kv_heads, head_dim] (token stride key_stride) */
+    const void* value;          /* [num_tokens, num_kv_heads, head_dim] (token stride value_stride) */
+    int64_t key_stride;         /* elements between consecutive tokens; 0 = num_kv_heads*head_dim */
+    int64_t value_stride;
+    void* key_cache;            /* [num_blocks, block_size, num_kv_heads, head_dim] */
+    void* value_cache;
+    float* key_scales;          /* FP8 only: [num_blocks, block_size, num_kv_heads] */
+    float* value_scales;
+    const int32_t* slot_mapping;/* [num_tokens] device */
+    int32_t num_tokens;
+    int32_t num_kv_heads;
+    int32_t head_dim;
+    int32_t block_size;
+    int32_t num_blocks;
+    int32_t src_dtype;          /* VKV_DTYPE_F32 / F16 */
+    int32_t cache_dtype;        /* VKV_DTYPE_F32 / F16 / FP8_E4M3 */
+} vkv_append_params;
+
+int vkv_reshape_and_cache(const vkv_append_params* p, vkv_stream_t stream);
+
+/* Host helper: slot_mapping[t] = block_table[(ctx+t)/bs]*bs + (ctx+t)%bs for
+ * t < num_tokens (the reference's placement, src/layers/attention.cpp:85-94).
+ * Returns VKV_ERR_SHAPE if a position falls outside block_table (where the
+ * reference aborts, :87-90).  Pure host code, no device access. */
+int vkv_slot_mapping_host(const int32_t* block_table, int32_t table_len, int32_t block_size,
+                          int32_t context_len, int32_t num_tokens, int32_t* slot_mapping);
+
+/* -------------------------------------------------------------------------
+ * Paged decode attention.
+ *
+ * Replaces vllm::paged_attention_forward (src/attention/paged_attention.cu:85-93,
+ * include/vllm/attention/paged_attention.hpp:9-28).  For sequence s and query
+ * head h: kv head = h / (num_heads / num_kv_heads); ctx = min(context_lens[s],
+ * max_context_len, max_blocks_per_seq * block_size); the result is
+ * softmax(scale * q . K[0:ctx]^T) . V[0:ctx] with K/V gathered through
+ * block_tables[s][t / block_size]; ctx == 0 yields zeros.  accumulate = 1
+ * adds the result into output (the reference's `out +=`, its caller zeroes
+ * output first, src/layers/attention.cpp:128); accumulate = 0 overwrites.
+ *
+ * io_dtype (query and output): F32 or F16.  kv_dtype: F32 (io F32 only),
+ * F16 or FP8_E4M3 (needs key_scales / value_scales).  head_dim 64, 128 or
+ * 256; num_heads / num_kv_heads in 1..8.
+ *
+ * Long contexts are split into partitions of partition_size tokens that are
+ * reduced by a second kernel; that needs vkv_paged_decode_workspace_size()
+ * bytes of device workspace.  workspace == NULL uses a buffer the library
+ * owns per device (grown with hipMalloc on first use, never shrunk).
+ * ------------------------------------------------------------------------- */
+typedef struct vkv_decode_params {
+    void* output;               /* [num_seqs, num_heads, head_dim] io_dtype */
+    const void* query;          /* [num_seqs, num_heads, head_dim] io_dtype (seq stride query_stride) */
+    const void* key_cache;      /* [num_blocks, block_size, num_kv_heads, head_dim] kv_dtype */
+    const void* value_cache;
+    const float* key_scales;    /* FP8 only: [num_blocks, block_size, num_kv_heads] */
+    const float* value_scales;
+    const int32_t* block_tables;/* [num_seqs, max_blocks_per_seq] */
+    const int32_t* context_lens;/* [num_seqs] */
+    int64_t query_stride;       /* elements between sequences in query; 0 = num_heads*head_dim */
+    int32_t num_seqs;
+    int32_t num_heads;
+    int32_t num_kv_heads;
+    int32_t head_dim;
+    int32_t block_size;
+    int32_t max_context_len;
+    int32_t max_blocks_per_seq;
+    int32_t num_blocks;         /* >0: block ids outside [0,num_blocks) read block 0 instead of faulting */
+    float scale;
+    int32_t io_dtype;
+    int32_t kv_dtype;
+    int32_t accumulate;
+    int32_t partition_size;     /* tokens per split-K partition; 0 = library default */
+    void* workspace;            /* optional, see above */
+    size_t workspace_bytes;
+} vkv_decode_params;
+
+size_t vkv_paged_decode_workspace_size(const vkv_decode_params* p);
+int vkv_paged_decode(const vkv_decode_params* p, vkv_stream_t stream);
+
+/* -------------------------------------------------------------------------
+ * Chunked-prefill (and mixed) paged attention, causal.
+ *
+ * The reference runs a prompt one token at a time through the decode path
+ * (src/core/engine.cpp:157-164), so query token j of sequence s, at absolute
+ * position pos = context_lens[s] - q_len_s + j, attends keys 0..pos of that
+ * sequence.  This entry point does all of a step's query tokens at once;
+ * the chunk's own K/V must already be in the cache (vkv_reshape_and_cache).
+ * query_start_loc[s]..query_start_loc[s+1] are sequence s's rows of query.
+ * Rows with q_len 1 are plain decode.
+ * ------------------------------------------------------------------------- */
+typedef struct vkv_prefill_params {
+    void* output;               /* [num_query_tokens, num_heads, head_dim] io_dtype */
+    const void* query;          /* [num_query_tokens, num_heads, head_dim] io_dtype */
+    const void* key_cache;
+    const void* value_cache;
+    const float* key_scales;
+    const float* value_scales;
+    const int32_t* block_tables;    /* [num_seqs, max_blocks_per_seq] */
+    const int32_t* context_lens;    /* [num_seqs] total keys incl. this step's tokens */
+    const int32_t* query_start_loc; /* [num_seqs + 1] device */
+    int64_t query_stride;       /* elements between query rows; 0 = num_heads*head_dim */
+    int32_t num_seqs;
+    int32_t num_query_tokens;
+    int32_t max_query_len;      /* host bound on q_len over sequences */
+    int32_t num_heads;
+    int32_t num_kv_heads;
+    int32_t head_dim;
+    int32_t block_size;
+    int32_t max_blocks_per_seq;
+    int32_t num_blocks;
+    float scale;
+    int32_t io_dtype;
+    int32_t kv_dtype;
+} vkv_prefill_params;
+
+int vkv_paged_prefill(const vkv_prefill_params* p, vkv_stream_t stream);
+
+/* -------------------------------------------------------------------------
+ * Block copy (copy-on-write on fork) and swap (HBM <-> pinned host).
+ *
+ * No counterpart exists in the reference; the nearest hooks are
+ * BlockManager::inc_ref (src/core/block_manager.cpp:37-41) and the
+ * "for preemption / swap" BlockTable::to_id_list declaration
+ * (include/vllm/core/block_manager.hpp:39-40).  A plane is one per-layer
+ * array indexed by block id: K, V and, for FP8, the two scale arrays.  Block b
+ * of layer l of plane p starts at base + l*layer_stride_bytes + b*block_bytes.
+ * ------------------------------------------------------------------------- */
+typedef struct vkv_block_plane {
+    void* base;
+    int64_t layer_stride_bytes;
+    int64_t block_bytes;
+} vkv_block_plane;
+
+/* For every (src, dst) pair in block_pairs ([num_pairs][2], device memory) and
+ * every layer and plane: block dst <- block src.  Destinations must be
+ * distinct and no destination may appear as a source (then every copy reads
+ * the pre-call contents); both are the caller's contract, checkable on the
+ * host with vkv_check_block_pairs_host().  Ids outside [0,num_blocks) are
+ * skipped.  At most 4 planes. */
+int vkv_copy_blocks(const vkv_block_plane* planes, int32_t num_planes, int32_t num_layers,
+                    int32_t num_blocks, const int32_t* block_pairs, int32_t num_pairs,
+                    vkv_stream_t stream);
+
+int vkv_check_block_pairs_host(const int32_t* block_pairs, int32_t num_pairs, int32_t num_blocks);
+
+/* Swap.  host_base is pinned host memory from hipHostMalloc (device-accessible);
+ * host block h occupies host_block_bytes = sum over planes of
+ * num_layers*block_bytes at host_base + h*host_block_bytes, ordered
+ * [plane][layer][block bytes].  direction 0 (out): host block pair.dst <- device
+ * block pair.src; direction 1 (in): device block pair.dst <- host block pair.src.
+ * block_pairs is device memory.  Ids out of range are skipped. */
+enum { VKV_SWAP_OUT = 0, VKV_SWAP_IN = 1 };
+
+size_t vkv_swap_host_block_bytes(const vkv_block_plane* planes, int32_t num_planes, int32_t num_layers);
+
+int vkv_swap_blocks(const vkv_block_plane* dev_planes, int32_t num_planes, int32_t num_layers,
+                    int32_t num_dev_blocks, void* host_base, int32_t num_host_blocks,
+                    const int32_t* block_pairs, int32_t num_pairs, int32_t direction,
+                    vkv_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VLLM_KV_AMD_H */

@@ -1,0 +1,164 @@
+// test_host_gpu.cpp — the C++ host API on a GPU: KVCache geometry (the
+// reference's tests/unit/test_kv_cache.cpp:4-16, restated), KVCache::append and
+// vllm::paged_attention_forward against a direct host computation.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+#include <random>
+#include <vector>
+
+#include "check.hpp"
+#include "vllm/attention/paged_attention.hpp"
+#include "vllm/memory/kv_cache.hpp"
+#include "vllm/utils/hip_utils.hpp"
+
+using vllm::KVCache;
+
+TEST_CASE(kv_cache_basic_allocation) {  // reference test_kv_cache.cpp:4-10
+    KVCache cache(4, 16, 16, 8, 128);
+    CHECK_EQ(cache.num_layers(), 4u);
+    CHECK_EQ(cache.num_blocks(), 16u);
+    CHECK_EQ(cache.block_size(), 16u);
+    CHECK(cache.total_bytes() > 0);
+    CHECK_EQ(cache.total_bytes(), 2u * 4 * 16 * 16 * 8 * 128 * 4);  // fp32 by default, as in the reference
+}
+
+TEST_CASE(kv_cache_pointers_valid) {  // reference test_kv_cache.cpp:12-16
+    KVCache cache(2, 4, 8, 4, 64);
+    CHECK(cache.k_ptr(0, 0) != nullptr);
+    CHECK(cache.v_ptr(0, 0) != nullptr);
+    // per-layer and per-block strides of [L][N][bs][Hkv][D] floats
+    auto* k00 = static_cast<char*>(cache.k_ptr(0, 0));
+    CHECK_EQ(static_cast<char*>(cache.k_ptr(0, 1)) - k00, 8 * 4 * 64 * 4);
+    CHECK_EQ(static_cast<char*>(cache.k_ptr(1, 0)) - k00, 4 * 8 * 4 * 64 * 4);
+}
+
+TEST_CASE(kv_cache_fp8_geometry) {
+    KVCache cache(2, 10, 16, 8, 128, nullptr, nullptr, vllm::KVDtype::kFP8E4M3);
+    CHECK_EQ(cache.block_bytes(), 16u * 8 * 128);
+    CHECK_EQ(cache.scale_block_bytes(), 16u * 8 * 4);
+    CHECK_EQ(cache.host_block_bytes(), 2u * 2 * (16 * 8 * 128 + 16 * 8 * 4));
+    CHECK(cache.k_scale_ptr(1, 3) != nullptr);
+}
+
+TEST_CASE(append_and_paged_attention_forward_fp32) {
+    // One sequence, the reference's per-token loop replaced by KVCache::append,
+    // then vllm::paged_attention_forward with `out +=` on a zeroed output.
+    const int L = 2, N = 8, bs = 16, Hkv = 2, D = 64, H = 4, ctx = 37, layer = 1;
+    KVCache cache(L, N, bs, Hkv, D);
+    std::mt19937 gen(3);
+    std::normal_distribution<float> nd(0.f, 0.5f);
+    std::vector<float> k(ctx * Hkv * D), v(ctx * Hkv * D), q(H * D);
+    for (auto& x : k) x = nd(gen);
+    for (auto& x : v) x = nd(gen);
+    for (auto& x : q) x = nd(gen);
+    std::vector<int32_t> table = {5, 2, 7};  // 3 blocks cover 37 tokens
+    std::vector<int32_t> slots(ctx);
+    VLLM_KV_CHECK(vkv_slot_mapping_host(table.data(), 3, bs, 0, ctx, slots.data()));
+    float *dk, *dv, *dq, *dout;
+    int32_t *dslots, *dtable, *dctx;
+    VLLM_HIP_CHECK(hipMalloc(&dk, k.size() * 4));
+    VLLM_HIP_CHECK(hipMalloc(&dv, v.size() * 4));
+    VLLM_HIP_CHECK(hipMalloc(&dq, q.size() * 4));
+    VLLM_HIP_CHECK(hipMalloc(&dout, q.size() * 4));
+    VLLM_HIP_CHECK(hipMalloc(&dslots, ctx * 4));
+    VLLM_HIP_CHECK(hipMalloc(&dtable, 3 * 4));
+    VLLM_HIP_CHECK(hipMalloc(&dctx, 4));
+    VLLM_HIP_CHECK(hipMemcpy(dk, k.data(), k.size() * 4, hipMemcpyHostToDevice));
+    VLLM_HIP_CHECK(hipMemcpy(dv, v.data(), v.size() * 4, hipMemcpyHostToDevice));
+    VLLM_HIP_CHECK(hipMemcpy(dq, q.data(), q.size() * 4, hipMemcpyHostToDevice));
+    VLLM_HIP_CHECK(hipMemcpy(dslots, slots.data(), ctx * 4, hipMemcpyHostToDevice));
+    VLLM_HIP_CHECK(hipMemcpy(dtable, table.data(), 3 * 4, hipMemcpyHostToDevice));
+    const int32_t c = ctx;
+    VLLM_HIP_CHECK(hipMemcpy(dctx, &c, 4, hipMemcpyHostToDevice));
+    VLLM_HIP_CHECK(hipMemset(dout, 0, q.size() * 4));
+    cache.append(layer, dk, dv, dslots, ctx, vllm::KVDtype::kF32, nullptr);
+
+    // the appended rows sit where the reference's memcpy loop puts them
+    std::vector<float> row(Hkv * D);
+    VLLM_HIP_CHECK(hipMemcpy(row.data(), static_cast<float*>(cache.k_ptr(layer, 2)) + 4 * Hkv * D, row.size() * 4,
+                             hipMemcpyDeviceToHost));  // position 20 = block 1 (id 2), slot 4
+    bool same = true;
+    for (int i = 0; i < Hkv * D; ++i) same &= row[i] == k[20 * Hkv * D + i];
+    CHECK(same);
+
+    vllm::PagedAttentionParams p{};
+    p.output = dout;
+    p.query = dq;
+    p.key_cache = static_cast<const float*>(cache.k_ptr(layer, 0));
+    p.value_cache = static_cast<const float*>(cache.v_ptr(layer, 0));
+    p.block_tables = dtable;
+    p.context_lens = dctx;
+    p.num_seqs = 1;
+    p.num_heads = H;
+    p.num_kv_heads = Hkv;
+    p.head_dim = D;
+    p.block_size = bs;
+    p.max_context_len = N * bs;
+    p.max_blocks_per_seq = 3;
+    p.scale = 1.0f / std::sqrt(float(D));
+    p.stream = nullptr;
+    vllm::paged_attention_forward(p);
+    std::vector<float> out(q.size());
+    VLLM_HIP_CHECK(hipMemcpy(out.data(), dout, out.size() * 4, hipMemcpyDeviceToHost));
+
+    double worst = 0;
+    for (int h = 0; h < H; ++h) {
+        const int kvh = h / (H / Hkv);
+        std::vector<double> logit(ctx);
+        double m = -1e300, sum = 0;
+        for (int t = 0; t < ctx; ++t) {
+            double d = 0;
+            for (int i = 0; i < D; ++i) d += double(q[h * D + i]) * k[(t * Hkv + kvh) * D + i];
+            logit[t] = d * p.scale;
+            m = std::max(m, logit[t]);
+        }
+        for (int t = 0; t < ctx; ++t) sum += std::exp(logit[t] - m);
+        for (int i = 0; i < D; ++i) {
+            double o = 0;
+            for (int t = 0; t < ctx; ++t) o += std::exp(logit[t] - m) / sum * v[(t * Hkv + kvh) * D + i];
+            worst = std::max(worst, std::fabs(o - out[h * D + i]) / (2e-5 + 1e-4 * std::fabs(o)));
+        }
+    }
+    CHECK(worst <= 1.0);
+    if (worst > 1.0) std::printf("  worst error ratio %.3f\n", worst);
+    (void)hipFree(dk);
+    (void)hipFree(dv);
+    (void)hipFree(dq);
+    (void)hipFree(dout);
+    (void)hipFree(dslots);
+    (void)hipFree(dtable);
+    (void)hipFree(dctx);
+}
+
+TEST_CASE(copy_blocks_through_kv_cache) {
+    KVCache cache(3, 6, 16, 2, 64, nullptr, nullptr, vllm::KVDtype::kF16);
+    const size_t bytes = cache.block_bytes();
+    std::vector<uint8_t> pattern(bytes);
+    for (size_t i = 0; i < bytes; ++i) pattern[i] = uint8_t(i * 7 + 3);
+    for (int l = 0; l < 3; ++l) VLLM_HIP_CHECK(hipMemcpy(cache.k_ptr(l, 1), pattern.data(), bytes, hipMemcpyHostToDevice));
+    int32_t pairs[2] = {1, 4};
+    int32_t* dpairs;
+    VLLM_HIP_CHECK(hipMalloc(&dpairs, sizeof(pairs)));
+    VLLM_HIP_CHECK(hipMemcpy(dpairs, pairs, sizeof(pairs), hipMemcpyHostToDevice));
+    cache.copy_blocks(dpairs, 1, nullptr);
+    VLLM_HIP_CHECK(hipDeviceSynchronize());
+    std::vector<uint8_t> got(bytes);
+    bool same = true;
+    for (int l = 0; l < 3; ++l) {
+        VLLM_HIP_CHECK(hipMemcpy(got.data(), cache.k_ptr(l, 4), bytes, hipMemcpyDeviceToHost));
+        same &= got == pattern;
+    }
+    CHECK(same);
+    (void)hipFree(dpairs);
+}
+
+int main() {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0) {
+        std::printf("no GPU\n");
+        return 2;
+    }
+    return check::run_all();
+}

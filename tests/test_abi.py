@@ -1,0 +1,112 @@
+"""CPU checks of the C ABI library: it loads without a GPU, exports every symbol
+the header declares, and rejects bad arguments on the host before any launch."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "vllm_kv_amd.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(vkv_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_matches_binding_list(vkv):
+    assert declared_functions() == sorted(vkv.EXPORTED)
+
+
+def test_library_exports_every_declared_symbol(vkv):
+    lib = vkv.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    assert lib.vkv_abi_version() == 1
+
+
+def test_struct_sizes_match_header_layout(vkv):
+    # int64 after 8 pointers etc.: sizes fixed by the C layout rules (x86-64 SysV)
+    assert ctypes.sizeof(vkv.AppendParams) == 9 * 8 + 7 * 4 + 4  # trailing pad to 8
+    assert ctypes.sizeof(vkv.DecodeParams) == 8 * 8 + 8 + 14 * 4 + 8 + 8
+    assert ctypes.sizeof(vkv.BlockPlane) == 24
+
+
+def _decode_params(vkv, **over):
+    p = vkv.DecodeParams(output=16, query=16, key_cache=16, value_cache=16, block_tables=16, context_lens=16,
+                         num_seqs=2, num_heads=32, num_kv_heads=8, head_dim=128, block_size=16,
+                         max_context_len=4096, max_blocks_per_seq=256, num_blocks=1000, scale=0.088,
+                         io_dtype=1, kv_dtype=1)
+    for k, v in over.items():
+        setattr(p, k, v)
+    return p
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(num_heads=30), -2),            # not a multiple of num_kv_heads
+    (dict(num_heads=80), -3),            # group 10 > 8
+    (dict(head_dim=96), -3),
+    (dict(block_size=24), -3),           # not a power of two
+    (dict(io_dtype=1, kv_dtype=0), -3),  # fp32 KV with fp16 io
+    (dict(kv_dtype=2), -1),              # fp8 without scales
+    (dict(query=0), -1),
+    (dict(key_cache=24), -5),            # misaligned
+    (dict(max_blocks_per_seq=0), -2),
+])
+def test_decode_argument_errors(vkv, over, code):
+    lib = vkv.load()
+    p = _decode_params(vkv, **over)
+    assert lib.vkv_paged_decode(ctypes.byref(p), None) == code
+    assert lib.vkv_last_error()
+
+
+def test_decode_zero_sequences_is_noop(vkv):
+    lib = vkv.load()
+    p = _decode_params(vkv, num_seqs=0)
+    assert lib.vkv_paged_decode(ctypes.byref(p), None) == 0
+
+
+def test_workspace_size_formula(vkv):
+    lib = vkv.load()
+    p = _decode_params(vkv, num_seqs=64, max_context_len=4112, max_blocks_per_seq=257)
+    # default partition 256 tokens: ceil(4112/256) = 17 partitions of (D + 2) floats per (seq, head)
+    assert lib.vkv_paged_decode_workspace_size(ctypes.byref(p)) == 64 * 32 * 17 * (128 + 2) * 4
+
+
+def test_append_argument_errors(vkv):
+    lib = vkv.load()
+    base = dict(key=16, value=16, key_cache=16, value_cache=16, slot_mapping=16, num_tokens=4, num_kv_heads=8,
+                head_dim=128, block_size=16, num_blocks=10, src_dtype=1, cache_dtype=1)
+    p = vkv.AppendParams(**base)
+    p.key_stride = 3  # smaller than a row
+    assert lib.vkv_reshape_and_cache(ctypes.byref(p), None) == -2
+    p = vkv.AppendParams(**{**base, "cache_dtype": 2})
+    assert lib.vkv_reshape_and_cache(ctypes.byref(p), None) == -1  # fp8 needs scales
+    p = vkv.AppendParams(**{**base, "src_dtype": 1, "cache_dtype": 0})
+    assert lib.vkv_reshape_and_cache(ctypes.byref(p), None) == -3
+    p = vkv.AppendParams(**{**base, "num_tokens": 0})
+    assert lib.vkv_reshape_and_cache(ctypes.byref(p), None) == 0
+
+
+def test_slot_mapping_host_matches_reference_placement(vkv):
+    """slot = block_table[pos/bs]*bs + pos%bs (src/layers/attention.cpp:85-94); a
+    position beyond the table is an error (the reference aborts, :87-90)."""
+    lib = vkv.load()
+    table = np.array([7, 2, 9], np.int32)
+    out = np.zeros(5, np.int32)
+    assert lib.vkv_slot_mapping_host(table.ctypes.data, 3, 16, 14, 5, out.ctypes.data) == 0
+    assert out.tolist() == [7 * 16 + 14, 7 * 16 + 15, 2 * 16 + 0, 2 * 16 + 1, 2 * 16 + 2]
+    assert lib.vkv_slot_mapping_host(table.ctypes.data, 3, 16, 46, 5, out.ctypes.data) == -2
+
+
+def test_copy_pairs_check(vkv):
+    lib = vkv.load()
+    ok = np.array([[0, 5], [1, 6], [2, 7]], np.int32)
+    assert lib.vkv_check_block_pairs_host(ok.ctypes.data, 3, 8) == 0
+    bad = np.array([[0, 5], [5, 6]], np.int32)
+    assert lib.vkv_check_block_pairs_host(bad.ctypes.data, 2, 8) == -2
+    oob = np.array([[0, 8]], np.int32)
+    assert lib.vkv_check_block_pairs_host(oob.ctypes.data, 1, 8) == -2

@@ -1,0 +1,126 @@
+"""GPU parity of KV append (reshape_and_cache): bit-exact against the oracle.
+
+Reference behaviour: src/layers/attention.cpp:84-102 (each token's K/V row copied
+whole to slot block_table[pos/bs]*bs + pos%bs).  FP8 quantisation has no
+reference counterpart; its codes and scales must equal the oracle's bit for bit.
+"""
+import numpy as np
+import pytest
+
+from helpers import to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(rng, N=48, bs=16, Hkv=4, D=128, T=70, src=np.float16):
+    slots = rng.permutation(N * bs)[:T].astype(np.int32)
+    slots[3] = -1                    # padding token: skipped
+    slots[7] = N * bs + 5            # outside the pool: skipped, never written
+    k = (rng.standard_normal((T, Hkv, D), dtype=np.float32) * 0.7).astype(src)
+    v = (rng.standard_normal((T, Hkv, D), dtype=np.float32) * 0.7).astype(src)
+    return slots, k, v
+
+
+@pytest.mark.parametrize("src,cache", [(np.float16, np.float16), (np.float32, np.float32), (np.float32, np.float16)])
+@pytest.mark.parametrize("Hkv,D,bs", [(4, 128, 16), (2, 64, 16), (8, 128, 32), (1, 256, 8)])
+def test_append_bitexact(vkv, oracle, cuda, src, cache, Hkv, D, bs):
+    import torch
+    rng = np.random.default_rng(100 + Hkv * D + bs)
+    N = 40
+    slots, k, v = _case(rng, N=N, bs=bs, Hkv=Hkv, D=D, T=61, src=src)
+    kc_ref = np.zeros((N, bs, Hkv, D), cache)
+    vc_ref = np.zeros_like(kc_ref)
+    oracle.reshape_and_cache(k.view(np.uint16) if src == np.float16 else k,
+                             v.view(np.uint16) if src == np.float16 else v,
+                             kc_ref.view(np.uint16) if cache == np.float16 else kc_ref,
+                             vc_ref.view(np.uint16) if cache == np.float16 else vc_ref, slots)
+    tdt = torch.float16 if cache == np.float16 else torch.float32
+    kc = torch.zeros((N, bs, Hkv, D), dtype=tdt, device=cuda)
+    vc = torch.zeros_like(kc)
+    vkv.reshape_and_cache(to_dev(k, cuda), to_dev(v, cuda), kc, vc, to_dev(slots, cuda))
+    torch.cuda.synchronize()
+    assert np.array_equal(to_np(kc).view(np.uint8), kc_ref.view(np.uint8))
+    assert np.array_equal(to_np(vc).view(np.uint8), vc_ref.view(np.uint8))
+
+
+def test_append_strided_source(vkv, oracle, cuda):
+    """K and V as views into a fused [T, (H + 2 Hkv) * D] projection output."""
+    import torch
+    rng = np.random.default_rng(7)
+    N, bs, Hkv, D, H, T = 16, 16, 2, 64, 14, 20
+    qkv = (rng.standard_normal((T, (H + 2 * Hkv) * D), dtype=np.float32)).astype(np.float16)
+    slots = rng.permutation(N * bs)[:T].astype(np.int32)
+    k = qkv[:, H * D:(H + Hkv) * D].reshape(T, Hkv, D)
+    v = qkv[:, (H + Hkv) * D:].reshape(T, Hkv, D)
+    kc_ref = np.zeros((N, bs, Hkv, D), np.float16)
+    vc_ref = np.zeros_like(kc_ref)
+    oracle.reshape_and_cache(np.ascontiguousarray(k).view(np.uint16), np.ascontiguousarray(v).view(np.uint16),
+                             kc_ref.view(np.uint16), vc_ref.view(np.uint16), slots)
+    tq = to_dev(qkv, cuda)
+    tk = tq[:, H * D:(H + Hkv) * D].view(T, Hkv, D)
+    tv = tq[:, (H + Hkv) * D:].view(T, Hkv, D)
+    kc = torch.zeros((N, bs, Hkv, D), dtype=torch.float16, device=cuda)
+    vc = torch.zeros_like(kc)
+    vkv.reshape_and_cache(tk, tv, kc, vc, to_dev(slots, cuda))
+    torch.cuda.synchronize()
+    assert np.array_equal(to_np(kc).view(np.uint16), kc_ref.view(np.uint16))
+    assert np.array_equal(to_np(vc).view(np.uint16), vc_ref.view(np.uint16))
+
+
+@pytest.mark.parametrize("src", [np.float16, np.float32])
+@pytest.mark.parametrize("Hkv,D", [(8, 128), (2, 64), (1, 256), (4, 32)])
+def test_append_fp8_bitexact(vkv, oracle, cuda, src, Hkv, D):
+    """Codes and per-(token, head) scales equal the oracle's: amax/448, x/scale RNE-saturated."""
+    import torch
+    rng = np.random.default_rng(11 + D + Hkv)
+    N, bs, T = 32, 16, 90
+    slots, k, v = _case(rng, N=N, bs=bs, Hkv=Hkv, D=D, T=T, src=np.float32)
+    k[::9] *= 8.0                                 # outliers
+    k[5, 0] = 0.0                                 # amax == 0 -> scale 1, codes 0 (or 0x80 for -0)
+    v[6] *= 1e-5                                  # tiny values: subnormal codes
+    v[8, :, :3] = [[-0.0, 65504.0, -65504.0]] if src == np.float16 else [[-0.0, 3e4, -3e4]]
+    k = k.astype(src)
+    v = v.astype(src)
+    kc_ref = np.zeros((N, bs, Hkv, D), np.uint8)
+    vc_ref = np.zeros_like(kc_ref)
+    ks_ref = np.zeros((N, bs, Hkv), np.float32)
+    vs_ref = np.zeros_like(ks_ref)
+    o_k = k.view(np.uint16) if src == np.float16 else k
+    o_v = v.view(np.uint16) if src == np.float16 else v
+    oracle.reshape_and_cache(o_k, o_v, kc_ref, vc_ref, slots, ks_ref, vs_ref)
+    kc = torch.zeros((N, bs, Hkv, D), dtype=torch.uint8, device=cuda)
+    vc = torch.zeros_like(kc)
+    ks = torch.zeros((N, bs, Hkv), dtype=torch.float32, device=cuda)
+    vs = torch.zeros_like(ks)
+    vkv.reshape_and_cache(to_dev(k, cuda), to_dev(v, cuda), kc, vc, to_dev(slots, cuda), ks, vs)
+    torch.cuda.synchronize()
+    assert np.array_equal(to_np(ks).view(np.uint32), ks_ref.view(np.uint32))
+    assert np.array_equal(to_np(vs).view(np.uint32), vs_ref.view(np.uint32))
+    assert np.array_equal(to_np(kc), kc_ref)
+    assert np.array_equal(to_np(vc), vc_ref)
+
+
+def test_append_then_gather_is_identity_c2(vkv, cuda):
+    """Full C2 shape: appending each sequence's next token then gathering it back
+    through the block tables returns the input rows bit for bit."""
+    import torch
+    from vllm_kv_amd import workloads
+    cfg = workloads.config2()
+    lay = cfg.layout
+    S = cfg.num_seqs
+    slots = lay.slots(cfg.prev_lens, np.arange(S))
+    g = torch.Generator(device=cuda).manual_seed(1)
+    shape = (lay.num_blocks, lay.block_size, cfg.num_kv_heads, cfg.head_dim)
+    kc = torch.zeros(shape, dtype=torch.float16, device=cuda)
+    vc = torch.zeros_like(kc)
+    k = (torch.randn((S, cfg.num_kv_heads, cfg.head_dim), generator=g, device=cuda) * 0.3).half()
+    v = (torch.randn((S, cfg.num_kv_heads, cfg.head_dim), generator=g, device=cuda) * 0.3).half()
+    ts = to_dev(slots, cuda).long()
+    vkv.reshape_and_cache(k, v, kc, vc, ts.int())
+    torch.cuda.synchronize()
+    got_k = kc.view(-1, cfg.num_kv_heads, cfg.head_dim)[ts]
+    got_v = vc.view(-1, cfg.num_kv_heads, cfg.head_dim)[ts]
+    assert torch.equal(got_k.view(torch.int16), k.view(torch.int16))
+    assert torch.equal(got_v.view(torch.int16), v.view(torch.int16))
+    # nothing else was written
+    assert int((kc != 0).sum()) == int((k != 0).sum())

@@ -1,0 +1,257 @@
+"""GPU parity of paged decode attention against the oracle.
+
+The oracle restates src/attention/paged_attention.cu:13-82.  fp16 outputs must be
+within 2e-3 abs + 1e-2 rel of it; the fp32 reference-API path within
+2e-5 abs + 1e-4 rel; FP8-KV outputs within the fp16 bound of the oracle run on the
+same FP8 cache and within 3e-2 relative (Frobenius, per sequence and head) of
+the unquantised fp16 result.
+"""
+import numpy as np
+import pytest
+
+from helpers import (F16_ATOL, F16_RTOL, F32_ATOL, F32_RTOL, assert_close, to_dev, to_np)
+
+pytestmark = pytest.mark.gpu
+
+
+def _pool(rng, N, bs, Hkv, D, sigma):
+    k = (rng.standard_normal((N, bs, Hkv, D), dtype=np.float32) * sigma).astype(np.float16)
+    v = (rng.standard_normal((N, bs, Hkv, D), dtype=np.float32) * sigma).astype(np.float16)
+    return k, v
+
+
+def _layout(rng, ctx, bs, extra_blocks=3):
+    from vllm_kv_amd import workloads
+    need = int(sum((c + bs - 1) // bs for c in ctx))
+    return workloads.make_layout(np.asarray(ctx, np.int32), bs, rng, num_blocks=max(need + extra_blocks, 1),
+                                 max_blocks_per_seq=max(1, max((c + bs - 1) // bs for c in ctx)))
+
+
+def _run_decode(vkv, cuda, q, k, v, lay, scale, io, **kw):
+    import torch
+    tdt = torch.float16 if io == np.float16 else torch.float32
+    S, H, D = q.shape
+    out = torch.zeros((S, H, D), dtype=tdt, device=cuda)
+    vkv.paged_decode(out, to_dev(q.astype(io), cuda), to_dev(k, cuda), to_dev(v, cuda),
+                     to_dev(lay.block_tables, cuda), to_dev(lay.context_lens, cuda), scale, **kw)
+    torch.cuda.synchronize()
+    return to_np(out).astype(np.float32)
+
+
+CASES = [
+    # (H, Hkv, D, bs, contexts)
+    (14, 2, 64, 16, [1, 17, 255, 256, 257, 600]),
+    (32, 8, 128, 16, [1, 2, 16, 100, 511, 512, 513, 1300]),
+    (28, 4, 128, 32, [31, 32, 33, 700]),
+    (8, 8, 128, 16, [5, 300]),
+    (16, 8, 256, 8, [9, 64, 520]),
+    (24, 4, 64, 64, [1, 63, 64, 65, 1000]),
+    (40, 5, 128, 16, [77, 290]),
+    (24, 8, 128, 16, [0, 7, 33]),
+]
+
+
+@pytest.mark.parametrize("H,Hkv,D,bs,ctx", CASES)
+def test_decode_f16_vs_oracle(vkv, oracle, cuda, H, Hkv, D, bs, ctx):
+    rng = np.random.default_rng(H * 1000 + D + bs)
+    lay = _layout(rng, ctx, bs)
+    k, v = _pool(rng, lay.num_blocks, bs, Hkv, D, 0.5)
+    q = (rng.standard_normal((len(ctx), H, D), dtype=np.float32) * 0.5).astype(np.float16)
+    scale = float(1.0 / np.sqrt(np.float32(D)))
+    ref = oracle.paged_decode(q.astype(np.float32), k.view(np.uint16), v.view(np.uint16), lay.block_tables,
+                              lay.context_lens, scale)
+    got = _run_decode(vkv, cuda, q, k, v, lay, scale, np.float16)
+    assert_close(got, ref, F16_ATOL, F16_RTOL, "fp16 decode")
+
+
+@pytest.mark.parametrize("partition_size", [16, 64, 128, 512])
+def test_decode_partition_sizes(vkv, oracle, cuda, partition_size):
+    """Split-K merging is independent of where the context is cut."""
+    rng = np.random.default_rng(5)
+    ctx = [1, 15, 16, 17, 300, 1025]
+    lay = _layout(rng, ctx, 16)
+    k, v = _pool(rng, lay.num_blocks, 16, 4, 128, 0.5)
+    q = (rng.standard_normal((len(ctx), 16, 128), dtype=np.float32) * 0.5).astype(np.float16)
+    scale = 1.0 / np.sqrt(128.0)
+    ref = oracle.paged_decode(q.astype(np.float32), k.view(np.uint16), v.view(np.uint16), lay.block_tables,
+                              lay.context_lens, scale)
+    got = _run_decode(vkv, cuda, q, k, v, lay, scale, np.float16, partition_size=partition_size)
+    assert_close(got, ref, F16_ATOL, F16_RTOL, f"partition {partition_size}")
+
+
+def test_decode_f32_reference_api_semantics(vkv, oracle, cuda):
+    """fp32 Q/K/V/output, output accumulated into (reference `out +=`), ctx clamp
+    to max_context_len, ctx 0 leaves the output untouched."""
+    import torch
+    rng = np.random.default_rng(9)
+    H, Hkv, D, bs = 14, 2, 64, 16
+    ctx = [0, 1, 40, 300, 513]
+    lay = _layout(rng, ctx, bs)
+    k = rng.standard_normal((lay.num_blocks, bs, Hkv, D), dtype=np.float32) * 0.5
+    v = rng.standard_normal((lay.num_blocks, bs, Hkv, D), dtype=np.float32) * 0.5
+    q = rng.standard_normal((len(ctx), H, D), dtype=np.float32) * 0.5
+    prior = rng.standard_normal((len(ctx), H, D), dtype=np.float32)
+    scale = 0.125
+    max_ctx = 257
+    ref = oracle.paged_decode(q, k, v, lay.block_tables, lay.context_lens, scale,
+                              max_context_len=max_ctx, out=prior.copy())
+    out = to_dev(prior, cuda)
+    vkv.paged_decode(out, to_dev(q, cuda), to_dev(k, cuda), to_dev(v, cuda), to_dev(lay.block_tables, cuda),
+                     to_dev(lay.context_lens, cuda), scale, max_context_len=max_ctx, accumulate=True)
+    torch.cuda.synchronize()
+    got = to_np(out)
+    assert np.array_equal(got[0], prior[0])  # ctx 0
+    assert_close(got, ref, F32_ATOL, F32_RTOL, "fp32 decode")
+
+
+def test_decode_f32_io_f16_kv(vkv, oracle, cuda):
+    rng = np.random.default_rng(21)
+    ctx = [3, 200, 700]
+    lay = _layout(rng, ctx, 16)
+    k, v = _pool(rng, lay.num_blocks, 16, 8, 128, 0.3)
+    q = rng.standard_normal((3, 32, 128), dtype=np.float32) * 0.3
+    scale = 1.0 / np.sqrt(128.0)
+    ref = oracle.paged_decode(q, k.view(np.uint16), v.view(np.uint16), lay.block_tables, lay.context_lens, scale)
+    got = _run_decode(vkv, cuda, q, k, v, lay, scale, np.float32)
+    assert_close(got, ref, F32_ATOL, 1e-3, "fp32-io fp16-kv decode")
+
+
+def test_decode_config1_golden(vkv, cuda):
+    """C1 (Qwen2.5-0.5B layer): append one token per sequence, then decode; compare
+    with the committed golden output of the oracle (tests/golden/config1.npz)."""
+    import os
+    import sys
+    import torch
+    sys.path.insert(0, os.path.join(os.path.dirname(__file__), "golden"))
+    import make_config1
+    g = np.load(make_config1.PATH)
+    inp = make_config1.generate()
+    assert make_config1.digest(inp["key_cache"], inp["value_cache"], inp["new_k"], inp["new_v"],
+                               inp["query"]) == str(g["inputs_sha256"]), "C1 input generator drifted"
+    kc = to_dev(inp["key_cache"], cuda)
+    vc = to_dev(inp["value_cache"], cuda)
+    vkv.reshape_and_cache(to_dev(inp["new_k"], cuda), to_dev(inp["new_v"], cuda), kc, vc,
+                          to_dev(g["slot_mapping"], cuda))
+    q = to_dev(inp["query"], cuda)
+    out = torch.zeros(q.shape, dtype=torch.float16, device=cuda)
+    vkv.paged_decode(out, q, kc, vc, to_dev(g["block_tables"], cuda), to_dev(g["context_lens"], cuda),
+                     float(g["scale"]))
+    torch.cuda.synchronize()
+    assert make_config1.digest(to_np(kc), to_np(vc)) == str(g["after_sha256"])
+    assert_close(to_np(out).astype(np.float32), g["output"], F16_ATOL, F16_RTOL, "C1 golden")
+
+
+def _fp8_case(rng, ctx, H, Hkv, D, bs):
+    lay = _layout(rng, ctx, bs)
+    N = lay.num_blocks
+    k = rng.standard_normal((N, bs, Hkv, D), dtype=np.float32)
+    v = rng.standard_normal((N, bs, Hkv, D), dtype=np.float32)
+    out_mask = rng.random(k.shape) < 0.01
+    k[out_mask] *= 8
+    v[rng.random(v.shape) < 0.01] *= 8
+    return lay, k.astype(np.float16), v.astype(np.float16)
+
+
+@pytest.mark.parametrize("H,Hkv,D,bs,ctx", [(32, 8, 128, 16, [1, 130, 600, 2000]), (14, 2, 64, 16, [5, 257]),
+                                            (28, 4, 128, 32, [33, 900])])
+def test_decode_fp8(vkv, oracle, cuda, H, Hkv, D, bs, ctx):
+    import torch
+    rng = np.random.default_rng(4 + D)
+    lay, k16, v16 = _fp8_case(rng, ctx, H, Hkv, D, bs)
+    N = lay.num_blocks
+    q = rng.standard_normal((len(ctx), H, D), dtype=np.float32).astype(np.float16)
+    scale = float(1.0 / np.sqrt(np.float32(D)))
+    # quantise the whole pool with the GPU append (its bit-exactness is tested separately)
+    slots = np.arange(N * bs, dtype=np.int32)
+    kc = torch.zeros((N, bs, Hkv, D), dtype=torch.uint8, device=cuda)
+    vc = torch.zeros_like(kc)
+    ks = torch.zeros((N, bs, Hkv), dtype=torch.float32, device=cuda)
+    vs = torch.zeros_like(ks)
+    vkv.reshape_and_cache(to_dev(k16.reshape(-1, Hkv, D), cuda), to_dev(v16.reshape(-1, Hkv, D), cuda),
+                          kc, vc, to_dev(slots, cuda), ks, vs)
+    torch.cuda.synchronize()
+    out = torch.zeros((len(ctx), H, D), dtype=torch.float16, device=cuda)
+    vkv.paged_decode(out, to_dev(q, cuda), kc, vc, to_dev(lay.block_tables, cuda), to_dev(lay.context_lens, cuda),
+                     scale, key_scales=ks, value_scales=vs)
+    torch.cuda.synchronize()
+    got = to_np(out).astype(np.float32)
+    ref8 = oracle.paged_decode(q.astype(np.float32), to_np(kc), to_np(vc), lay.block_tables, lay.context_lens,
+                               scale, key_scales=to_np(ks), value_scales=to_np(vs))
+    assert_close(got, ref8, F16_ATOL, F16_RTOL, "fp8 decode vs oracle on the same fp8 cache")
+    ref16 = oracle.paged_decode(q.astype(np.float32), k16.view(np.uint16), v16.view(np.uint16), lay.block_tables,
+                                lay.context_lens, scale)
+    num = np.linalg.norm(got - ref16, axis=-1)
+    den = np.linalg.norm(ref16, axis=-1)
+    assert (num <= 3e-2 * den + 1e-6).all(), f"fp8 vs fp16 relative error {float((num / den).max()):.4f} > 3e-2"
+
+
+def test_decode_config2_sampled(vkv, oracle, cuda):
+    """Full C2 (Llama-3-8B shape, B=64, ctx U[512,4096]): append + decode on the GPU;
+    six sequences are recomputed by the oracle from their own blocks; a second
+    decode over a re-permuted pool (same contents, other block ids) must give
+    bit-identical output."""
+    import torch
+    from vllm_kv_amd import workloads
+    cfg = workloads.config2()
+    lay = cfg.layout
+    S, H, Hkv, D, bs = cfg.num_seqs, cfg.num_heads, cfg.num_kv_heads, cfg.head_dim, cfg.block_size
+    g = torch.Generator(device=cuda).manual_seed(cfg.seed)
+    shape = (lay.num_blocks, bs, Hkv, D)
+    kc = (torch.randn(shape, generator=g, device=cuda) * cfg.sigma).half()
+    vc = (torch.randn(shape, generator=g, device=cuda) * cfg.sigma).half()
+    q = (torch.randn((S, H, D), generator=g, device=cuda) * cfg.sigma).half()
+    nk = (torch.randn((S, Hkv, D), generator=g, device=cuda) * cfg.sigma).half()
+    nv = (torch.randn((S, Hkv, D), generator=g, device=cuda) * cfg.sigma).half()
+    slots = to_dev(lay.slots(cfg.prev_lens, np.arange(S)), cuda)
+    bt = to_dev(lay.block_tables, cuda)
+    cl = to_dev(lay.context_lens, cuda)
+    vkv.reshape_and_cache(nk, nv, kc, vc, slots)
+    out = torch.zeros((S, H, D), dtype=torch.float16, device=cuda)
+    vkv.paged_decode(out, q, kc, vc, bt, cl, cfg.scale)
+    torch.cuda.synchronize()
+    got = to_np(out).astype(np.float32)
+    qn = to_np(q).astype(np.float32)
+    for s in [0, 7, 19, 33, 50, 63]:
+        n = int(lay.context_lens[s])
+        nblk = (n + bs - 1) // bs
+        ids = lay.block_tables[s, :nblk]
+        kk = to_np(kc[torch.from_numpy(ids).long().to(cuda)]).view(np.uint16)
+        vv = to_np(vc[torch.from_numpy(ids).long().to(cuda)]).view(np.uint16)
+        ref = oracle.paged_decode(qn[s:s + 1], kk, vv, np.arange(nblk, dtype=np.int32)[None, :],
+                                  np.array([n], np.int32), cfg.scale)
+        assert_close(got[s:s + 1], ref, F16_ATOL, F16_RTOL, f"C2 sequence {s}")
+    # relabel every physical block: contents move, tables follow; output must not change
+    perm = torch.from_numpy(np.random.default_rng(77).permutation(lay.num_blocks)).long().to(cuda)
+    kc2 = torch.empty_like(kc)
+    vc2 = torch.empty_like(vc)
+    kc2[perm] = kc
+    vc2[perm] = vc
+    bt2 = torch.where(bt >= 0, perm[bt.long().clamp(min=0)], bt.long()).int()
+    out2 = torch.zeros_like(out)
+    vkv.paged_decode(out2, q, kc2, vc2, bt2, cl, cfg.scale)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), out2.view(torch.int16))
+
+
+def test_decode_caller_workspace_and_errors(vkv, cuda):
+    import torch
+    rng = np.random.default_rng(3)
+    ctx = [40, 900]
+    lay = _layout(rng, ctx, 16)
+    k, v = _pool(rng, lay.num_blocks, 16, 2, 64, 0.5)
+    q = (rng.standard_normal((2, 4, 64), dtype=np.float32)).astype(np.float16)
+    args = (to_dev(q, cuda), to_dev(k, cuda), to_dev(v, cuda), to_dev(lay.block_tables, cuda),
+            to_dev(lay.context_lens, cuda), 0.125)
+    out_a = torch.zeros((2, 4, 64), dtype=torch.float16, device=cuda)
+    vkv.paged_decode(out_a, *args)
+    need = vkv.decode_workspace_size(out_a, *args)
+    assert need > 0
+    ws = torch.empty(need // 4 + 4, dtype=torch.float32, device=cuda)
+    out_b = torch.zeros_like(out_a)
+    vkv.paged_decode(out_b, *args, workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(out_a, out_b)
+    small = torch.empty(16, dtype=torch.float32, device=cuda)
+    with pytest.raises(vkv.VkvError) as e:
+        vkv.paged_decode(out_b, *args, workspace=small)
+    assert e.value.code == -4

@@ -1,0 +1,189 @@
+// append.hip — KV append (reshape_and_cache) for gfx950.
+//
+// Replaces the reference's two cudaMemcpyAsync calls per token per layer
+// (src/layers/attention.cpp:84-102) with one launch over all tokens.  The
+// cache layout [block][slot][kv_head][head_dim] makes a slot's K (or V) row one
+// contiguous num_kv_heads*head_dim vector at slot * row, so the append is a row
+// scatter: every lane moves 16 destination bytes with one 16-byte load and one
+// 16-byte store per K and V, consecutive lanes on consecutive bytes.
+#include "common.hpp"
+#include "launch.hpp"
+
+namespace vkv {
+namespace {
+
+struct AppendArgs {
+    const char* key;
+    const char* value;
+    char* key_cache;
+    char* value_cache;
+    float* key_scales;
+    float* value_scales;
+    const int32_t* slot_mapping;
+    int64_t key_stride_bytes;    // source bytes between tokens
+    int64_t value_stride_bytes;
+    int64_t row_bytes;           // destination bytes of one slot (all kv heads)
+    int64_t num_slots;
+    int64_t total;               // work items
+    int32_t chunks_per_row;      // 16-byte destination chunks per row (copy kernels)
+    int32_t num_kv_heads;
+};
+
+__device__ __forceinline__ u32x4 f32x8_to_f16x8(u32x4 a, u32x4 b) {
+    u32x4 r;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const float x0 = __builtin_bit_cast(float, a[2 * i]);
+        const float x1 = __builtin_bit_cast(float, a[2 * i + 1]);
+        r[i] = uint32_t(f32_to_f16_bits(x0)) | (uint32_t(f32_to_f16_bits(x1)) << 16);
+        const float y0 = __builtin_bit_cast(float, b[2 * i]);
+        const float y1 = __builtin_bit_cast(float, b[2 * i + 1]);
+        r[2 + i] = uint32_t(f32_to_f16_bits(y0)) | (uint32_t(f32_to_f16_bits(y1)) << 16);
+    }
+    return r;
+}
+
+// Same-type append (bit copy, SRC_PER_DST = 1) or f32 -> f16 (SRC_PER_DST = 2,
+// 32 source bytes per 16 destination bytes).
+template <int SRC_PER_DST>
+__global__ __launch_bounds__(256) void append_rows_kernel(AppendArgs a) {
+    const int64_t stride = int64_t(gridDim.x) * blockDim.x;
+    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < a.total; i += stride) {
+        const int64_t t = i / a.chunks_per_row;
+        const int64_t c = i - t * a.chunks_per_row;
+        const int64_t slot = a.slot_mapping[t];
+        if (slot < 0 || slot >= a.num_slots) continue;
+        const int64_t dst = slot * a.row_bytes + c * 16;
+        const char* ks = a.key + t * a.key_stride_bytes + c * 16 * SRC_PER_DST;
+        const char* vs = a.value + t * a.value_stride_bytes + c * 16 * SRC_PER_DST;
+        if constexpr (SRC_PER_DST == 1) {
+            const u32x4 k = load16(ks);
+            const u32x4 v = load16(vs);
+            store16(a.key_cache + dst, k);
+            store16(a.value_cache + dst, v);
+        } else {
+            const u32x4 k0 = load16(ks), k1 = load16(ks + 16);
+            const u32x4 v0 = load16(vs), v1 = load16(vs + 16);
+            store16(a.key_cache + dst, f32x8_to_f16x8(k0, k1));
+            store16(a.value_cache + dst, f32x8_to_f16x8(v0, v1));
+        }
+    }
+}
+
+// Quantise-on-append to e4m3fn.  A group of LPT = head_dim/16 consecutive
+// lanes holds one (token, kv head) vector, 16 elements per lane; the group's
+// amax comes from a DPP max reduction, then every lane divides its elements by
+// the common scale (IEEE division) and stores 16 codes.
+template <typename SRC, int LPT>
+__global__ __launch_bounds__(256) void append_fp8_kernel(AppendArgs a) {
+    constexpr int SRC_BYTES = 16 * int(sizeof(SRC));
+    const int64_t stride = int64_t(gridDim.x) * blockDim.x;
+    const int64_t per_token = int64_t(a.num_kv_heads) * LPT;
+    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < a.total; i += stride) {
+        const int64_t t = i / per_token;
+        const int64_t r = i - t * per_token;  // head * LPT + sub
+        const int64_t slot = a.slot_mapping[t];
+        // Whole groups share t, so the skip below is uniform within a group.
+        if (slot < 0 || slot >= a.num_slots) continue;
+        const int64_t head = r / LPT;
+#pragma unroll
+        for (int kv = 0; kv < 2; ++kv) {
+            const char* src = (kv ? a.value + t * a.value_stride_bytes : a.key + t * a.key_stride_bytes) +
+                              r * SRC_BYTES;
+            float x[16];
+#pragma unroll
+            for (int j = 0; j < SRC_BYTES / 16; ++j) {
+                const u32x4 w = load16(src + 16 * j);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if constexpr (sizeof(SRC) == 4) {
+                        x[4 * j + e] = __builtin_bit_cast(float, w[e]);
+                    } else {
+                        x[8 * j + 2 * e] = f16_bits_to_f32(uint16_t(w[e] & 0xFFFFu));
+                        x[8 * j + 2 * e + 1] = f16_bits_to_f32(uint16_t(w[e] >> 16));
+                    }
+                }
+            }
+            float amax = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) amax = fmaxf(amax, fabsf(x[e]));
+            amax = group_max<LPT>(amax);
+            const float scale = fp8_scale_from_amax(amax);
+            u32x4 q;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                uint32_t packed = 0;
+#pragma unroll
+                for (int b = 0; b < 4; ++b) packed |= f32_to_fp8_sat(x[4 * w + b] / scale) << (8 * b);
+                q[w] = packed;
+            }
+            char* cache = kv ? a.value_cache : a.key_cache;
+            store16(cache + slot * a.row_bytes + r * 16, q);
+            if ((r % LPT) == 0) {
+                float* scales = kv ? a.value_scales : a.key_scales;
+                scales[slot * a.num_kv_heads + head] = scale;
+            }
+        }
+    }
+}
+
+int grid_for(int64_t total) {
+    int64_t blocks = (total + 255) / 256;
+    const int64_t cap = int64_t(256) * 64;  // 64 workgroups per CU, then grid-stride
+    if (blocks > cap) blocks = cap;
+    if (blocks < 1) blocks = 1;
+    return int(blocks);
+}
+
+template <typename SRC>
+int launch_fp8(const AppendArgs& a, int lpt, hipStream_t st) {
+    const int g = grid_for(a.total);
+    switch (lpt) {
+        case 1: hipLaunchKernelGGL((append_fp8_kernel<SRC, 1>), dim3(g), dim3(256), 0, st, a); break;
+        case 2: hipLaunchKernelGGL((append_fp8_kernel<SRC, 2>), dim3(g), dim3(256), 0, st, a); break;
+        case 4: hipLaunchKernelGGL((append_fp8_kernel<SRC, 4>), dim3(g), dim3(256), 0, st, a); break;
+        case 8: hipLaunchKernelGGL((append_fp8_kernel<SRC, 8>), dim3(g), dim3(256), 0, st, a); break;
+        case 16: hipLaunchKernelGGL((append_fp8_kernel<SRC, 16>), dim3(g), dim3(256), 0, st, a); break;
+        default: return -1;
+    }
+    return 0;
+}
+
+}  // namespace
+
+int launch_append(const vkv_append_params* p, hipStream_t st) {
+    const int src_eb = p->src_dtype == VKV_DTYPE_F32 ? 4 : 2;
+    const int dst_eb = p->cache_dtype == VKV_DTYPE_F32 ? 4 : p->cache_dtype == VKV_DTYPE_F16 ? 2 : 1;
+    const int64_t row = int64_t(p->num_kv_heads) * p->head_dim;
+    AppendArgs a;
+    a.key = static_cast<const char*>(p->key);
+    a.value = static_cast<const char*>(p->value);
+    a.key_cache = static_cast<char*>(p->key_cache);
+    a.value_cache = static_cast<char*>(p->value_cache);
+    a.key_scales = p->key_scales;
+    a.value_scales = p->value_scales;
+    a.slot_mapping = p->slot_mapping;
+    a.key_stride_bytes = (p->key_stride ? p->key_stride : row) * src_eb;
+    a.value_stride_bytes = (p->value_stride ? p->value_stride : row) * src_eb;
+    a.row_bytes = row * dst_eb;
+    a.num_slots = int64_t(p->num_blocks) * p->block_size;
+    a.num_kv_heads = p->num_kv_heads;
+    if (p->cache_dtype == VKV_DTYPE_FP8_E4M3) {
+        const int lpt = p->head_dim / 16;
+        a.chunks_per_row = 0;
+        a.total = int64_t(p->num_tokens) * p->num_kv_heads * lpt;
+        if (p->src_dtype == VKV_DTYPE_F32) return launch_fp8<float>(a, lpt, st);
+        return launch_fp8<_Float16>(a, lpt, st);
+    }
+    a.chunks_per_row = int32_t(a.row_bytes / 16);
+    a.total = int64_t(p->num_tokens) * a.chunks_per_row;
+    const int g = grid_for(a.total);
+    if (src_eb == dst_eb) {
+        hipLaunchKernelGGL((append_rows_kernel<1>), dim3(g), dim3(256), 0, st, a);
+    } else {
+        hipLaunchKernelGGL((append_rows_kernel<2>), dim3(g), dim3(256), 0, st, a);
+    }
+    return 0;
+}
+
+}  // namespace vkv

@@ -1,0 +1,323 @@
+// capi.cpp — the extern "C" boundary declared in include/vllm_kv_amd.h.
+//
+// Every entry point validates its arguments on the host (so that no kernel is
+// launched with a shape it does not support), then calls the launcher.  No
+// entry point synchronises the device.  The only allocation is the per-device
+// split-K workspace used when the caller passes none.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <unordered_set>
+#include <vector>
+
+#include "launch.hpp"
+#include "vllm_kv_amd.h"
+
+namespace {
+
+thread_local char g_last_error[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int hip_status(hipError_t e, const char* what) {
+    if (e == hipSuccess) return VKV_OK;
+    return fail(int(e), "%s: %s", what, hipGetErrorString(e));
+}
+
+// Launch errors (bad configuration, missing code object) surface here.
+int after_launch(int rc, const char* what) {
+    if (rc != 0) return fail(rc, "%s: no kernel compiled for this dtype/head_dim/group combination", what);
+    return hip_status(hipGetLastError(), what);
+}
+
+bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
+
+// Per-device workspace owned by the library (grow-only).
+struct DeviceWorkspace {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+std::mutex g_ws_mutex;
+std::vector<DeviceWorkspace> g_ws;
+
+int library_workspace(size_t need, void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_status(e, "hipGetDevice");
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    if (size_t(dev) >= g_ws.size()) g_ws.resize(size_t(dev) + 1);
+    DeviceWorkspace& w = g_ws[size_t(dev)];
+    if (w.bytes < need) {
+        if (w.ptr) {
+            // The old buffer may still be in use by queued work on any stream.
+            e = hipDeviceSynchronize();
+            if (e != hipSuccess) return hip_status(e, "hipDeviceSynchronize (workspace grow)");
+            (void)hipFree(w.ptr);
+            w.ptr = nullptr;
+            w.bytes = 0;
+        }
+        size_t sz = need < (size_t(1) << 20) ? (size_t(1) << 20) : need;
+        e = hipMalloc(&w.ptr, sz);
+        if (e != hipSuccess) return hip_status(e, "hipMalloc (decode workspace)");
+        w.bytes = sz;
+    }
+    *out = w.ptr;
+    return VKV_OK;
+}
+
+int check_decode(const vkv_decode_params* p) {
+    if (!p) return fail(VKV_ERR_NULL, "vkv_paged_decode: params is NULL");
+    if (p->num_seqs < 0) return fail(VKV_ERR_SHAPE, "num_seqs < 0");
+    if (p->num_seqs == 0) return VKV_OK;
+    if (!p->output || !p->query || !p->key_cache || !p->value_cache || !p->block_tables || !p->context_lens)
+        return fail(VKV_ERR_NULL, "vkv_paged_decode: a required pointer is NULL");
+    if (p->num_heads <= 0 || p->num_kv_heads <= 0 || p->num_heads % p->num_kv_heads != 0)
+        return fail(VKV_ERR_SHAPE, "num_heads (%d) must be a positive multiple of num_kv_heads (%d)", p->num_heads,
+                    p->num_kv_heads);
+    const int G = p->num_heads / p->num_kv_heads;
+    if (G > 8) return fail(VKV_ERR_UNSUPPORTED, "group size %d > 8 not built", G);
+    if (p->head_dim != 64 && p->head_dim != 128 && p->head_dim != 256)
+        return fail(VKV_ERR_UNSUPPORTED, "head_dim %d not built (64, 128, 256)", p->head_dim);
+    if (!is_pow2(p->block_size) || p->block_size > 1024)
+        return fail(VKV_ERR_UNSUPPORTED, "block_size %d must be a power of two <= 1024", p->block_size);
+    if (p->max_blocks_per_seq <= 0) return fail(VKV_ERR_SHAPE, "max_blocks_per_seq must be > 0");
+    if (p->num_blocks < 0) return fail(VKV_ERR_SHAPE, "num_blocks < 0");
+    if (p->io_dtype != VKV_DTYPE_F32 && p->io_dtype != VKV_DTYPE_F16)
+        return fail(VKV_ERR_UNSUPPORTED, "io_dtype %d unsupported", p->io_dtype);
+    if (p->kv_dtype == VKV_DTYPE_F32 && p->io_dtype != VKV_DTYPE_F32)
+        return fail(VKV_ERR_UNSUPPORTED, "fp32 KV requires fp32 query/output");
+    if (p->kv_dtype != VKV_DTYPE_F32 && p->kv_dtype != VKV_DTYPE_F16 && p->kv_dtype != VKV_DTYPE_FP8_E4M3)
+        return fail(VKV_ERR_UNSUPPORTED, "kv_dtype %d unsupported", p->kv_dtype);
+    if (p->kv_dtype == VKV_DTYPE_FP8_E4M3 && (!p->key_scales || !p->value_scales))
+        return fail(VKV_ERR_NULL, "FP8 KV needs key_scales and value_scales");
+    if (p->query_stride < 0) return fail(VKV_ERR_SHAPE, "query_stride < 0");
+    const int64_t qs = p->query_stride ? p->query_stride : int64_t(p->num_heads) * p->head_dim;
+    if (qs < int64_t(p->num_heads) * p->head_dim)
+        return fail(VKV_ERR_SHAPE, "query_stride smaller than num_heads*head_dim");
+    const int io_eb = p->io_dtype == VKV_DTYPE_F32 ? 4 : 2;
+    if ((reinterpret_cast<uintptr_t>(p->key_cache) | reinterpret_cast<uintptr_t>(p->value_cache)) & 15u)
+        return fail(VKV_ERR_ALIGN, "key_cache/value_cache must be 16-byte aligned");
+    if ((reinterpret_cast<uintptr_t>(p->query) & uintptr_t(io_eb - 1)) ||
+        (reinterpret_cast<uintptr_t>(p->output) & uintptr_t(io_eb - 1)))
+        return fail(VKV_ERR_ALIGN, "query/output misaligned for their dtype");
+    if (p->partition_size < 0) return fail(VKV_ERR_SHAPE, "partition_size < 0");
+    return VKV_OK;
+}
+
+int check_append(const vkv_append_params* p) {
+    if (!p) return fail(VKV_ERR_NULL, "vkv_reshape_and_cache: params is NULL");
+    if (p->num_tokens < 0) return fail(VKV_ERR_SHAPE, "num_tokens < 0");
+    if (p->num_tokens == 0) return VKV_OK;
+    if (!p->key || !p->value || !p->key_cache || !p->value_cache || !p->slot_mapping)
+        return fail(VKV_ERR_NULL, "vkv_reshape_and_cache: a required pointer is NULL");
+    if (p->num_kv_heads <= 0 || p->head_dim <= 0 || p->block_size <= 0 || p->num_blocks <= 0)
+        return fail(VKV_ERR_SHAPE, "num_kv_heads, head_dim, block_size, num_blocks must be > 0");
+    if (p->src_dtype != VKV_DTYPE_F32 && p->src_dtype != VKV_DTYPE_F16)
+        return fail(VKV_ERR_UNSUPPORTED, "src_dtype %d unsupported", p->src_dtype);
+    const int src_eb = p->src_dtype == VKV_DTYPE_F32 ? 4 : 2;
+    const int64_t row = int64_t(p->num_kv_heads) * p->head_dim;
+    if (p->key_stride < 0 || p->value_stride < 0) return fail(VKV_ERR_SHAPE, "negative stride");
+    const int64_t ks = p->key_stride ? p->key_stride : row;
+    const int64_t vs = p->value_stride ? p->value_stride : row;
+    if (ks < row || vs < row) return fail(VKV_ERR_SHAPE, "token stride smaller than num_kv_heads*head_dim");
+    const uintptr_t src_bits = reinterpret_cast<uintptr_t>(p->key) | reinterpret_cast<uintptr_t>(p->value) |
+                               uintptr_t(ks * src_eb) | uintptr_t(vs * src_eb);
+    const uintptr_t dst_bits = reinterpret_cast<uintptr_t>(p->key_cache) | reinterpret_cast<uintptr_t>(p->value_cache);
+    if ((src_bits | dst_bits) & 15u)
+        return fail(VKV_ERR_ALIGN, "key/value/caches and token strides must be 16-byte aligned");
+    switch (p->cache_dtype) {
+        case VKV_DTYPE_F32:
+            if (p->src_dtype != VKV_DTYPE_F32) return fail(VKV_ERR_UNSUPPORTED, "fp32 cache needs fp32 source");
+            if ((row * 4) % 16) return fail(VKV_ERR_ALIGN, "row bytes must be a multiple of 16");
+            break;
+        case VKV_DTYPE_F16:
+            if ((row * 2) % 16) return fail(VKV_ERR_ALIGN, "row bytes must be a multiple of 16");
+            break;
+        case VKV_DTYPE_FP8_E4M3: {
+            if (!p->key_scales || !p->value_scales) return fail(VKV_ERR_NULL, "FP8 cache needs scale arrays");
+            const int lpt = p->head_dim / 16;
+            if (p->head_dim % 16 || !is_pow2(lpt) || lpt > 16)
+                return fail(VKV_ERR_UNSUPPORTED, "FP8 append needs head_dim in {16,32,64,128,256}");
+            break;
+        }
+        default:
+            return fail(VKV_ERR_UNSUPPORTED, "cache_dtype %d unsupported", p->cache_dtype);
+    }
+    return VKV_OK;
+}
+
+int fill_planes(const vkv_block_plane* planes, int32_t num_planes, vkv::PlaneSet* out) {
+    if (!planes) return fail(VKV_ERR_NULL, "planes is NULL");
+    if (num_planes < 1 || num_planes > 4) return fail(VKV_ERR_SHAPE, "num_planes must be 1..4");
+    std::memset(out, 0, sizeof(*out));
+    out->num_planes = num_planes;
+    for (int i = 0; i < num_planes; ++i) {
+        if (!planes[i].base) return fail(VKV_ERR_NULL, "plane %d base is NULL", i);
+        if (planes[i].block_bytes <= 0 || planes[i].layer_stride_bytes < 0)
+            return fail(VKV_ERR_SHAPE, "plane %d has block_bytes <= 0 or negative layer stride", i);
+        out->base[i] = static_cast<char*>(planes[i].base);
+        out->layer_stride[i] = planes[i].layer_stride_bytes;
+        out->block_bytes[i] = planes[i].block_bytes;
+    }
+    return VKV_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* vkv_last_error(void) { return g_last_error; }
+
+int vkv_abi_version(void) { return 1; }
+
+int vkv_reshape_and_cache(const vkv_append_params* p, vkv_stream_t stream) {
+    int rc = check_append(p);
+    if (rc != VKV_OK || p->num_tokens == 0) return rc;
+    return after_launch(vkv::launch_append(p, reinterpret_cast<hipStream_t>(stream)), "vkv_reshape_and_cache");
+}
+
+int vkv_slot_mapping_host(const int32_t* block_table, int32_t table_len, int32_t block_size, int32_t context_len,
+                          int32_t num_tokens, int32_t* slot_mapping) {
+    if ((!block_table && table_len > 0) || (!slot_mapping && num_tokens > 0))
+        return fail(VKV_ERR_NULL, "vkv_slot_mapping_host: NULL pointer");
+    if (block_size <= 0 || table_len < 0 || context_len < 0 || num_tokens < 0)
+        return fail(VKV_ERR_SHAPE, "vkv_slot_mapping_host: bad sizes");
+    for (int32_t t = 0; t < num_tokens; ++t) {
+        const int64_t pos = int64_t(context_len) + t;
+        const int64_t logical = pos / block_size;
+        if (logical >= table_len)
+            return fail(VKV_ERR_SHAPE, "KV block table missing position %lld", static_cast<long long>(pos));
+        slot_mapping[t] = int32_t(int64_t(block_table[logical]) * block_size + pos % block_size);
+    }
+    return VKV_OK;
+}
+
+size_t vkv_paged_decode_workspace_size(const vkv_decode_params* p) {
+    if (check_decode(p) != VKV_OK || p->num_seqs == 0) return 0;
+    return vkv::plan_decode(p).workspace_bytes;
+}
+
+int vkv_paged_decode(const vkv_decode_params* p, vkv_stream_t stream) {
+    int rc = check_decode(p);
+    if (rc != VKV_OK || p->num_seqs == 0) return rc;
+    const vkv::DecodePlan plan = vkv::plan_decode(p);
+    void* ws = p->workspace;
+    if (ws) {
+        if (p->workspace_bytes < plan.workspace_bytes)
+            return fail(VKV_ERR_WORKSPACE, "workspace %zu bytes < %zu needed", p->workspace_bytes,
+                        plan.workspace_bytes);
+        if (reinterpret_cast<uintptr_t>(ws) & 15u) return fail(VKV_ERR_ALIGN, "workspace must be 16-byte aligned");
+    } else {
+        rc = library_workspace(plan.workspace_bytes, &ws);
+        if (rc != VKV_OK) return rc;
+    }
+    return after_launch(vkv::launch_decode(p, plan, ws, reinterpret_cast<hipStream_t>(stream)), "vkv_paged_decode");
+}
+
+int vkv_paged_prefill(const vkv_prefill_params* p, vkv_stream_t stream) {
+    if (!p) return fail(VKV_ERR_NULL, "vkv_paged_prefill: params is NULL");
+    if (p->num_seqs < 0 || p->num_query_tokens < 0) return fail(VKV_ERR_SHAPE, "negative size");
+    if (p->num_seqs == 0 || p->num_query_tokens == 0) return VKV_OK;
+    if (!p->query_start_loc) return fail(VKV_ERR_NULL, "query_start_loc is NULL");
+    if (p->num_query_tokens > 65535) return fail(VKV_ERR_UNSUPPORTED, "more than 65535 query rows per call");
+    // Shape/dtype rules are those of decode, with one row per query token.
+    vkv_decode_params d{};
+    d.output = p->output;
+    d.query = p->query;
+    d.key_cache = p->key_cache;
+    d.value_cache = p->value_cache;
+    d.key_scales = p->key_scales;
+    d.value_scales = p->value_scales;
+    d.block_tables = p->block_tables;
+    d.context_lens = p->context_lens;
+    d.query_stride = p->query_stride;
+    d.num_seqs = p->num_query_tokens;
+    d.num_heads = p->num_heads;
+    d.num_kv_heads = p->num_kv_heads;
+    d.head_dim = p->head_dim;
+    d.block_size = p->block_size;
+    d.max_context_len = 0x7FFFFFFF;
+    d.max_blocks_per_seq = p->max_blocks_per_seq;
+    d.num_blocks = p->num_blocks;
+    d.scale = p->scale;
+    d.io_dtype = p->io_dtype;
+    d.kv_dtype = p->kv_dtype;
+    int rc = check_decode(&d);
+    if (rc != VKV_OK) return rc;
+    const vkv::DecodePlan plan = vkv::plan_prefill(p);
+    void* ws = nullptr;
+    rc = library_workspace(plan.workspace_bytes, &ws);
+    if (rc != VKV_OK) return rc;
+    return after_launch(vkv::launch_prefill_rows(p, plan, ws, reinterpret_cast<hipStream_t>(stream)),
+                        "vkv_paged_prefill");
+}
+
+int vkv_check_block_pairs_host(const int32_t* block_pairs, int32_t num_pairs, int32_t num_blocks) {
+    if (num_pairs < 0) return fail(VKV_ERR_SHAPE, "num_pairs < 0");
+    if (num_pairs > 0 && !block_pairs) return fail(VKV_ERR_NULL, "block_pairs is NULL");
+    std::unordered_set<int32_t> dsts;
+    dsts.reserve(size_t(num_pairs) * 2);
+    for (int32_t i = 0; i < num_pairs; ++i) {
+        const int32_t s = block_pairs[2 * i], d = block_pairs[2 * i + 1];
+        if (s < 0 || s >= num_blocks || d < 0 || d >= num_blocks)
+            return fail(VKV_ERR_SHAPE, "pair %d (%d -> %d) outside [0, %d)", i, s, d, num_blocks);
+        if (!dsts.insert(d).second) return fail(VKV_ERR_SHAPE, "destination block %d repeated", d);
+    }
+    for (int32_t i = 0; i < num_pairs; ++i)
+        if (dsts.count(block_pairs[2 * i]))
+            return fail(VKV_ERR_SHAPE, "block %d is both a source and a destination", block_pairs[2 * i]);
+    return VKV_OK;
+}
+
+int vkv_copy_blocks(const vkv_block_plane* planes, int32_t num_planes, int32_t num_layers, int32_t num_blocks,
+                    const int32_t* block_pairs, int32_t num_pairs, vkv_stream_t stream) {
+    if (num_pairs < 0 || num_layers < 0 || num_blocks < 0) return fail(VKV_ERR_SHAPE, "negative size");
+    if (num_pairs == 0 || num_layers == 0) return VKV_OK;
+    if (!block_pairs) return fail(VKV_ERR_NULL, "block_pairs is NULL");
+    vkv::PlaneSet ps;
+    int rc = fill_planes(planes, num_planes, &ps);
+    if (rc != VKV_OK) return rc;
+    return after_launch(vkv::launch_copy_blocks(ps, num_layers, num_blocks, block_pairs, num_pairs,
+                                                reinterpret_cast<hipStream_t>(stream)),
+                        "vkv_copy_blocks");
+}
+
+size_t vkv_swap_host_block_bytes(const vkv_block_plane* planes, int32_t num_planes, int32_t num_layers) {
+    if (!planes || num_planes < 1 || num_planes > 4 || num_layers < 0) return 0;
+    size_t total = 0;
+    for (int i = 0; i < num_planes; ++i) total += size_t(planes[i].block_bytes) * size_t(num_layers);
+    return total;
+}
+
+int vkv_swap_blocks(const vkv_block_plane* dev_planes, int32_t num_planes, int32_t num_layers, int32_t num_dev_blocks,
+                    void* host_base, int32_t num_host_blocks, const int32_t* block_pairs, int32_t num_pairs,
+                    int32_t direction, vkv_stream_t stream) {
+    if (num_pairs < 0 || num_layers < 0 || num_dev_blocks < 0 || num_host_blocks < 0)
+        return fail(VKV_ERR_SHAPE, "negative size");
+    if (direction != VKV_SWAP_OUT && direction != VKV_SWAP_IN) return fail(VKV_ERR_SHAPE, "bad direction");
+    if (num_pairs == 0 || num_layers == 0) return VKV_OK;
+    if (!block_pairs || !host_base) return fail(VKV_ERR_NULL, "block_pairs or host_base is NULL");
+    vkv::PlaneSet ps;
+    int rc = fill_planes(dev_planes, num_planes, &ps);
+    if (rc != VKV_OK) return rc;
+    // The kernel addresses host memory through its device mapping.
+    void* dev_view = nullptr;
+    hipError_t e = hipHostGetDevicePointer(&dev_view, host_base, 0);
+    if (e != hipSuccess) return hip_status(e, "hipHostGetDevicePointer (host_base must come from hipHostMalloc)");
+    const int64_t hbb = int64_t(vkv_swap_host_block_bytes(dev_planes, num_planes, num_layers));
+    return after_launch(vkv::launch_swap_blocks(ps, num_layers, num_dev_blocks, static_cast<char*>(dev_view), hbb,
+                                                num_host_blocks, block_pairs, num_pairs, direction,
+                                                reinterpret_cast<hipStream_t>(stream)),
+                        "vkv_swap_blocks");
+}
+
+}  // extern "C"

@@ -1,0 +1,41 @@
+// launch.hpp — internal launchers behind the C ABI.  Arguments reaching these
+// functions have been validated by capi.cpp; each returns 0 or a negative
+// VKV_ERR_* for a combination that has no compiled kernel.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "vllm_kv_amd.h"
+
+namespace vkv {
+
+int launch_append(const vkv_append_params* p, hipStream_t st);
+
+// Split-K decode: partition kernel + reduce kernel.  part_o / part_ml point into
+// a workspace of decode_workspace_bytes(); partition_size already normalised.
+struct DecodePlan {
+    int partition_size;
+    int max_parts;
+    size_t workspace_bytes;
+};
+DecodePlan plan_decode(const vkv_decode_params* p);
+int launch_decode(const vkv_decode_params* p, const DecodePlan& plan, void* workspace, hipStream_t st);
+
+// Prefill through the decode kernels: one row per query token with its causal
+// context; workspace holds the partials plus the row -> (sequence, context) map.
+DecodePlan plan_prefill(const vkv_prefill_params* p);
+int launch_prefill_rows(const vkv_prefill_params* p, const DecodePlan& plan, void* workspace, hipStream_t st);
+
+struct PlaneSet {
+    char* base[4];
+    int64_t layer_stride[4];
+    int64_t block_bytes[4];
+    int32_t num_planes;
+};
+int launch_copy_blocks(const PlaneSet& planes, int32_t num_layers, int32_t num_blocks,
+                       const int32_t* pairs, int32_t num_pairs, hipStream_t st);
+int launch_swap_blocks(const PlaneSet& planes, int32_t num_layers, int32_t num_dev_blocks,
+                       char* host_base, int64_t host_block_bytes, int32_t num_host_blocks,
+                       const int32_t* pairs, int32_t num_pairs, int32_t direction, hipStream_t st);
+
+}  // namespace vkv
