@@ -104,6 +104,7 @@ TEST_CASE(append_and_paged_attention_forward_fp32) {
     VLLM_HIP_CHECK(hipMemcpy(out.data(), dout, out.size() * 4, hipMemcpyDeviceToHost));
 
     double worst = 0;
+    int printed = 0;
     for (int h = 0; h < H; ++h) {
         const int kvh = h / (H / Hkv);
         std::vector<double> logit(ctx);
@@ -118,7 +119,12 @@ TEST_CASE(append_and_paged_attention_forward_fp32) {
         for (int i = 0; i < D; ++i) {
             double o = 0;
             for (int t = 0; t < ctx; ++t) o += std::exp(logit[t] - m) / sum * v[(t * Hkv + kvh) * D + i];
-            worst = std::max(worst, std::fabs(o - out[h * D + i]) / (2e-5 + 1e-4 * std::fabs(o)));
+            const double r = std::fabs(o - out[h * D + i]) / (2e-5 + 1e-4 * std::fabs(o));
+            if (r > 1.0 && printed < 6) {
+                std::printf("  head %d dim %d: got %.6f expected %.6f\n", h, i, out[h * D + i], o);
+                ++printed;
+            }
+            worst = std::max(worst, r);
         }
     }
     CHECK(worst <= 1.0);

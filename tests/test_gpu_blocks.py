@@ -19,8 +19,9 @@ def _planes(rng, L, N, bs, Hkv, D, fp8):
         ks = rng.random((L, N, bs, Hkv), dtype=np.float32)
         vs = rng.random((L, N, bs, Hkv), dtype=np.float32)
         return [k, v, ks, vs]
-    k = rng.integers(0, 1 << 16, size=(L, N, bs, Hkv, D), dtype=np.uint16)
-    v = rng.integers(0, 1 << 16, size=(L, N, bs, Hkv, D), dtype=np.uint16)
+    # fp16 planes carried as int16 bit patterns (torch indexes int16, not uint16)
+    k = rng.integers(-(1 << 15), 1 << 15, size=(L, N, bs, Hkv, D), dtype=np.int16)
+    v = rng.integers(-(1 << 15), 1 << 15, size=(L, N, bs, Hkv, D), dtype=np.int16)
     return [k, v]
 
 

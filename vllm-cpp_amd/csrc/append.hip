@@ -33,11 +33,11 @@ __device__ __forceinline__ u32x4 f32x8_to_f16x8(u32x4 a, u32x4 b) {
     u32x4 r;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-        const float x0 = __builtin_bit_cast(float, a[2 * i]);
-        const float x1 = __builtin_bit_cast(float, a[2 * i + 1]);
+        const float x0 = as_f32(a[2 * i]);
+        const float x1 = as_f32(a[2 * i + 1]);
         r[i] = uint32_t(f32_to_f16_bits(x0)) | (uint32_t(f32_to_f16_bits(x1)) << 16);
-        const float y0 = __builtin_bit_cast(float, b[2 * i]);
-        const float y1 = __builtin_bit_cast(float, b[2 * i + 1]);
+        const float y0 = as_f32(b[2 * i]);
+        const float y1 = as_f32(b[2 * i + 1]);
         r[2 + i] = uint32_t(f32_to_f16_bits(y0)) | (uint32_t(f32_to_f16_bits(y1)) << 16);
     }
     return r;
@@ -97,7 +97,7 @@ __global__ __launch_bounds__(256) void append_fp8_kernel(AppendArgs a) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     if constexpr (sizeof(SRC) == 4) {
-                        x[4 * j + e] = __builtin_bit_cast(float, w[e]);
+                        x[4 * j + e] = as_f32(w[e]);
                     } else {
                         x[8 * j + 2 * e] = f16_bits_to_f32(uint16_t(w[e] & 0xFFFFu));
                         x[8 * j + 2 * e + 1] = f16_bits_to_f32(uint16_t(w[e] >> 16));

@@ -27,6 +27,13 @@ struct KvTraits<kF16> { static constexpr int bytes = 2; };
 template <>
 struct KvTraits<kFp8> { static constexpr int bytes = 1; };
 
+// Bit casts between 32-bit lanes and float always go through these by-value
+// helpers.  clang (ROCm 7.2) lowers __builtin_bit_cast applied directly to an
+// element of an ext_vector_type value as a read of element 0 for every index
+// (one dword load feeding all four uses), so that form is never used here.
+__device__ __forceinline__ float as_f32(uint32_t w) { return __builtin_bit_cast(float, w); }
+__device__ __forceinline__ uint32_t as_u32(float x) { return __builtin_bit_cast(uint32_t, x); }
+
 __device__ __forceinline__ u32x4 load16(const void* p) {
     return *reinterpret_cast<const u32x4*>(p);
 }

@@ -72,7 +72,7 @@ template <int KVT>
 __device__ __forceinline__ void unpack_chunk(const u32x4 w, float* v) {
     if constexpr (KVT == kF32) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = __builtin_bit_cast(float, w[i]);
+        for (int i = 0; i < 4; ++i) v[i] = as_f32(w[i]);
     } else if constexpr (KVT == kF16) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -306,7 +306,7 @@ __global__ __launch_bounds__(256) void decode_partition_kernel(DecodeArgs a) {
             for (int e = 0; e < EPL; e += 4) {
                 u32x4 w4;
 #pragma unroll
-                for (int k = 0; k < 4 && e + k < EPL; ++k) w4[k] = __builtin_bit_cast(uint32_t, acc[h][e + k]);
+                for (int k = 0; k < 4 && e + k < EPL; ++k) w4[k] = as_u32(acc[h][e + k]);
                 store16(o + e, w4);
             }
             if (sub == 0) {

@@ -108,6 +108,13 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     if not os.path.exists(path):
         raise RuntimeError(f"{path} is missing: build it with __graft_entry__.build() "
                            "(make -C vllm-cpp_amd)")
+    # torch ships its own libamdhip64.so.7.  Loading torch first makes the
+    # library bind to that runtime (same soname); loading it first would map a
+    # second HIP runtime into the process, which then sees no device.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     lib = ctypes.CDLL(path)
     lib.vkv_last_error.restype = ctypes.c_char_p
     lib.vkv_abi_version.restype = ctypes.c_int
