@@ -103,8 +103,8 @@ def main():
     bt = torch.from_numpy(lay.block_tables).to(dev)
     cl = torch.from_numpy(lay.context_lens).to(dev)
     out = torch.empty((S, H, D), dtype=torch.float16, device=dev)
-    ws = torch.empty(vkv.decode_workspace_size(out, q, kc, vc, bt, cl, cfg.scale) // 4 + 4,
-                     dtype=torch.float32, device=dev)
+    ws = torch.zeros(vkv.decode_workspace_size(out, q, kc, vc, bt, cl, cfg.scale) // 4 + 4,
+                     dtype=torch.float32, device=dev)  # first 256 bytes: counters, zero before first use
     stream = torch.cuda.current_stream()
 
     def append():

@@ -119,7 +119,10 @@ int vkv_slot_mapping_host(const int32_t* block_table, int32_t table_len, int32_t
  * Long contexts are split into partitions of partition_size tokens that are
  * reduced by a second kernel; that needs vkv_paged_decode_workspace_size()
  * bytes of device workspace.  workspace == NULL uses a buffer the library
- * owns per device (grown with hipMalloc on first use, never shrunk).
+ * owns per device (grown with hipMalloc on first use, never shrunk).  A
+ * caller workspace must have its first 1024 bytes zeroed before its first use
+ * (work counters; every call leaves them zero again), and calls that may run
+ * concurrently need distinct workspaces.  At most 16000 sequences per call.
  * ------------------------------------------------------------------------- */
 typedef struct vkv_decode_params {
     void* output;               /* [num_seqs, num_heads, head_dim] io_dtype */

@@ -72,8 +72,9 @@ def test_decode_zero_sequences_is_noop(vkv):
 def test_workspace_size_formula(vkv):
     lib = vkv.load()
     p = _decode_params(vkv, num_seqs=64, max_context_len=4112, max_blocks_per_seq=257)
-    # default partition 256 tokens: ceil(4112/256) = 17 partitions of (D + 2) floats per (seq, head)
-    assert lib.vkv_paged_decode_workspace_size(ctypes.byref(p)) == 64 * 32 * 17 * (128 + 2) * 4
+    # 1 KiB of claim counters, then partitions of 512 tokens: ceil(4112/512) = 9 partials
+    # of (D + 2) floats per (seq, head)
+    assert lib.vkv_paged_decode_workspace_size(ctypes.byref(p)) == 1024 + 64 * 32 * 9 * (128 + 2) * 4
 
 
 def test_append_argument_errors(vkv):

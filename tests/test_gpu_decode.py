@@ -250,12 +250,12 @@ def test_decode_caller_workspace_and_errors(vkv, cuda):
     vkv.paged_decode(out_a, *args)
     need = vkv.decode_workspace_size(out_a, *args)
     assert need > 0
-    ws = torch.empty(need // 4 + 4, dtype=torch.float32, device=cuda)
+    ws = torch.zeros(need // 4 + 4, dtype=torch.float32, device=cuda)  # header must start zeroed
     out_b = torch.zeros_like(out_a)
     vkv.paged_decode(out_b, *args, workspace=ws)
     torch.cuda.synchronize()
     assert torch.equal(out_a, out_b)
-    small = torch.empty(16, dtype=torch.float32, device=cuda)
+    small = torch.zeros(16, dtype=torch.float32, device=cuda)
     with pytest.raises(vkv.VkvError) as e:
         vkv.paged_decode(out_b, *args, workspace=small)
     assert e.value.code == -4

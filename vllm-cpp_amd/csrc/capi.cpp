@@ -41,6 +41,9 @@ int after_launch(int rc, const char* what) {
 
 bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
 
+// The decode kernel keeps one prefix entry per sequence (row) in LDS.
+constexpr int kMaxRows = 16000;
+
 // Per-device workspace owned by the library (grow-only).
 struct DeviceWorkspace {
     void* ptr = nullptr;
@@ -68,6 +71,9 @@ int library_workspace(size_t need, void** out) {
         size_t sz = need < (size_t(1) << 20) ? (size_t(1) << 20) : need;
         e = hipMalloc(&w.ptr, sz);
         if (e != hipSuccess) return hip_status(e, "hipMalloc (decode workspace)");
+        // The first 1 KiB holds the decode claim counters, which must start at zero.
+        e = hipMemset(w.ptr, 0, 1024);
+        if (e != hipSuccess) return hip_status(e, "hipMemset (decode workspace header)");
         w.bytes = sz;
     }
     *out = w.ptr;
@@ -110,6 +116,8 @@ int check_decode(const vkv_decode_params* p) {
         (reinterpret_cast<uintptr_t>(p->output) & uintptr_t(io_eb - 1)))
         return fail(VKV_ERR_ALIGN, "query/output misaligned for their dtype");
     if (p->partition_size < 0) return fail(VKV_ERR_SHAPE, "partition_size < 0");
+    if (p->num_seqs > kMaxRows)
+        return fail(VKV_ERR_UNSUPPORTED, "more than %d sequences (rows) per call", kMaxRows);
     return VKV_OK;
 }
 
@@ -228,7 +236,6 @@ int vkv_paged_prefill(const vkv_prefill_params* p, vkv_stream_t stream) {
     if (p->num_seqs < 0 || p->num_query_tokens < 0) return fail(VKV_ERR_SHAPE, "negative size");
     if (p->num_seqs == 0 || p->num_query_tokens == 0) return VKV_OK;
     if (!p->query_start_loc) return fail(VKV_ERR_NULL, "query_start_loc is NULL");
-    if (p->num_query_tokens > 65535) return fail(VKV_ERR_UNSUPPORTED, "more than 65535 query rows per call");
     // Shape/dtype rules are those of decode, with one row per query token.
     vkv_decode_params d{};
     d.output = p->output;

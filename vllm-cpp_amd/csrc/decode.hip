@@ -17,12 +17,18 @@
 // slice of the G query vectors in registers; the per-token dot is completed by
 // a DPP butterfly over the LPT lanes.
 //
-// Phases per item: (A) logits of the partition into this wave's LDS slice,
-// tracking the running max; (B) p = exp2(logit - max) in place and its sum;
-// (C) o = sum p * V with fp32 accumulators, reduced across the TPL token lanes.
-// The partial (o, max, sum) goes to the workspace; a second kernel merges the
-// partitions of every (sequence, head) with the usual log-sum-exp rescale.
-// Logits are kept in the log2 domain (scale * log2 e folded into the scale).
+// Single pass per item (online softmax): each chunk of CH = U*TPL tokens
+// issues its K and V loads together (2U independent loads per lane, 8 KiB per
+// wave for D=128 fp16), computes the chunk's logits, raises the running max
+// (rescaling the accumulators only when it grows, a wave-uniform branch), then
+// accumulates p * V in fp32.  No LDS is used, so occupancy is bounded by VGPRs
+// alone and any partition size works.  The partial (o, max, sum) of the item
+// goes to the workspace; a second kernel merges the partitions of every
+// (sequence, head) with the usual log-sum-exp rescale.  Logits live in the
+// log2 domain (scale * log2 e folded into the scale).
+//
+// FP8 lanes load 8 bytes (8 codes) so that fp8 and fp16 share one lane layout
+// (D=128: 16 lanes per token) and one register footprint.
 #include <type_traits>
 
 #include "common.hpp"
@@ -32,7 +38,22 @@ namespace vkv {
 namespace {
 
 constexpr int kWavesPerBlock = 4;
-constexpr int kLoadsPerChunk = 4;  // independent 16-byte loads in flight per lane per chunk
+// Workspace layout: a 1 KiB header holding the work-claim counters (zero
+// between calls: the merge kernel resets them) followed by the partials.
+constexpr size_t kWorkspaceHeader = 1024;
+constexpr int kClaimSequences = 8;
+constexpr int kCounterStride = 32;  // ints: one 128-byte line per counter
+// Loads per lane per chunk for group sizes <= 4 (half that above): 8 keeps
+// 16 KiB of K/V in flight per wave at D=128 fp16.  Build-time tuning knob.
+#ifndef VKV_DECODE_UNROLL
+#define VKV_DECODE_UNROLL 4
+#endif
+constexpr int kUnroll = VKV_DECODE_UNROLL;
+// Register budget: at least this many waves per SIMD (3 -> at most 168 VGPRs).
+#ifndef VKV_DECODE_MIN_WAVES
+#define VKV_DECODE_MIN_WAVES 3
+#endif
+constexpr int kMinWavesPerSimd = VKV_DECODE_MIN_WAVES;
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct DecodeArgs {
@@ -59,17 +80,37 @@ struct DecodeArgs {
     int32_t max_parts;
     float scale_log2;
     int32_t accumulate;
+    int32_t num_rows;         // sequences (decode) or query rows (prefill)
+    int* counters;            // claim counters in the workspace header (zero between calls)
 };
 
-template <typename IO>
-__device__ __forceinline__ float io_to_f32(IO x) {
-    return static_cast<float>(x);
+template <int KVT>
+struct LaneLoad {
+    static constexpr int bytes = KVT == kFp8 ? 8 : 16;  // bytes per lane per load
+    static constexpr int words = bytes / 4;
+    static constexpr int elems = bytes / KvTraits<KVT>::bytes;
+};
+
+template <int KVT>
+__device__ __forceinline__ void load_lane(const char* p, uint32_t* w) {
+    if constexpr (LaneLoad<KVT>::bytes == 16) {
+        const u32x4 v = load16(p);
+        w[0] = v[0];
+        w[1] = v[1];
+        w[2] = v[2];
+        w[3] = v[3];
+    } else {
+        typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+        const u32x2 v = *reinterpret_cast<const u32x2*>(p);
+        w[0] = v[0];
+        w[1] = v[1];
+    }
 }
 
-// Unpack one 16-byte KV chunk into EPL floats in dimension order.  FP8 values
-// come out scaled by 2^-8 (the caller folds 256 into its per-token scale).
+// Unpack one lane load into EPL floats in dimension order.  FP8 values come out
+// scaled by 2^-8 (the caller folds 256 into its per-token scale).
 template <int KVT>
-__device__ __forceinline__ void unpack_chunk(const u32x4 w, float* v) {
+__device__ __forceinline__ void unpack_lane(const uint32_t* w, float* v) {
     if constexpr (KVT == kF32) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) v[i] = as_f32(w[i]);
@@ -82,7 +123,7 @@ __device__ __forceinline__ void unpack_chunk(const u32x4 w, float* v) {
         }
     } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < 2; ++i) {
             uint32_t lo, hi;
             fp8x4_to_half2x2_scaled(w[i], lo, hi);
             const half2_t a = as_half2(lo), b = as_half2(hi);
@@ -94,36 +135,36 @@ __device__ __forceinline__ void unpack_chunk(const u32x4 w, float* v) {
     }
 }
 
+// One work item: partition `part` of row s (a sequence, or a prefill query
+// row) for kv head kvh, computed by the calling wave alone.  Writes the
+// item's partial (o, max, sum) to the workspace.
 template <typename IO, int KVT, int D, int G>
-__global__ __launch_bounds__(256) void decode_partition_kernel(DecodeArgs a) {
+__device__ __forceinline__ void decode_item(const DecodeArgs& a, const int s, const int kvh, const int part,
+                                            const int lane) {
     constexpr int EB = KvTraits<KVT>::bytes;
-    constexpr int EPL = 16 / EB;      // elements per lane per load
-    constexpr int LPT = D / EPL;      // lanes per token
-    constexpr int TPL = kWave / LPT;  // tokens per wave-wide load
-    constexpr int U = kLoadsPerChunk;
-    constexpr int CH = U * TPL;       // tokens per chunk
+    constexpr int LW = LaneLoad<KVT>::words;
+    constexpr int EPL = LaneLoad<KVT>::elems;  // elements per lane per load
+    constexpr int LPT = D / EPL;               // lanes per token
+    constexpr int TPL = kWave / LPT;           // tokens per wave-wide load
+    constexpr int U = G <= 4 ? kUnroll : kUnroll / 2;  // loads per lane per chunk, for K and for V
+    constexpr int CH = U * TPL;                // tokens per chunk
     // fp16 query against fp16 or fp8 keys: packed fp16 dot products (v_dot2_f32_f16).
     constexpr bool HALF_DOT = std::is_same<IO, _Float16>::value && KVT != kF32;
     static_assert(LPT >= 1 && LPT <= kWave && (kWave % LPT) == 0, "head_dim / dtype mapping");
 
-    extern __shared__ float lds[];
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
-    const int s = blockIdx.z;
-    const int kvh = blockIdx.y;
-    const int part = blockIdx.x * kWavesPerBlock + wave;
-    if (part >= a.max_parts) return;
     const int seq = a.row_seq ? a.row_seq[s] : s;
     int ctx = a.row_ctx ? a.row_ctx[s] : a.cl[s];
     ctx = ctx < a.max_ctx ? ctx : a.max_ctx;
     const int t0 = part * a.P;
-    if (t0 >= ctx) return;  // whole wave leaves; no workgroup barrier is used
+    if (t0 >= ctx) return;
     const int n = (ctx - t0) < a.P ? (ctx - t0) : a.P;
-    float* lg = lds + wave * G * a.P;  // [G][P] logits, then probabilities
 
-    const int sub = lane % LPT;  // which 16-byte slice of the head vector
+    const int sub = lane % LPT;  // which slice of the head vector
     const int grp = lane / LPT;  // which token of a wave-wide load
     const int bs_mask = (1 << a.bs_log2) - 1;
+    // A wave-wide load never straddles a block when block_size >= TPL: then
+    // its block id is wave-uniform and comes from one readlane.
+    const bool load_in_block = (1 << a.bs_log2) >= TPL;
 
     // Physical block ids of this partition, one per lane (P / block_size <= 64).
     const int nb = (n + bs_mask) >> a.bs_log2;
@@ -159,142 +200,243 @@ __global__ __launch_bounds__(256) void decode_partition_kernel(DecodeArgs a) {
             }
         } else {
 #pragma unroll
-            for (int e = 0; e < EPL; ++e) qf[h][e] = io_to_f32(qp[e]);
+            for (int e = 0; e < EPL; ++e) qf[h][e] = static_cast<float>(qp[e]);
         }
     }
 
-    const int64_t head_off_bytes = (int64_t(kvh) * D + sub * EPL) * EB;
-    const int64_t slot_stride_bytes = int64_t(a.num_kv_heads) * D * EB;
-    float logit_scale = a.scale_log2;
-    if constexpr (KVT == kFp8) logit_scale *= kFp8HalfScale;
-
-    // ---------------- phase A: logits
-    float mx[G];
+    // The max is tracked on raw dots, which needs a positive scale: a negative
+    // one is moved into the query (exact sign flip).
+    const bool neg_scale = a.scale_log2 < 0.0f;
+    if (neg_scale) {
 #pragma unroll
-    for (int h = 0; h < G; ++h) mx[h] = -INFINITY;
-
-    for (int c = 0; c < n; c += CH) {
-        u32x4 kr[U];
-        float ksc[U];
-        bool valid[U];
-        int tok[U];
+        for (int h = 0; h < G; ++h) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            tok[u] = c + u * TPL + grp;
-            valid[u] = tok[u] < n;
-            const int blk = __shfl(my_block, tok[u] >> a.bs_log2, kWave);
-            const int64_t slot = (int64_t(blk) << a.bs_log2) + (tok[u] & bs_mask);
-            kr[u] = valid[u] ? load16(a.kc + slot * slot_stride_bytes + head_off_bytes) : u32x4{0, 0, 0, 0};
-            if constexpr (KVT == kFp8) ksc[u] = valid[u] ? a.ks[slot * a.num_kv_heads + kvh] : 0.0f;
+            for (int i = 0; i < QW; ++i) qh[h][i] ^= 0x80008000u;
+#pragma unroll
+            for (int e = 0; e < QF; ++e) qf[h][e] = -qf[h][e];
         }
+    }
+
+    // Byte offsets: slots are slot_stride apart, blocks block_stride apart.  A
+    // lane's offset inside a chunk is fixed (its token row and head slice), so
+    // full chunks address K/V as (wave-uniform block base) + (32-bit lane offset).
+    const uint32_t slot_stride = uint32_t(a.num_kv_heads) * D * EB;
+    const int64_t block_stride = int64_t(slot_stride) << a.bs_log2;
+    const uint32_t lane_off = uint32_t(grp) * slot_stride + uint32_t(kvh * D + sub * EPL) * EB;
+    // Running max m is kept on raw dot products (fp8: times the key scale);
+    // sc turns raw values into log2-domain logits inside the exp2 argument.
+    float sc = neg_scale ? -a.scale_log2 : a.scale_log2;
+    if constexpr (KVT == kFp8) sc *= kFp8HalfScale;
+    // fp16 V: p * V as packed dot products over token pairs, weights rounded to fp16.
+    constexpr bool PAIR_PV = HALF_DOT && KVT == kF16 && (U % 2) == 0;
+
+    float m[G], l[G], acc[G][EPL];
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        m[h] = -INFINITY;
+        l[h] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[h][e] = 0.0f;
+    }
+
+    // Registers of one chunk of CH tokens: K and V lane loads (plus FP8 scales).
+    struct ChunkRegs {
+        uint32_t k[U][LW];
+        uint32_t v[U][LW];
+        float ks[U];
+        float vs[U];
+    };
+
+    // Issue the loads of the chunk starting at token c.  TAIL: the last,
+    // partly valid chunk (masked); other chunks carry no validity checks.
+    auto load_chunk = [&](ChunkRegs& b, const int c, auto) __attribute__((always_inline)) {
+        if (load_in_block) {
+            // Each wave-wide load covers TPL consecutive tokens of one block, so
+            // its base address is wave-uniform (scalar) and every lane adds the
+            // same 32-bit offset: no per-load vector address arithmetic.
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int tu = c + u * TPL;
+                const int blk = __builtin_amdgcn_readlane(my_block, (tu >> a.bs_log2) & 63);
+                const int64_t boff = int64_t(blk) * block_stride + int64_t(tu & bs_mask) * slot_stride;
+                load_lane<KVT>(a.kc + boff + lane_off, b.k[u]);
+                load_lane<KVT>(a.vc + boff + lane_off, b.v[u]);
+                if constexpr (KVT == kFp8) {
+                    const int64_t si = ((int64_t(blk) << a.bs_log2) + (tu & bs_mask) + grp) * a.num_kv_heads + kvh;
+                    b.ks[u] = a.ks[si];
+                    b.vs[u] = a.vs[si] * kFp8HalfScale;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int tok = c + u * TPL + grp;
+                const int blk = __shfl(my_block, (tok >> a.bs_log2) & 63, kWave);
+                const int64_t slot = (int64_t(blk) << a.bs_log2) + (tok & bs_mask);
+                const int64_t off = slot * slot_stride + (lane_off - uint32_t(grp) * slot_stride);
+                load_lane<KVT>(a.kc + off, b.k[u]);
+                load_lane<KVT>(a.vc + off, b.v[u]);
+                if constexpr (KVT == kFp8) {
+                    b.ks[u] = a.ks[slot * a.num_kv_heads + kvh];
+                    b.vs[u] = a.vs[slot * a.num_kv_heads + kvh] * kFp8HalfScale;
+                }
+            }
+        }
+    };
+
+    // Consume a loaded chunk: logits, running max, weights, p * V.
+    auto compute_chunk = [&](const ChunkRegs& b_in, auto tail_tag, const int c = 0) __attribute__((always_inline)) {
+        constexpr bool TAIL = decltype(tail_tag)::value;
+        // In the last chunk, tokens at or past n are masked: their logit is
+        // -inf, their weight 0 and their V zero (whatever the memory held).
+        bool valid[U];
+        ChunkRegs b = b_in;
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            float d[G];
+            valid[u] = !TAIL || (c + u * TPL + grp < n);
+            if constexpr (TAIL) {
+#pragma unroll
+                for (int w = 0; w < LW; ++w) b.v[u][w] = valid[u] ? b.v[u][w] : 0u;
+                if constexpr (KVT == kFp8) b.vs[u] = valid[u] ? b.vs[u] : 0.0f;
+            }
+        }
+        // raw dot products of the chunk, complete in every lane of a token group
+        float r[U][G];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            float x[G];
             if constexpr (HALF_DOT) {
 #pragma unroll
-                for (int h = 0; h < G; ++h) d[h] = 0.0f;
+                for (int h = 0; h < G; ++h) x[h] = 0.0f;
                 if constexpr (KVT == kF16) {
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const half2_t kk = as_half2(kr[u][i]);
+                    for (int i = 0; i < LW; ++i) {
+                        const half2_t kk = as_half2(b.k[u][i]);
 #pragma unroll
-                        for (int h = 0; h < G; ++h) d[h] = dot2(as_half2(qh[h][i]), kk, d[h]);
+                        for (int h = 0; h < G; ++h) x[h] = dot2(as_half2(qh[h][i]), kk, x[h]);
                     }
                 } else {
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
+                    for (int i = 0; i < LW; ++i) {
                         uint32_t lo, hi;
-                        fp8x4_to_half2x2_scaled(kr[u][i], lo, hi);
+                        fp8x4_to_half2x2_scaled(b.k[u][i], lo, hi);
 #pragma unroll
                         for (int h = 0; h < G; ++h) {
-                            d[h] = dot2(as_half2(qh[h][2 * i]), as_half2(lo), d[h]);
-                            d[h] = dot2(as_half2(qh[h][2 * i + 1]), as_half2(hi), d[h]);
+                            x[h] = dot2(as_half2(qh[h][2 * i]), as_half2(lo), x[h]);
+                            x[h] = dot2(as_half2(qh[h][2 * i + 1]), as_half2(hi), x[h]);
                         }
                     }
                 }
             } else {
                 float kv[EPL];
-                unpack_chunk<KVT>(kr[u], kv);
+                unpack_lane<KVT>(b.k[u], kv);
 #pragma unroll
                 for (int h = 0; h < G; ++h) {
-                    float acc = 0.0f;
+                    float t = 0.0f;
 #pragma unroll
-                    for (int e = 0; e < EPL; ++e) acc = fmaf(qf[h][e], kv[e], acc);
-                    d[h] = acc;
+                    for (int e = 0; e < EPL; ++e) t = fmaf(qf[h][e], kv[e], t);
+                    x[h] = t;
                 }
             }
-            float sc = logit_scale;
-            if constexpr (KVT == kFp8) sc *= ksc[u];
 #pragma unroll
             for (int h = 0; h < G; ++h) {
-                float x = group_sum<LPT>(d[h]) * sc;
-                x = valid[u] ? x : -INFINITY;
-                mx[h] = fmaxf(mx[h], x);
-                if (sub == 0 && valid[u]) lg[h * a.P + tok[u]] = x;
+                float y = group_sum<LPT>(x[h]);
+                if constexpr (KVT == kFp8) y *= b.ks[u];
+                r[u][h] = (TAIL && !valid[u]) ? -INFINITY : y;
             }
         }
-    }
-#pragma unroll
-    for (int h = 0; h < G; ++h) mx[h] = cross_group_max<LPT>(mx[h]);
-    wave_lds_sync();
 
-    // ---------------- phase B: probabilities and their sum
-    float sum[G];
-#pragma unroll
-    for (int h = 0; h < G; ++h) sum[h] = 0.0f;
-    for (int j = lane; j < n; j += kWave) {
+        // running max: rescale only when it grows (the value is wave-uniform)
+        float msc[G];
 #pragma unroll
         for (int h = 0; h < G; ++h) {
-            const float p = __builtin_amdgcn_exp2f(lg[h * a.P + j] - mx[h]);
-            lg[h * a.P + j] = p;
-            sum[h] += p;
+            float cm = r[0][h];
+#pragma unroll
+            for (int u = 1; u < U; ++u) cm = fmaxf(cm, r[u][h]);
+            cm = cross_group_max<LPT>(cm);
+            if (cm > m[h]) {
+                const float alpha = __builtin_amdgcn_exp2f((m[h] - cm) * sc);
+                m[h] = cm;
+                l[h] *= alpha;
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) acc[h][e] *= alpha;
+            }
+            msc[h] = m[h] * sc;
         }
-    }
-#pragma unroll
-    for (int h = 0; h < G; ++h) sum[h] = group_sum<kWave>(sum[h]);
-    wave_lds_sync();
 
-    // ---------------- phase C: o = sum_t p_t * V_t
-    float acc[G][EPL];
+        // weights p = exp2(r * sc - m * sc); masked tokens weigh exactly 0
+        float p[U][G];
 #pragma unroll
-    for (int h = 0; h < G; ++h)
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) acc[h][e] = 0.0f;
-
-    for (int c = 0; c < n; c += CH) {
-        u32x4 vr[U];
-        float vsc[U];
-        bool valid[U];
-        int tok[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            tok[u] = c + u * TPL + grp;
-            valid[u] = tok[u] < n;
-            const int blk = __shfl(my_block, tok[u] >> a.bs_log2, kWave);
-            const int64_t slot = (int64_t(blk) << a.bs_log2) + (tok[u] & bs_mask);
-            vr[u] = valid[u] ? load16(a.vc + slot * slot_stride_bytes + head_off_bytes) : u32x4{0, 0, 0, 0};
-            if constexpr (KVT == kFp8) vsc[u] = valid[u] ? a.vs[slot * a.num_kv_heads + kvh] * kFp8HalfScale : 0.0f;
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            float w[G];
+        for (int u = 0; u < U; ++u)
 #pragma unroll
             for (int h = 0; h < G; ++h) {
-                w[h] = valid[u] ? lg[h * a.P + tok[u]] : 0.0f;
-                if constexpr (KVT == kFp8) w[h] *= vsc[u];
+                const float e2 = __builtin_amdgcn_exp2f(fmaf(r[u][h], sc, -msc[h]));
+                p[u][h] = (TAIL && !valid[u]) ? 0.0f : e2;
             }
-            float v[EPL];
-            unpack_chunk<KVT>(vr[u], v);
+
+        if constexpr (PAIR_PV) {
+            const half2_t ones = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
 #pragma unroll
-            for (int e = 0; e < EPL; ++e)
+            for (int u = 0; u < U; u += 2) {
+                half2_t pp[G];
 #pragma unroll
-                for (int h = 0; h < G; ++h) acc[h][e] = fmaf(w[h], v[e], acc[h][e]);
+                for (int h = 0; h < G; ++h) {
+                    pp[h] = half2_t{static_cast<_Float16>(p[u][h]), static_cast<_Float16>(p[u + 1][h])};
+                    l[h] = dot2(pp[h], ones, l[h]);
+                }
+#pragma unroll
+                for (int i = 0; i < LW; ++i) {
+                    // (dim 2i of token u, of token u+1) and (dim 2i+1 of both)
+                    const uint32_t lo = __builtin_amdgcn_perm(b.v[u + 1][i], b.v[u][i], 0x05040100u);
+                    const uint32_t hi = __builtin_amdgcn_perm(b.v[u + 1][i], b.v[u][i], 0x07060302u);
+#pragma unroll
+                    for (int h = 0; h < G; ++h) {
+                        acc[h][2 * i] = dot2(pp[h], as_half2(lo), acc[h][2 * i]);
+                        acc[h][2 * i + 1] = dot2(pp[h], as_half2(hi), acc[h][2 * i + 1]);
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                float v[EPL];
+                unpack_lane<KVT>(b.v[u], v);
+#pragma unroll
+                for (int h = 0; h < G; ++h) {
+                    l[h] += p[u][h];
+                    float w = p[u][h];
+                    if constexpr (KVT == kFp8) w *= b.vs[u];
+#pragma unroll
+                    for (int e = 0; e < EPL; ++e) acc[h][e] = fmaf(w, v[e], acc[h][e]);
+                }
+            }
         }
+    };
+
+    // Chunks in order; each chunk's loads are issued together and consumed
+    // before the next chunk's.  Loads are never masked: every address is
+    // valid (block ids past the partition are 0), so the steady-state loop
+    // has no branches; only the last chunk masks tokens past n (and zeroes
+    // their V).
+    const int nc = (n + CH - 1) / CH;
+    for (int i = 0; i + 1 < nc; ++i) {
+        ChunkRegs b;
+        load_chunk(b, i * CH, std::false_type{});
+        compute_chunk(b, std::false_type{});
     }
+    {
+        ChunkRegs b;
+        load_chunk(b, (nc - 1) * CH, std::false_type{});
+        if ((n % CH) != 0) compute_chunk(b, std::true_type{}, (nc - 1) * CH);
+        else compute_chunk(b, std::false_type{});
+    }
+
 #pragma unroll
-    for (int h = 0; h < G; ++h)
+    for (int h = 0; h < G; ++h) {
+        l[h] = cross_group_sum<LPT>(l[h]);
 #pragma unroll
         for (int e = 0; e < EPL; ++e) acc[h][e] = cross_group_sum<LPT>(acc[h][e]);
+    }
 
     // ---------------- partial result
     if (grp == 0) {
@@ -306,14 +448,113 @@ __global__ __launch_bounds__(256) void decode_partition_kernel(DecodeArgs a) {
             for (int e = 0; e < EPL; e += 4) {
                 u32x4 w4;
 #pragma unroll
-                for (int k = 0; k < 4 && e + k < EPL; ++k) w4[k] = as_u32(acc[h][e + k]);
+                for (int k = 0; k < 4; ++k) w4[k] = as_u32(acc[h][e + k]);
                 store16(o + e, w4);
             }
             if (sub == 0) {
-                a.part_ml[item * 2] = mx[h];
-                a.part_ml[item * 2 + 1] = sum[h];
+                a.part_ml[item * 2] = m[h] * sc;  // log2-domain max, as the merge expects
+                a.part_ml[item * 2 + 1] = l[h];
             }
         }
+    }
+}
+
+// Persistent partition kernel.  Items (row, partition, kv head) are numbered
+// densely, kv head fastest, so no wave is launched for a partition that does
+// not exist (the context lengths live on the device, so a fixed grid would
+// carry many empty slots for long-tailed batches) and the waves of a
+// workgroup hold adjacent kv heads of the same blocks.  Workgroups claim item
+// groups dynamically, so all stay busy until the list runs out.  Nothing
+// waits on another workgroup.
+template <typename IO, int KVT, int D, int G>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kMinWavesPerSimd)))
+void decode_partition_kernel(DecodeArgs a) {
+    extern __shared__ int prefix[];  // [num_rows + 1] exclusive prefix of partitions per row
+    const int lane = threadIdx.x & (kWave - 1);
+    const int nrows = a.num_rows;
+
+    // Partitions per row and their exclusive prefix, scanned by the whole
+    // workgroup: each thread sums a contiguous tile of rows, the 256 tile sums
+    // are scanned with wave shuffles plus one LDS step, then each thread writes
+    // its tile's prefix entries.
+    __shared__ int wave_total[kWavesPerBlock];
+    auto parts_of = [&](int r) {
+        int ctx = a.row_ctx ? a.row_ctx[r] : a.cl[r];
+        ctx = ctx < a.max_ctx ? ctx : a.max_ctx;
+        return ctx > 0 ? (ctx + a.P - 1) / a.P : 0;
+    };
+    const int per = (nrows + int(blockDim.x) - 1) / int(blockDim.x);
+    const int r0 = int(threadIdx.x) * per;
+    int local = 0;
+    for (int i = 0; i < per; ++i)
+        if (r0 + i < nrows) local += parts_of(r0 + i);
+    int incl = local;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+        const int y = __shfl_up(incl, o, kWave);
+        if (lane >= o) incl += y;
+    }
+    const int wave = threadIdx.x / kWave;
+    if (lane == kWave - 1) wave_total[wave] = incl;
+    __syncthreads();
+    int before = 0;
+    for (int w = 0; w < wave; ++w) before += wave_total[w];
+    int run = before + incl - local;
+    for (int i = 0; i < per; ++i) {
+        if (r0 + i < nrows) {
+            prefix[r0 + i] = run;
+            run += parts_of(r0 + i);
+        }
+    }
+    if (threadIdx.x == blockDim.x - 1) prefix[nrows] = before + incl;
+    __syncthreads();
+    const int num_pairs = prefix[nrows];
+    const int num_items = num_pairs * a.num_kv_heads;
+
+    // Item groups of 4 consecutive items (4 adjacent kv heads of one
+    // partition) go to a workgroup, one item per wave.  Round 0 is static:
+    // workgroup b takes group b.  Later groups g >= gridDim.x are dealt in 8
+    // interleaved sequences g = gridDim.x + 8k + q, each with its own counter
+    // (separate cache lines, so claims on different sequences do not queue on
+    // one address).  A workgroup claims from sequence blockIdx.x % 8 first and
+    // moves on to the next sequence when one is exhausted, so every group is
+    // processed exactly once wherever the workgroups run.
+    __shared__ int next_group;
+    const int num_groups = (num_items + kWavesPerBlock - 1) / kWavesPerBlock;
+    const int g0 = int(gridDim.x);
+    int g = blockIdx.x;
+    int q = blockIdx.x % kClaimSequences;
+    int tried = 0;
+    while (g < num_groups) {
+        const int item = g * kWavesPerBlock + wave;
+        if (item < num_items) {
+            const int pair = item / a.num_kv_heads;
+            const int kvh = item - pair * a.num_kv_heads;
+            int lo = 0, hi = nrows - 1;  // row = last r with prefix[r] <= pair
+            while (lo < hi) {
+                const int mid = (lo + hi + 1) >> 1;
+                if (prefix[mid] <= pair) lo = mid;
+                else hi = mid - 1;
+            }
+            decode_item<IO, KVT, D, G>(a, lo, kvh, pair - prefix[lo], lane);
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            int next = num_groups;
+            while (tried < kClaimSequences) {
+                const int k = atomicAdd(a.counters + q * kCounterStride, 1);
+                const int cand = g0 + kClaimSequences * k + q;
+                if (cand < num_groups) {
+                    next = cand;
+                    break;
+                }
+                q = (q + 1) % kClaimSequences;  // this sequence is exhausted
+                ++tried;
+            }
+            next_group = next;
+        }
+        __syncthreads();
+        g = next_group;
     }
 }
 
@@ -323,6 +564,9 @@ __global__ __launch_bounds__(D) void decode_reduce_kernel(DecodeArgs a) {
     const int s = blockIdx.y;
     const int h = blockIdx.x;
     const int d = threadIdx.x;
+    // The partition kernel has finished (same stream): return its claim
+    // counters to zero for the next call.
+    if (s == 0 && h == 0 && d < kClaimSequences) a.counters[d * kCounterStride] = 0;
     int ctx = a.row_ctx ? a.row_ctx[s] : a.cl[s];
     ctx = ctx < a.max_ctx ? ctx : a.max_ctx;
     const int np = ctx > 0 ? (ctx + a.P - 1) / a.P : 0;
@@ -347,9 +591,21 @@ __global__ __launch_bounds__(D) void decode_reduce_kernel(DecodeArgs a) {
 }
 
 template <typename IO, int KVT, int D, int G>
-void launch_g(const DecodeArgs& args, int grid_x, int Hkv, int S, size_t lds, hipStream_t st) {
-    hipLaunchKernelGGL((decode_partition_kernel<IO, KVT, D, G>), dim3(grid_x, Hkv, S),
+void launch_g(const DecodeArgs& args, int grid_x, int grid_y, int grid_z, size_t lds, hipStream_t st) {
+    hipLaunchKernelGGL((decode_partition_kernel<IO, KVT, D, G>), dim3(grid_x, grid_y, grid_z),
                        dim3(kWave * kWavesPerBlock), lds, st, args);
+}
+
+int device_cu_count() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
 }
 
 template <typename IO, int KVT, int D>
@@ -399,14 +655,12 @@ int ilog2(int x) {
 DecodePlan plan_decode(const vkv_decode_params* p) {
     DecodePlan plan;
     const int bs = p->block_size;
-    int P = p->partition_size > 0 ? p->partition_size : 256;
+    int P = p->partition_size > 0 ? p->partition_size : 512;
     // A partition starts on a block boundary and holds at most 64 blocks
-    // (one block id per lane); logits of 4 waves x G heads x P fit 64 KiB of LDS.
+    // (one block id per lane).
     if (P < bs) P = bs;
     P = (P / bs) * bs;
     if (P > 64 * bs) P = 64 * bs;
-    const int G = p->num_kv_heads > 0 ? p->num_heads / p->num_kv_heads : 1;
-    while (P > bs && int64_t(kWavesPerBlock) * G * P * 4 > 65536) P -= bs;
     int64_t max_ctx = p->max_context_len;
     const int64_t table_tokens = int64_t(p->max_blocks_per_seq) * bs;
     if (max_ctx > table_tokens) max_ctx = table_tokens;
@@ -414,7 +668,8 @@ DecodePlan plan_decode(const vkv_decode_params* p) {
     plan.partition_size = P;
     plan.max_parts = int((max_ctx + P - 1) / P);
     if (plan.max_parts < 1) plan.max_parts = 1;
-    plan.workspace_bytes = size_t(p->num_seqs) * p->num_heads * plan.max_parts * (p->head_dim + 2) * sizeof(float);
+    plan.workspace_bytes = kWorkspaceHeader +
+                           size_t(p->num_seqs) * p->num_heads * plan.max_parts * (p->head_dim + 2) * sizeof(float);
     return plan;
 }
 
@@ -452,8 +707,10 @@ int launch_rows(const vkv_decode_params* p, const DecodePlan& plan, void* worksp
     a.row_seq = row_seq;
     a.row_ctx = row_ctx;
     const size_t o_elems = size_t(p->num_seqs) * p->num_heads * plan.max_parts * p->head_dim;
-    a.part_o = static_cast<float*>(workspace);
+    a.counters = static_cast<int*>(workspace);
+    a.part_o = reinterpret_cast<float*>(static_cast<char*>(workspace) + kWorkspaceHeader);
     a.part_ml = a.part_o + o_elems;
+    a.num_rows = p->num_seqs;
     a.q_stride = p->query_stride ? p->query_stride : int64_t(p->num_heads) * p->head_dim;
     a.num_heads = p->num_heads;
     a.num_kv_heads = p->num_kv_heads;
@@ -469,23 +726,31 @@ int launch_rows(const vkv_decode_params* p, const DecodePlan& plan, void* worksp
     a.accumulate = p->accumulate;
 
     const int G = p->num_heads / p->num_kv_heads;
-    const int grid_x = (plan.max_parts + kWavesPerBlock - 1) / kWavesPerBlock;
-    const size_t lds = size_t(kWavesPerBlock) * G * plan.partition_size * sizeof(float);
+    // Persistent grid: enough workgroups to fill every CU at the kernel's
+    // occupancy, but never more waves than items.
+    const int64_t max_items = int64_t(p->num_seqs) * plan.max_parts * p->num_kv_heads;
+    int64_t wgs = int64_t(device_cu_count()) * kMinWavesPerSimd;
+    const int64_t item_wgs = (max_items + kWavesPerBlock - 1) / kWavesPerBlock;
+    if (wgs > item_wgs) wgs = item_wgs;
+    if (wgs < 1) wgs = 1;
+    const int grid_x = int(wgs);
+    const int grid_y = 1;
+    const size_t lds = (size_t(p->num_seqs) + 1) * sizeof(int);
     const int D = p->head_dim;
     int rc;
     if (p->io_dtype == VKV_DTYPE_F32) {
         switch (p->kv_dtype) {
-            case VKV_DTYPE_F32: rc = dispatch_d<float, kF32>(D, G, a, grid_x, p->num_kv_heads, p->num_seqs, lds, st); break;
-            case VKV_DTYPE_F16: rc = dispatch_d<float, kF16>(D, G, a, grid_x, p->num_kv_heads, p->num_seqs, lds, st); break;
-            case VKV_DTYPE_FP8_E4M3: rc = dispatch_d<float, kFp8>(D, G, a, grid_x, p->num_kv_heads, p->num_seqs, lds, st); break;
+            case VKV_DTYPE_F32: rc = dispatch_d<float, kF32>(D, G, a, grid_x, grid_y, 1, lds, st); break;
+            case VKV_DTYPE_F16: rc = dispatch_d<float, kF16>(D, G, a, grid_x, grid_y, 1, lds, st); break;
+            case VKV_DTYPE_FP8_E4M3: rc = dispatch_d<float, kFp8>(D, G, a, grid_x, grid_y, 1, lds, st); break;
             default: return VKV_ERR_UNSUPPORTED;
         }
         if (rc) return rc;
         return launch_reduce<float>(D, a, p->num_heads, p->num_seqs, st);
     }
     switch (p->kv_dtype) {
-        case VKV_DTYPE_F16: rc = dispatch_d<_Float16, kF16>(D, G, a, grid_x, p->num_kv_heads, p->num_seqs, lds, st); break;
-        case VKV_DTYPE_FP8_E4M3: rc = dispatch_d<_Float16, kFp8>(D, G, a, grid_x, p->num_kv_heads, p->num_seqs, lds, st); break;
+        case VKV_DTYPE_F16: rc = dispatch_d<_Float16, kF16>(D, G, a, grid_x, grid_y, 1, lds, st); break;
+        case VKV_DTYPE_FP8_E4M3: rc = dispatch_d<_Float16, kFp8>(D, G, a, grid_x, grid_y, 1, lds, st); break;
         default: return VKV_ERR_UNSUPPORTED;
     }
     if (rc) return rc;
