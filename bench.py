@@ -32,6 +32,18 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
+def measured_traffic():
+    """HBM bytes per decode call from the committed rocprofv3 PMC summary
+    (profiles/decode_c2_traffic.md: FETCH_SIZE and WRITE_SIZE, calibrated on a
+    1 GiB copy); None if that summary is absent."""
+    path = os.path.join(ROOT, "profiles", "decode_c2_traffic.json")
+    try:
+        with open(path) as f:
+            return int(json.load(f)["traffic_bytes_per_launch"])
+    except (OSError, ValueError, KeyError):
+        return None
+
+
 def cpu_baseline(kc, vc, q, lay, cfg, num_seqs=64, min_seconds=10.0):
     """CPU oracle decode (oracle/kv_oracle.c, a C restatement of the reference
     kernel) on the first num_seqs sequences, repeated until min_seconds have
@@ -76,6 +88,9 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle timing")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only run a plain 1 GiB device-to-device copy 10 times (calibrates the "
+                         "FETCH_SIZE / WRITE_SIZE counters against a kernel of known traffic)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the paged KV path "
@@ -89,6 +104,14 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.copy_probe:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("[bench] copy probe: 10 copies of 1 GiB")
+        return
     cfg = workloads.config2()
     lay = cfg.layout
     S, H, Hkv, D, bs = cfg.num_seqs, cfg.num_heads, cfg.num_kv_heads, cfg.head_dim, cfg.block_size
@@ -167,8 +190,9 @@ def main():
         "append_gbs": round(append_bytes / (ms_append * 1e-3) / 1e9, 2),
         "kv_bytes_per_call": kv_bytes,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "paged decode (partition + merge kernels), event-timed on the launch stream"},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                     "kernel": "paged decode (partition + merge kernels), event-timed on the launch stream",
+                     "achieved_note": "algorithmic KV bytes per call / decode call time"},
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(kc, vc, q, lay, cfg)
