@@ -29,6 +29,7 @@
 //
 // FP8 lanes load 8 bytes (8 codes) so that fp8 and fp16 share one lane layout
 // (D=128: 16 lanes per token) and one register footprint.
+#include <cstdlib>
 #include <type_traits>
 
 #include "common.hpp"
@@ -82,6 +83,7 @@ struct DecodeArgs {
     int32_t accumulate;
     int32_t num_rows;         // sequences (decode) or query rows (prefill)
     int* counters;            // claim counters in the workspace header (zero between calls)
+    int32_t mfma_enabled;     // use the matrix-core QK^T variant where it applies
 };
 
 template <int KVT>
@@ -459,6 +461,215 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, const int s, co
     }
 }
 
+// MFMA variant of one work item, for fp16 query and fp16 keys with D = 128
+// and block_size a multiple of 16.  A chunk is 16 tokens of one block.
+//   QK^T on the matrix cores (v_mfma_f32_16x16x32_f16, 4 per chunk): rows =
+//   the chunk's 16 tokens (A operand = K, lane l loads token l%16, 16 bytes at
+//   dims 32i + 8(l/16)), columns = query heads (B operand = Q, head l%16 of
+//   the group, zero for l%16 >= G).  The accumulator gives lane l the logits
+//   of head l%16 for tokens 4(l/16)..+3.
+//   Softmax on that layout (running max per head, lanes sharing l%16 agree),
+//   probabilities through a 16 x G slice of LDS to the V layout, and p * V as
+//   packed fp16 dot products over token pairs (lane l: token 4u + l/16, dims
+//   8(l%16)..+7), as in the VALU variant.
+// This moves the 128 VALU instructions of the per-token dot products and their
+// cross-lane sums per chunk onto the matrix pipe.
+template <int G>
+__device__ __forceinline__ void decode_item_mfma(const DecodeArgs& a, const int s, const int kvh, const int part,
+                                                 const int lane, float* plds) {
+    constexpr int D = 128;
+    constexpr int CH = 16;
+    typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+    typedef float float4_t __attribute__((ext_vector_type(4)));
+    static_assert(G <= 16, "group size must fit the 16 MFMA columns");
+
+    const int seq = a.row_seq ? a.row_seq[s] : s;
+    int ctx = a.row_ctx ? a.row_ctx[s] : a.cl[s];
+    ctx = ctx < a.max_ctx ? ctx : a.max_ctx;
+    const int t0 = part * a.P;
+    if (t0 >= ctx) return;
+    const int n = (ctx - t0) < a.P ? (ctx - t0) : a.P;
+    const int bs_mask = (1 << a.bs_log2) - 1;
+    const int col = lane & 15;  // MFMA column (query head) / V dim slice
+    const int quad = lane >> 4; // MFMA k-slice / accumulator row group / V token in a load
+
+    const int nb = (n + bs_mask) >> a.bs_log2;
+    int my_block = 0;
+    if (lane < nb) {
+        my_block = a.bt[int64_t(seq) * a.max_blocks_per_seq + (t0 >> a.bs_log2) + lane];
+        if (a.num_blocks > 0 && unsigned(my_block) >= unsigned(a.num_blocks)) my_block = 0;
+    }
+
+    // Q as the B operand; a negative scale is moved into Q (exact sign flip).
+    const int h0 = kvh * G;
+    const bool neg_scale = a.scale_log2 < 0.0f;
+    half8_t qb[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        u32x4 w = {0u, 0u, 0u, 0u};
+        if (col < G) {
+            const char* qp = static_cast<const char*>(a.q) +
+                             (int64_t(s) * a.q_stride + int64_t(h0 + col) * D + 32 * i + 8 * quad) * 2;
+            w = load16(qp);
+            if (neg_scale) w ^= u32x4{0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u};
+        }
+        qb[i] = __builtin_bit_cast(half8_t, w);
+    }
+    const float sc = neg_scale ? -a.scale_log2 : a.scale_log2;
+
+    const uint32_t slot_stride = uint32_t(a.num_kv_heads) * D * 2;
+    const int64_t block_stride = int64_t(slot_stride) << a.bs_log2;
+    const uint32_t koff = uint32_t(col) * slot_stride + uint32_t(kvh * D + 8 * quad) * 2;
+    const uint32_t voff = uint32_t(quad) * slot_stride + uint32_t(kvh * D + 8 * col) * 2;
+
+    float m = -INFINITY;  // running max of this lane's head (col), raw units
+    float l = 0.0f;       // this lane's share of the head's weight sum
+    float acc[G][8];
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[h][e] = 0.0f;
+
+    struct Chunk {
+        u32x4 k[4];
+        u32x4 v[4];
+    };
+    // Issue the K (A-operand layout) and V (row layout) loads of the 16 tokens
+    // at c.  Addresses are always valid (block ids past the partition are 0).
+    auto load_chunk = [&](Chunk& ch, const int c) __attribute__((always_inline)) {
+        const int blk = __builtin_amdgcn_readlane(my_block, (c >> a.bs_log2) & 63);
+        const int64_t boff = int64_t(blk) * block_stride + int64_t(c & bs_mask) * slot_stride;
+        const char* kb = a.kc + boff;
+        const char* vb = a.vc + boff;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ch.k[i] = load16(kb + koff + 64 * i);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) ch.v[u] = load16(vb + voff + u * 4 * slot_stride);
+    };
+
+    auto compute_chunk = [&](Chunk& ch, const int c, auto tail_tag) __attribute__((always_inline)) {
+        constexpr bool TAIL = decltype(tail_tag)::value;
+        u32x4* kr = ch.k;
+        u32x4* vr = ch.v;
+        float4_t cc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, kr[i]), qb[i], cc, 0, 0, 0);
+        float r[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) r[k] = (TAIL && c + 4 * quad + k >= n) ? -INFINITY : cc[k];
+        if constexpr (TAIL) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                if (c + 4 * u + quad >= n) vr[u] = u32x4{0u, 0u, 0u, 0u};
+        }
+
+        // running max per head: lanes sharing col hold the same value after the exchange
+        float cm = fmaxf(fmaxf(r[0], r[1]), fmaxf(r[2], r[3]));
+        cm = fmaxf(cm, __shfl_xor(cm, 16, kWave));
+        cm = fmaxf(cm, __shfl_xor(cm, 32, kWave));
+        const bool grow = cm > m;
+        if (__builtin_amdgcn_ballot_w64(grow && col < G)) {
+            const float alpha = grow ? __builtin_amdgcn_exp2f((m - cm) * sc) : 1.0f;
+            if (grow) m = cm;
+            l *= alpha;
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+                // lane h holds column (head) h
+                const float ah = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), h));
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[h][e] *= ah;
+            }
+        }
+        const float msc = m * sc;
+        float pr[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            pr[k] = __builtin_amdgcn_exp2f(fmaf(r[k], sc, -msc));
+            if (TAIL && c + 4 * quad + k >= n) pr[k] = 0.0f;
+        }
+        // weights to LDS as [token][head]; the sum uses the fp16-rounded values
+        // that the p * V products use
+        if (col < G) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float pk = static_cast<float>(static_cast<_Float16>(pr[k]));
+                l += pk;
+                plds[(4 * quad + k) * G + col] = pk;
+            }
+        }
+        wave_lds_sync();
+#pragma unroll
+        for (int u = 0; u < 4; u += 2) {
+            half2_t pp[G];
+#pragma unroll
+            for (int h = 0; h < G; ++h)
+                pp[h] = half2_t{static_cast<_Float16>(plds[(4 * u + quad) * G + h]),
+                                static_cast<_Float16>(plds[(4 * (u + 1) + quad) * G + h])};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t lo = __builtin_amdgcn_perm(vr[u + 1][i], vr[u][i], 0x05040100u);
+                const uint32_t hi = __builtin_amdgcn_perm(vr[u + 1][i], vr[u][i], 0x07060302u);
+#pragma unroll
+                for (int h = 0; h < G; ++h) {
+                    acc[h][2 * i] = dot2(pp[h], as_half2(lo), acc[h][2 * i]);
+                    acc[h][2 * i + 1] = dot2(pp[h], as_half2(hi), acc[h][2 * i + 1]);
+                }
+            }
+        }
+        wave_lds_sync();
+    };
+
+    // Two chunks (32 tokens, 16 KiB of K/V per wave at D=128) are loaded
+    // before either is computed, doubling the bytes in flight per wave.
+    const int nc = (n + CH - 1) / CH;
+    const bool ragged = (n % CH) != 0;
+    int ci = 0;
+    for (; ci + 2 < nc; ci += 2) {
+        Chunk x, y;
+        load_chunk(x, ci * CH);
+        load_chunk(y, (ci + 1) * CH);
+        compute_chunk(x, ci * CH, std::false_type{});
+        compute_chunk(y, (ci + 1) * CH, std::false_type{});
+    }
+    if (ci + 1 < nc) {
+        Chunk x, y;
+        load_chunk(x, ci * CH);
+        load_chunk(y, (ci + 1) * CH);
+        compute_chunk(x, ci * CH, std::false_type{});
+        if (ragged) compute_chunk(y, (ci + 1) * CH, std::true_type{});
+        else compute_chunk(y, (ci + 1) * CH, std::false_type{});
+    } else {
+        Chunk x;
+        load_chunk(x, ci * CH);
+        if (ragged) compute_chunk(x, ci * CH, std::true_type{});
+        else compute_chunk(x, ci * CH, std::false_type{});
+    }
+
+    // head sums: lanes sharing col; accumulators: lanes sharing col (token groups)
+    l += __shfl_xor(l, 16, kWave);
+    l += __shfl_xor(l, 32, kWave);
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[h][e] = cross_group_sum<16>(acc[h][e]);
+
+    if (quad == 0) {
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            const int64_t item = (int64_t(s) * a.num_heads + h0 + h) * a.max_parts + part;
+            float* o = a.part_o + item * D + col * 8;
+            store16(o, u32x4{as_u32(acc[h][0]), as_u32(acc[h][1]), as_u32(acc[h][2]), as_u32(acc[h][3])});
+            store16(o + 4, u32x4{as_u32(acc[h][4]), as_u32(acc[h][5]), as_u32(acc[h][6]), as_u32(acc[h][7])});
+        }
+        if (col < G) {
+            const int64_t item = (int64_t(s) * a.num_heads + h0 + col) * a.max_parts + part;
+            a.part_ml[item * 2] = m * sc;
+            a.part_ml[item * 2 + 1] = l;
+        }
+    }
+}
+
 // Persistent partition kernel.  Items (row, partition, kv head) are numbered
 // densely, kv head fastest, so no wave is launched for a partition that does
 // not exist (the context lengths live on the device, so a fixed grid would
@@ -466,7 +677,7 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, const int s, co
 // workgroup hold adjacent kv heads of the same blocks.  Workgroups claim item
 // groups dynamically, so all stay busy until the list runs out.  Nothing
 // waits on another workgroup.
-template <typename IO, int KVT, int D, int G>
+template <typename IO, int KVT, int D, int G, bool MFMA>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kMinWavesPerSimd)))
 void decode_partition_kernel(DecodeArgs a) {
     extern __shared__ int prefix[];  // [num_rows + 1] exclusive prefix of partitions per row
@@ -520,6 +731,7 @@ void decode_partition_kernel(DecodeArgs a) {
     // moves on to the next sequence when one is exhausted, so every group is
     // processed exactly once wherever the workgroups run.
     __shared__ int next_group;
+    __shared__ float plds[MFMA ? kWavesPerBlock : 1][MFMA ? 16 * G : 1];
     const int num_groups = (num_items + kWavesPerBlock - 1) / kWavesPerBlock;
     const int g0 = int(gridDim.x);
     int g = blockIdx.x;
@@ -536,7 +748,8 @@ void decode_partition_kernel(DecodeArgs a) {
                 if (prefix[mid] <= pair) lo = mid;
                 else hi = mid - 1;
             }
-            decode_item<IO, KVT, D, G>(a, lo, kvh, pair - prefix[lo], lane);
+            if constexpr (MFMA) decode_item_mfma<G>(a, lo, kvh, pair - prefix[lo], lane, plds[wave]);
+            else decode_item<IO, KVT, D, G>(a, lo, kvh, pair - prefix[lo], lane);
         }
         __syncthreads();
         if (threadIdx.x == 0) {
@@ -590,10 +803,42 @@ __global__ __launch_bounds__(D) void decode_reduce_kernel(DecodeArgs a) {
     *out = static_cast<IO>(r);
 }
 
-template <typename IO, int KVT, int D, int G>
-void launch_g(const DecodeArgs& args, int grid_x, int grid_y, int grid_z, size_t lds, hipStream_t st) {
-    hipLaunchKernelGGL((decode_partition_kernel<IO, KVT, D, G>), dim3(grid_x, grid_y, grid_z),
-                       dim3(kWave * kWavesPerBlock), lds, st, args);
+// Workgroups of `kernel` one CU holds at once with `lds` bytes of dynamic LDS
+// (registers, LDS and wave slots), from the runtime's occupancy calculator;
+// cached per kernel for the last LDS size.
+template <typename K>
+int resident_blocks(K kernel, size_t lds) {
+    static thread_local size_t last_lds = ~size_t(0);
+    static thread_local int last = 0;
+    if (lds != last_lds) {
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, kWave * kWavesPerBlock, lds) != hipSuccess ||
+            n < 1)
+            n = 1;
+        last_lds = lds;
+        last = n;
+    }
+    return last;
+}
+
+// VKV_DECODE_BLOCKS_PER_CU=<n> overrides the persistent grid's workgroups per
+// CU (tuning; default: what the occupancy calculator says fits).
+int blocks_per_cu(int fits) {
+    static const int v = [] {
+        const char* e = std::getenv("VKV_DECODE_BLOCKS_PER_CU");
+        return e ? std::atoi(e) : 0;
+    }();
+    return v > 0 ? v : fits;
+}
+
+// VKV_DECODE_MFMA=0 in the environment selects the VALU variant everywhere
+// (read once per process).
+int mfma_enabled() {
+    static const int v = [] {
+        const char* e = std::getenv("VKV_DECODE_MFMA");
+        return (e && e[0] == '0') ? 0 : 1;
+    }();
+    return v;
 }
 
 int device_cu_count() {
@@ -607,6 +852,23 @@ int device_cu_count() {
     }
     return cached[dev];
 }
+
+template <typename IO, int KVT, int D, int G>
+void launch_g(const DecodeArgs& args, int grid_x, int grid_y, int grid_z, size_t lds, hipStream_t st) {
+    // Matrix-core QK^T for fp16 query and keys at D = 128 with blocks of a
+    // multiple of 16 tokens; the VALU variant covers everything else.
+    constexpr bool kMfmaShape = std::is_same<IO, _Float16>::value && KVT == kF16 && D == 128;
+    // grid_x arrives as the number of item groups (an upper bound); the
+    // persistent grid is what the device holds at once, never more.
+    auto run = [&](auto kernel) {
+        const int64_t wgs = int64_t(device_cu_count()) * blocks_per_cu(resident_blocks(kernel, lds));
+        const int gx = int(wgs < grid_x ? wgs : grid_x);
+        hipLaunchKernelGGL(kernel, dim3(gx > 0 ? gx : 1, grid_y, grid_z), dim3(kWave * kWavesPerBlock), lds, st, args);
+    };
+    if (kMfmaShape && args.bs_log2 >= 4 && args.mfma_enabled) run(decode_partition_kernel<IO, KVT, D, G, kMfmaShape>);
+    else run(decode_partition_kernel<IO, KVT, D, G, false>);
+}
+
 
 template <typename IO, int KVT, int D>
 int dispatch_g(int G, const DecodeArgs& args, int grid_x, int Hkv, int S, size_t lds, hipStream_t st) {
@@ -711,6 +973,7 @@ int launch_rows(const vkv_decode_params* p, const DecodePlan& plan, void* worksp
     a.part_o = reinterpret_cast<float*>(static_cast<char*>(workspace) + kWorkspaceHeader);
     a.part_ml = a.part_o + o_elems;
     a.num_rows = p->num_seqs;
+    a.mfma_enabled = mfma_enabled();
     a.q_stride = p->query_stride ? p->query_stride : int64_t(p->num_heads) * p->head_dim;
     a.num_heads = p->num_heads;
     a.num_kv_heads = p->num_kv_heads;
@@ -726,14 +989,12 @@ int launch_rows(const vkv_decode_params* p, const DecodePlan& plan, void* worksp
     a.accumulate = p->accumulate;
 
     const int G = p->num_heads / p->num_kv_heads;
-    // Persistent grid: enough workgroups to fill every CU at the kernel's
-    // occupancy, but never more waves than items.
+    // Persistent grid (sized in launch_g from the kernel's occupancy), never
+    // more workgroups than item groups.
     const int64_t max_items = int64_t(p->num_seqs) * plan.max_parts * p->num_kv_heads;
-    int64_t wgs = int64_t(device_cu_count()) * kMinWavesPerSimd;
-    const int64_t item_wgs = (max_items + kWavesPerBlock - 1) / kWavesPerBlock;
-    if (wgs > item_wgs) wgs = item_wgs;
-    if (wgs < 1) wgs = 1;
-    const int grid_x = int(wgs);
+    int64_t item_wgs = (max_items + kWavesPerBlock - 1) / kWavesPerBlock;
+    if (item_wgs > (int64_t(1) << 30)) item_wgs = int64_t(1) << 30;
+    const int grid_x = int(item_wgs < 1 ? 1 : item_wgs);
     const int grid_y = 1;
     const size_t lds = (size_t(p->num_seqs) + 1) * sizeof(int);
     const int D = p->head_dim;
