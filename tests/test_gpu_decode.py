@@ -237,6 +237,47 @@ def test_decode_config2_sampled(vkv, oracle, cuda):
     assert torch.equal(out.view(torch.int16), out2.view(torch.int16))
 
 
+@pytest.mark.parametrize("H,Hkv,D", [(8, 8, 64), (32, 8, 128)])
+def test_decode_more_groups_than_grid(vkv, oracle, cuda, H, Hkv, D):
+    """A batch with more work groups (4 kv-head items each) than the launch cap
+    of 16 per CU: the groups past the grid are claimed through the workspace
+    counters.  Sampled sequences against the oracle; a second call must agree
+    bit for bit (the counters return to zero)."""
+    import torch
+    S, bs, P = 2048, 16, 64
+    rng = np.random.default_rng(D + H)
+    ctx = rng.integers(150, 260, size=S).astype(np.int32)
+    lay = _layout(rng, ctx, bs)
+    groups = int(sum((c + P - 1) // P for c in ctx)) * Hkv // 4
+    cus = torch.cuda.get_device_properties(cuda).multi_processor_count
+    assert groups > 16 * cus, (groups, cus)
+    g = torch.Generator(device=cuda).manual_seed(11)
+    shape = (lay.num_blocks, bs, Hkv, D)
+    kc = (torch.randn(shape, generator=g, device=cuda) * 0.5).half()
+    vc = (torch.randn(shape, generator=g, device=cuda) * 0.5).half()
+    q = (torch.randn((S, H, D), generator=g, device=cuda) * 0.5).half()
+    bt = to_dev(lay.block_tables, cuda)
+    cl = to_dev(lay.context_lens, cuda)
+    scale = float(1.0 / np.sqrt(np.float32(D)))
+    out = torch.zeros((S, H, D), dtype=torch.float16, device=cuda)
+    vkv.paged_decode(out, q, kc, vc, bt, cl, scale, partition_size=P)
+    out2 = torch.zeros_like(out)
+    vkv.paged_decode(out2, q, kc, vc, bt, cl, scale, partition_size=P)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), out2.view(torch.int16))
+    got = to_np(out).astype(np.float32)
+    qn = to_np(q).astype(np.float32)
+    for s in [0, 1, 777, 1500, 2046, 2047]:
+        n = int(lay.context_lens[s])
+        nblk = (n + bs - 1) // bs
+        ids = torch.from_numpy(lay.block_tables[s, :nblk]).long().to(cuda)
+        kk = to_np(kc[ids]).view(np.uint16)
+        vv = to_np(vc[ids]).view(np.uint16)
+        ref = oracle.paged_decode(qn[s:s + 1], kk, vv, np.arange(nblk, dtype=np.int32)[None, :],
+                                  np.array([n], np.int32), scale)
+        assert_close(got[s:s + 1], ref, F16_ATOL, F16_RTOL, f"sequence {s}")
+
+
 def test_decode_caller_workspace_and_errors(vkv, cuda):
     import torch
     rng = np.random.default_rng(3)
