@@ -88,6 +88,8 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle timing")
+    ap.add_argument("--partition-size", type=int, default=0,
+                    help="decode split-K partition in tokens (0: the library's default)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy 10 times (calibrates the "
                          "FETCH_SIZE / WRITE_SIZE counters against a kernel of known traffic)")
@@ -126,7 +128,8 @@ def main():
     bt = torch.from_numpy(lay.block_tables).to(dev)
     cl = torch.from_numpy(lay.context_lens).to(dev)
     out = torch.empty((S, H, D), dtype=torch.float16, device=dev)
-    ws = torch.zeros(vkv.decode_workspace_size(out, q, kc, vc, bt, cl, cfg.scale) // 4 + 4,
+    P = args.partition_size
+    ws = torch.zeros(vkv.decode_workspace_size(out, q, kc, vc, bt, cl, cfg.scale, partition_size=P) // 4 + 4,
                      dtype=torch.float32, device=dev)  # first 256 bytes: counters, zero before first use
     stream = torch.cuda.current_stream()
 
@@ -134,7 +137,7 @@ def main():
         vkv.reshape_and_cache(nk, nv, kc, vc, slots, stream=stream)
 
     def decode():
-        vkv.paged_decode(out, q, kc, vc, bt, cl, cfg.scale, workspace=ws, stream=stream)
+        vkv.paged_decode(out, q, kc, vc, bt, cl, cfg.scale, workspace=ws, stream=stream, partition_size=P)
 
     def step():
         append()

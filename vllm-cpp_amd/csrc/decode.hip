@@ -72,8 +72,10 @@ struct DecodeArgs {
     const int32_t* cl;
     const int32_t* row_seq;  // prefill: query row -> sequence (NULL for decode: row == sequence)
     const int32_t* row_ctx;  // prefill: keys visible to the row (causal), replaces the ctx clamp
-    float* part_o;   // [S][H][max_parts][D]
-    float* part_ml;  // [S][H][max_parts][2] (max in log2 domain, sum)
+    // Partials, item-major so that one item's G heads are contiguous:
+    // slot ((s * Hkv + kvh) * max_parts + part) * G + g for head kvh * G + g.
+    float* part_o;   // [S][Hkv][max_parts][G][D]
+    float* part_ml;  // [S][Hkv][max_parts][G][2] (max in log2 domain, sum)
     int64_t q_stride;
     int32_t num_heads;
     int32_t num_kv_heads;
@@ -450,7 +452,7 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, const int s, co
     if (grp == 0) {
 #pragma unroll
         for (int h = 0; h < G; ++h) {
-            const int64_t item = (int64_t(s) * a.num_heads + h0 + h) * a.max_parts + part;
+            const int64_t item = ((int64_t(s) * a.num_kv_heads + kvh) * a.max_parts + part) * G + h;
             float* o = a.part_o + item * D + sub * EPL;
 #pragma unroll
             for (int e = 0; e < EPL; e += 4) {
@@ -665,13 +667,13 @@ __device__ __forceinline__ void decode_item_mfma(const DecodeArgs& a, const int 
     if (quad == 0) {
 #pragma unroll
         for (int h = 0; h < G; ++h) {
-            const int64_t item = (int64_t(s) * a.num_heads + h0 + h) * a.max_parts + part;
+            const int64_t item = ((int64_t(s) * a.num_kv_heads + kvh) * a.max_parts + part) * G + h;
             float* o = a.part_o + item * D + col * 8;
             store16(o, u32x4{as_u32(acc[h][0]), as_u32(acc[h][1]), as_u32(acc[h][2]), as_u32(acc[h][3])});
             store16(o + 4, u32x4{as_u32(acc[h][4]), as_u32(acc[h][5]), as_u32(acc[h][6]), as_u32(acc[h][7])});
         }
         if (col < G) {
-            const int64_t item = (int64_t(s) * a.num_heads + h0 + col) * a.max_parts + part;
+            const int64_t item = ((int64_t(s) * a.num_kv_heads + kvh) * a.max_parts + part) * G + col;
             a.part_ml[item * 2] = m * sc;
             a.part_ml[item * 2 + 1] = l;
         }
@@ -781,6 +783,12 @@ void decode_partition_kernel(DecodeArgs a) {
 }
 
 // Merge the partitions of one (sequence, head): one thread per output element.
+// The kernel is latency-bound (a few KiB per workgroup), so the partials of
+// the first kMergeBatch partitions are loaded together with the context length,
+// before the partition count is known: slots past the count are in the
+// workspace (max_parts per row) and their stale contents are masked out.
+// Longer rows continue in batches with a running max.
+constexpr int kMergeBatch = 8;
 template <typename IO, int D>
 __global__ __launch_bounds__(D) void decode_reduce_kernel(DecodeArgs a) {
     const int s = blockIdx.y;
@@ -789,26 +797,50 @@ __global__ __launch_bounds__(D) void decode_reduce_kernel(DecodeArgs a) {
     // The partition kernel has finished (same stream): return its claim
     // counters to zero for the next call.
     if (s == 0 && h == 0 && d < kClaimSequences) a.counters[d * kCounterStride] = 0;
+    const int64_t row = int64_t(s) * a.num_heads + h;
+    const int G = a.num_heads / a.num_kv_heads;
+    const int kvh = h / G;
+    const int64_t slot0 = (int64_t(s) * a.num_kv_heads + kvh) * a.max_parts * G + (h - kvh * G);
+    const float* ml = a.part_ml + slot0 * 2;
+    const float* o = a.part_o + slot0 * D + d;
+    float bm[kMergeBatch], bl[kMergeBatch], bo[kMergeBatch];
+    auto load_batch = [&](int i0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int k = 0; k < kMergeBatch; ++k) {
+            const int i = i0 + k < a.max_parts ? i0 + k : a.max_parts - 1;  // in-bounds slot
+            bm[k] = ml[int64_t(i) * G * 2];
+            bl[k] = ml[int64_t(i) * G * 2 + 1];
+            bo[k] = o[int64_t(i) * G * D];
+        }
+    };
+    load_batch(0);
     int ctx = a.row_ctx ? a.row_ctx[s] : a.cl[s];
     ctx = ctx < a.max_ctx ? ctx : a.max_ctx;
     const int np = ctx > 0 ? (ctx + a.P - 1) / a.P : 0;
-    const int64_t row = int64_t(s) * a.num_heads + h;
-    float r = 0.0f;
-    if (np > 0) {
-        const float* ml = a.part_ml + row * a.max_parts * 2;
-        const float* o = a.part_o + row * a.max_parts * D + d;
-        float m = -INFINITY;
-        for (int i = 0; i < np; ++i) m = fmaxf(m, ml[2 * i]);
-        float l = 0.0f, acc = 0.0f;
-        for (int i = 0; i < np; ++i) {
-            const float w = __builtin_amdgcn_exp2f(ml[2 * i] - m);
-            l = fmaf(w, ml[2 * i + 1], l);
-            acc = fmaf(w, o[int64_t(i) * D], acc);
+    float m = -INFINITY, l = 0.0f, acc = 0.0f;
+    for (int i0 = 0; i0 < np; i0 += kMergeBatch) {
+        if (i0 > 0) load_batch(i0);
+        float bmax = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < kMergeBatch; ++k)
+            if (i0 + k < np) bmax = fmaxf(bmax, bm[k]);
+        const float mn = fmaxf(m, bmax);
+        const float alpha = __builtin_amdgcn_exp2f(m - mn);  // 0 on the first batch
+        l *= alpha;
+        acc *= alpha;
+#pragma unroll
+        for (int k = 0; k < kMergeBatch; ++k) {
+            if (i0 + k < np) {
+                const float w = __builtin_amdgcn_exp2f(bm[k] - mn);
+                l = fmaf(w, bl[k], l);
+                acc = fmaf(w, bo[k], acc);
+            }
         }
-        r = acc / l;
+        m = mn;
     }
+    const float r0 = np > 0 ? acc / l : 0.0f;
     IO* out = static_cast<IO*>(a.out) + row * D + d;
-    if (a.accumulate) r += static_cast<float>(*out);
+    const float r = a.accumulate ? r0 + static_cast<float>(*out) : r0;
     *out = static_cast<IO>(r);
 }
 
