@@ -203,5 +203,102 @@ def main():
     print(json.dumps(result), flush=True)
 
 
+# --------------------------------------------------------------------------
+# --suite: the other rows of the path, one JSON line each (not the headline).
+
+
+def _events_ms(fn, n, stream):
+    import torch
+    ts = []
+    for _ in range(n):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        fn()
+        e1.record(stream)
+        ts.append((e0, e1))
+    torch.cuda.synchronize()
+    import numpy as np
+    v = np.array([a.elapsed_time(b) for a, b in ts])
+    return float(np.median(v)), float(np.percentile(v, 10)), float(np.percentile(v, 90))
+
+
+def _rand_half(shape, g, dev, sigma):
+    import torch
+    return (torch.randn(shape, generator=g, device=dev) * sigma).half()
+
+
+def suite_c3(dev, steps, warmup):
+    """C3 mixed step: append of the step's 4216 tokens, then one paged_prefill call over
+    8 prefill chunks (512 tokens on prior U[0,2048]) and 120 decodes (ctx U[1024,8192])."""
+    import numpy as np
+    import torch
+    import vllm_kv_amd as vkv
+    from vllm_kv_amd import workloads
+    cfg = workloads.config3()
+    lay = cfg.layout
+    H, Hkv, D, bs = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim, cfg.block_size
+    g = torch.Generator(device=dev).manual_seed(2)
+    kc = _rand_half((lay.num_blocks, bs, Hkv, D), g, dev, 0.3)
+    vc = _rand_half((lay.num_blocks, bs, Hkv, D), g, dev, 0.3)
+    qsl_np = cfg.query_start_loc
+    Tq = int(qsl_np[-1])
+    q = _rand_half((Tq, H, D), g, dev, 0.3)
+    nk = _rand_half((Tq, Hkv, D), g, dev, 0.3)
+    nv = _rand_half((Tq, Hkv, D), g, dev, 0.3)
+    seqs = np.repeat(np.arange(len(cfg.q_lens)), cfg.q_lens)
+    pos = np.concatenate([np.arange(p, p + n) for p, n in zip(cfg.prior_lens, cfg.q_lens)])
+    slots = torch.from_numpy(lay.slots(pos, seqs)).to(dev)
+    bt = torch.from_numpy(lay.block_tables).to(dev)
+    cl = torch.from_numpy(lay.context_lens).to(dev)
+    qsl = torch.from_numpy(qsl_np).to(dev)
+    out = torch.empty_like(q)
+    stream = torch.cuda.current_stream()
+    mql = int(cfg.q_lens.max())
+
+    def append():
+        vkv.reshape_and_cache(nk, nv, kc, vc, slots, stream=stream)
+
+    def attn():
+        vkv.paged_prefill(out, q, kc, vc, bt, cl, qsl, mql, cfg.scale, stream=stream)
+
+    for _ in range(warmup):
+        append()
+        attn()
+    torch.cuda.synchronize()
+    t_app = _events_ms(append, steps, stream)
+    t_att = _events_ms(attn, steps, stream)
+    npf = int((cfg.q_lens > 1).sum())
+    # attended keys per prefill query row: prior + j + 1; FLOPs = 4 D per (query head, key)
+    keys = sum(int(cfg.prior_lens[s]) * int(cfg.q_lens[s]) + int(cfg.q_lens[s]) * (int(cfg.q_lens[s]) + 1) // 2
+               for s in range(npf))
+    flops = 4.0 * D * H * keys
+    dec_bytes = int(lay.context_lens[npf:].astype(np.int64).sum()) * Hkv * D * 2 * 2
+    return {"row": "C3 mixed prefill+decode", "workload": "Qwen2.5-7B shape H28/Hkv4/D128 fp16 bs32; "
+            "8 x 512-token chunks on prior U[0,2048] + 120 decodes ctx U[1024,8192]; seed 2",
+            "query_tokens": Tq, "append_us_median": round(t_app[0] * 1e3, 2),
+            "prefill_call_us_median": round(t_att[0] * 1e3, 2), "prefill_call_us_p10_p90":
+            [round(t_att[1] * 1e3, 2), round(t_att[2] * 1e3, 2)],
+            "prefill_rows_gflop": round(flops / 1e9, 2), "decode_rows_kv_bytes": dec_bytes,
+            "step_us": round((t_app[0] + t_att[0]) * 1e3, 2)}
+
+
+SUITES = {"c3": suite_c3}
+
+
+def run_suite(names, steps, warmup):
+    import torch
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    for name in names:
+        log(f"[suite] {name}")
+        r = SUITES[name](dev, steps, warmup)
+        print(json.dumps(r), flush=True)
+        torch.cuda.empty_cache()
+
+
 if __name__ == "__main__":
+    if len(sys.argv) > 1 and sys.argv[1] == "--suite":
+        run_suite(sys.argv[2].split(",") if len(sys.argv) > 2 else list(SUITES), 20, 3)
+        sys.exit(0)
     main()

@@ -12,15 +12,9 @@ from helpers import F16_ATOL, F16_RTOL, assert_close, to_dev, to_np
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("H,Hkv,D,bs,q_lens,prior", [
-    (32, 8, 128, 16, [5, 1, 17], [0, 30, 40]),
-    (28, 4, 128, 32, [64, 1, 1, 33], [100, 500, 0, 7]),
-    (14, 2, 64, 16, [40], [0]),
-])
-def test_prefill_vs_oracle(vkv, oracle, cuda, H, Hkv, D, bs, q_lens, prior):
-    import torch
+def _case(H, Hkv, D, bs, q_lens, prior, seed):
     from vllm_kv_amd import workloads
-    rng = np.random.default_rng(sum(q_lens) + H)
+    rng = np.random.default_rng(seed)
     q_lens = np.asarray(q_lens, np.int32)
     ctx = np.asarray(prior, np.int32) + q_lens
     lay = workloads.make_layout(ctx, bs, rng, slack=0.2)
@@ -28,11 +22,65 @@ def test_prefill_vs_oracle(vkv, oracle, cuda, H, Hkv, D, bs, q_lens, prior):
     qsl = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
     Tq = int(qsl[-1])
     q = (rng.standard_normal((Tq, H, D), dtype=np.float32) * 0.5).astype(np.float16)
-    scale = float(1.0 / np.sqrt(np.float32(D)))
+    return lay, ctx, qsl, q, k, v, float(1.0 / np.sqrt(np.float32(D)))
+
+
+# fp16 queries at head_dim 64/128 run sequences with >= 2 query tokens on the
+# matrix-core kernel and single-token ones through split-K decode.
+@pytest.mark.parametrize("H,Hkv,D,bs,q_lens,prior", [
+    (32, 8, 128, 16, [5, 1, 17], [0, 30, 40]),
+    (28, 4, 128, 32, [64, 1, 1, 33], [100, 500, 0, 7]),
+    (14, 2, 64, 16, [40], [0]),
+    (16, 2, 128, 16, [40, 3, 1], [10, 0, 77]),      # group 8: eight waves per workgroup
+    (8, 8, 64, 8, [70, 2], [9000, 5]),              # MHA; 1131 blocks: block-id window reloads
+    (16, 4, 128, 64, [33, 1, 100], [64, 0, 129]),   # blocks larger than a key tile
+    (12, 4, 128, 16, [2, 31, 32, 65], [0, 1, 15, 300]),
+])
+def test_prefill_vs_oracle(vkv, oracle, cuda, H, Hkv, D, bs, q_lens, prior):
+    import torch
+    lay, ctx, qsl, q, k, v, scale = _case(H, Hkv, D, bs, q_lens, prior, sum(q_lens) + H)
+    Tq = q.shape[0]
     ref = oracle.paged_prefill(q.astype(np.float32), k.view(np.uint16), v.view(np.uint16), lay.block_tables,
                                ctx, qsl, scale)
     out = torch.zeros((Tq, H, D), dtype=torch.float16, device=cuda)
     vkv.paged_prefill(out, to_dev(q, cuda), to_dev(k, cuda), to_dev(v, cuda), to_dev(lay.block_tables, cuda),
-                      to_dev(ctx, cuda), to_dev(qsl, cuda), int(q_lens.max()), scale)
+                      to_dev(ctx, cuda), to_dev(qsl, cuda), int(max(q_lens)), scale)
     torch.cuda.synchronize()
     assert_close(to_np(out).astype(np.float32), ref, F16_ATOL, F16_RTOL, "prefill")
+
+
+def test_prefill_fp8_vs_oracle(vkv, oracle, cuda):
+    """FP8 cache (quantised by the GPU append): against the oracle on the same codes and scales."""
+    import torch
+    H, Hkv, D, bs = 28, 4, 128, 32
+    lay, ctx, qsl, q, k, v, scale = _case(H, Hkv, D, bs, [48, 1, 130], [20, 300, 64], 9)
+    N = lay.num_blocks
+    kc = torch.zeros((N, bs, Hkv, D), dtype=torch.uint8, device=cuda)
+    vc = torch.zeros_like(kc)
+    ks = torch.zeros((N, bs, Hkv), dtype=torch.float32, device=cuda)
+    vs = torch.zeros_like(ks)
+    slots = to_dev(np.arange(N * bs, dtype=np.int32), cuda)
+    vkv.reshape_and_cache(to_dev(k.reshape(-1, Hkv, D), cuda), to_dev(v.reshape(-1, Hkv, D), cuda), kc, vc, slots,
+                          ks, vs)
+    out = torch.zeros((q.shape[0], H, D), dtype=torch.float16, device=cuda)
+    vkv.paged_prefill(out, to_dev(q, cuda), kc, vc, to_dev(lay.block_tables, cuda), to_dev(ctx, cuda),
+                      to_dev(qsl, cuda), 130, scale, key_scales=ks, value_scales=vs)
+    torch.cuda.synchronize()
+    ref = oracle.paged_prefill(q.astype(np.float32), to_np(kc), to_np(vc), lay.block_tables, ctx, qsl, scale,
+                               key_scales=to_np(ks), value_scales=to_np(vs))
+    assert_close(to_np(out).astype(np.float32), ref, F16_ATOL, F16_RTOL, "fp8 prefill")
+
+
+def test_prefill_f32_rows(vkv, oracle, cuda):
+    """fp32 queries take the per-row decode path (reference precision)."""
+    import torch
+    from helpers import F32_ATOL, F32_RTOL
+    H, Hkv, D, bs = 8, 2, 64, 16
+    lay, ctx, qsl, q, k, v, scale = _case(H, Hkv, D, bs, [9, 1, 20], [3, 40, 0], 21)
+    q32 = q.astype(np.float32)
+    ref = oracle.paged_prefill(q32, k.view(np.uint16), v.view(np.uint16), lay.block_tables, ctx, qsl, scale)
+    out = torch.zeros((q.shape[0], H, D), dtype=torch.float32, device=cuda)
+    vkv.paged_prefill(out, to_dev(q32, cuda), to_dev(k, cuda), to_dev(v, cuda), to_dev(lay.block_tables, cuda),
+                      to_dev(ctx, cuda), to_dev(qsl, cuda), 20, scale)
+    torch.cuda.synchronize()
+    assert_close(to_np(out), ref, F32_ATOL, F32_RTOL, "fp32 prefill")

@@ -264,7 +264,7 @@ int vkv_paged_prefill(const vkv_prefill_params* p, vkv_stream_t stream) {
     void* ws = nullptr;
     rc = library_workspace(plan.workspace_bytes, &ws);
     if (rc != VKV_OK) return rc;
-    return after_launch(vkv::launch_prefill_rows(p, plan, ws, reinterpret_cast<hipStream_t>(stream)),
+    return after_launch(vkv::launch_prefill(p, plan, ws, reinterpret_cast<hipStream_t>(stream)),
                         "vkv_paged_prefill");
 }
 

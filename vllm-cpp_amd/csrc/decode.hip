@@ -72,6 +72,10 @@ struct DecodeArgs {
     const int32_t* cl;
     const int32_t* row_seq;  // prefill: query row -> sequence (NULL for decode: row == sequence)
     const int32_t* row_ctx;  // prefill: keys visible to the row (causal), replaces the ctx clamp
+    // Mixed prefill batch (rows = sequences): query_start_loc.  Only sequences
+    // with one query token are decoded here (query row qsl[s]); the others
+    // belong to the prefill kernel and have no partitions.
+    const int32_t* qsl;
     // Partials, item-major so that one item's G heads are contiguous:
     // slot ((s * Hkv + kvh) * max_parts + part) * G + g for head kvh * G + g.
     float* part_o;   // [S][Hkv][max_parts][G][D]
@@ -91,6 +95,16 @@ struct DecodeArgs {
     int* counters;            // claim counters in the workspace header (zero between calls)
     int32_t mfma_enabled;     // use the matrix-core QK^T variant where it applies
 };
+
+// Keys row r attends (clamped to the table) and the query/output row it uses.
+__device__ __forceinline__ int row_context(const DecodeArgs& a, int r) {
+    int ctx;
+    if (a.row_ctx) ctx = a.row_ctx[r];
+    else if (a.qsl) ctx = (a.qsl[r + 1] - a.qsl[r] == 1) ? a.cl[r] : 0;
+    else ctx = a.cl[r];
+    return ctx < a.max_ctx ? ctx : a.max_ctx;
+}
+__device__ __forceinline__ int64_t query_row(const DecodeArgs& a, int r) { return a.qsl ? a.qsl[r] : r; }
 
 template <int KVT>
 struct LaneLoad {
@@ -163,8 +177,7 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, const int s, co
     static_assert(LPT >= 1 && LPT <= kWave && (kWave % LPT) == 0, "head_dim / dtype mapping");
 
     const int seq = a.row_seq ? a.row_seq[s] : s;
-    int ctx = a.row_ctx ? a.row_ctx[s] : a.cl[s];
-    ctx = ctx < a.max_ctx ? ctx : a.max_ctx;
+    const int ctx = row_context(a, s);
     const int t0 = part * a.P;
     if (t0 >= ctx) return;
     const int n = (ctx - t0) < a.P ? (ctx - t0) : a.P;
@@ -187,7 +200,7 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, const int s, co
     // Query slices of the G heads.
     const int h0 = kvh * G;
     const char* qbase = static_cast<const char*>(a.q) +
-                        (int64_t(s) * a.q_stride + int64_t(h0) * D + sub * EPL) * int64_t(sizeof(IO));
+                        (query_row(a, s) * a.q_stride + int64_t(h0) * D + sub * EPL) * int64_t(sizeof(IO));
     constexpr int QW = HALF_DOT ? EPL / 2 : 1;  // half2 words per head (half path)
     constexpr int QF = HALF_DOT ? 1 : EPL;      // floats per head (float path)
     uint32_t qh[G][QW];
@@ -492,8 +505,7 @@ __device__ __forceinline__ void decode_item_mfma(const DecodeArgs& a, const int 
     static_assert(G <= 16, "group size must fit the 16 MFMA columns");
 
     const int seq = a.row_seq ? a.row_seq[s] : s;
-    int ctx = a.row_ctx ? a.row_ctx[s] : a.cl[s];
-    ctx = ctx < a.max_ctx ? ctx : a.max_ctx;
+    const int ctx = row_context(a, s);
     const int t0 = part * a.P;
     if (t0 >= ctx) return;
     const int n = (ctx - t0) < a.P ? (ctx - t0) : a.P;
@@ -517,7 +529,7 @@ __device__ __forceinline__ void decode_item_mfma(const DecodeArgs& a, const int 
         u32x4 w = {0u, 0u, 0u, 0u};
         if (col < G) {
             const char* qp = static_cast<const char*>(a.q) +
-                             (int64_t(s) * a.q_stride + int64_t(h0 + col) * D + 32 * i + 8 * quad) * 2;
+                             (query_row(a, s) * a.q_stride + int64_t(h0 + col) * D + 32 * i + 8 * quad) * 2;
             w = load16(qp);
             if (neg_scale) w ^= u32x4{0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u};
         }
@@ -700,8 +712,7 @@ void decode_partition_kernel(DecodeArgs a) {
     // its tile's prefix entries.
     __shared__ int wave_total[kWavesPerBlock];
     auto parts_of = [&](int r) {
-        int ctx = a.row_ctx ? a.row_ctx[r] : a.cl[r];
-        ctx = ctx < a.max_ctx ? ctx : a.max_ctx;
+        const int ctx = row_context(a, r);
         return ctx > 0 ? (ctx + a.P - 1) / a.P : 0;
     };
     const int per = (nrows + int(blockDim.x) - 1) / int(blockDim.x);
@@ -797,7 +808,6 @@ __global__ __launch_bounds__(D) void decode_reduce_kernel(DecodeArgs a) {
     // The partition kernel has finished (same stream): return its claim
     // counters to zero for the next call.
     if (s == 0 && h == 0 && d < kClaimSequences) a.counters[d * kCounterStride] = 0;
-    const int64_t row = int64_t(s) * a.num_heads + h;
     const int G = a.num_heads / a.num_kv_heads;
     const int kvh = h / G;
     const int64_t slot0 = (int64_t(s) * a.num_kv_heads + kvh) * a.max_parts * G + (h - kvh * G);
@@ -814,8 +824,8 @@ __global__ __launch_bounds__(D) void decode_reduce_kernel(DecodeArgs a) {
         }
     };
     load_batch(0);
-    int ctx = a.row_ctx ? a.row_ctx[s] : a.cl[s];
-    ctx = ctx < a.max_ctx ? ctx : a.max_ctx;
+    if (a.qsl && a.qsl[s + 1] - a.qsl[s] != 1) return;  // a prefill sequence: not decoded here
+    const int ctx = row_context(a, s);
     const int np = ctx > 0 ? (ctx + a.P - 1) / a.P : 0;
     float m = -INFINITY, l = 0.0f, acc = 0.0f;
     for (int i0 = 0; i0 < np; i0 += kMergeBatch) {
@@ -839,7 +849,7 @@ __global__ __launch_bounds__(D) void decode_reduce_kernel(DecodeArgs a) {
         m = mn;
     }
     const float r0 = np > 0 ? acc / l : 0.0f;
-    IO* out = static_cast<IO*>(a.out) + row * D + d;
+    IO* out = static_cast<IO*>(a.out) + (query_row(a, s) * a.num_heads + h) * D + d;
     const float r = a.accumulate ? r0 + static_cast<float>(*out) : r0;
     *out = static_cast<IO>(r);
 }
@@ -981,7 +991,7 @@ __global__ __launch_bounds__(256) void prefill_rows_kernel(const int32_t* qsl, c
 }
 
 int launch_rows(const vkv_decode_params* p, const DecodePlan& plan, void* workspace, const int32_t* row_seq,
-                const int32_t* row_ctx, hipStream_t st) {
+                const int32_t* row_ctx, const int32_t* qsl, hipStream_t st) {
     DecodeArgs a;
     a.out = p->output;
     a.q = p->query;
@@ -993,6 +1003,7 @@ int launch_rows(const vkv_decode_params* p, const DecodePlan& plan, void* worksp
     a.cl = p->context_lens;
     a.row_seq = row_seq;
     a.row_ctx = row_ctx;
+    a.qsl = qsl;
     const size_t o_elems = size_t(p->num_seqs) * p->num_heads * plan.max_parts * p->head_dim;
     a.counters = static_cast<int*>(workspace);
     a.part_o = reinterpret_cast<float*>(static_cast<char*>(workspace) + kWorkspaceHeader);
@@ -1044,26 +1055,12 @@ int launch_rows(const vkv_decode_params* p, const DecodePlan& plan, void* worksp
 }
 
 int launch_decode(const vkv_decode_params* p, const DecodePlan& plan, void* workspace, hipStream_t st) {
-    return launch_rows(p, plan, workspace, nullptr, nullptr, st);
+    return launch_rows(p, plan, workspace, nullptr, nullptr, nullptr, st);
 }
 
-DecodePlan plan_prefill(const vkv_prefill_params* p) {
-    vkv_decode_params d{};
-    d.num_seqs = p->num_query_tokens;
-    d.num_heads = p->num_heads;
-    d.num_kv_heads = p->num_kv_heads;
-    d.head_dim = p->head_dim;
-    d.block_size = p->block_size;
-    d.max_blocks_per_seq = p->max_blocks_per_seq;
-    d.max_context_len = 0x7FFFFFFF;
-    DecodePlan plan = plan_decode(&d);
-    // row_seq and row_ctx follow the partials
-    plan.workspace_bytes += size_t(p->num_query_tokens) * 2 * sizeof(int32_t);
-    return plan;
-}
-
-int launch_prefill_rows(const vkv_prefill_params* p, const DecodePlan& plan, void* workspace, hipStream_t st) {
-    // Rows are decoded like sequences of a decode call, each with its causal context.
+// Decode parameters for the rows of a prefill call: one row per query token
+// (row_map) or one per sequence (mixed batch, decoding the single-token ones).
+vkv_decode_params prefill_as_decode(const vkv_prefill_params* p, bool per_sequence) {
     vkv_decode_params d{};
     d.output = p->output;
     d.query = p->query;
@@ -1073,8 +1070,8 @@ int launch_prefill_rows(const vkv_prefill_params* p, const DecodePlan& plan, voi
     d.value_scales = p->value_scales;
     d.block_tables = p->block_tables;
     d.context_lens = p->context_lens;
-    d.query_stride = p->query_stride;
-    d.num_seqs = p->num_query_tokens;
+    d.query_stride = p->query_stride ? p->query_stride : int64_t(p->num_heads) * p->head_dim;
+    d.num_seqs = per_sequence ? p->num_seqs : p->num_query_tokens;
     d.num_heads = p->num_heads;
     d.num_kv_heads = p->num_kv_heads;
     d.head_dim = p->head_dim;
@@ -1086,6 +1083,36 @@ int launch_prefill_rows(const vkv_prefill_params* p, const DecodePlan& plan, voi
     d.io_dtype = p->io_dtype;
     d.kv_dtype = p->kv_dtype;
     d.accumulate = 0;
+    return d;
+}
+
+DecodePlan plan_prefill(const vkv_prefill_params* p) {
+    if (prefill_mfma_supported(p)) {
+        // single-token sequences through split-K decode, one row per sequence
+        const vkv_decode_params d = prefill_as_decode(p, true);
+        return plan_decode(&d);
+    }
+    const vkv_decode_params d = prefill_as_decode(p, false);
+    DecodePlan plan = plan_decode(&d);
+    // row_seq and row_ctx follow the partials
+    plan.workspace_bytes += size_t(p->num_query_tokens) * 2 * sizeof(int32_t);
+    return plan;
+}
+
+int launch_prefill(const vkv_prefill_params* p, const DecodePlan& plan, void* workspace, hipStream_t st) {
+    if (prefill_mfma_supported(p)) {
+        // Mixed batch: the decode kernels take the sequences with one query
+        // token, the matrix-core kernel every sequence with two or more.  Each
+        // writes only its own output rows.
+        const vkv_decode_params d = prefill_as_decode(p, true);
+        const int rc = launch_rows(&d, plan, workspace, nullptr, nullptr, p->query_start_loc, st);
+        if (rc) return rc;
+        return launch_prefill_mfma(p, st);
+    }
+    // Every query row decoded like a sequence of a decode call, each with its
+    // causal context (the reference's prefill is one decode per position,
+    // src/core/engine.cpp:157-164).
+    const vkv_decode_params d = prefill_as_decode(p, false);
     const size_t partial_bytes = plan.workspace_bytes - size_t(p->num_query_tokens) * 2 * sizeof(int32_t);
     int32_t* row_seq = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + partial_bytes);
     int32_t* row_ctx = row_seq + p->num_query_tokens;
@@ -1095,7 +1122,7 @@ int launch_prefill_rows(const vkv_prefill_params* p, const DecodePlan& plan, voi
     hipLaunchKernelGGL(prefill_rows_kernel, dim3((p->num_query_tokens + 255) / 256), dim3(256), 0, st,
                        p->query_start_loc, p->context_lens, p->num_seqs, p->num_query_tokens, table_tokens, row_seq,
                        row_ctx);
-    return launch_rows(&d, plan, workspace, row_seq, row_ctx, st);
+    return launch_rows(&d, plan, workspace, row_seq, row_ctx, nullptr, st);
 }
 
 }  // namespace vkv

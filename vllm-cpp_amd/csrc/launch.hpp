@@ -21,10 +21,15 @@ struct DecodePlan {
 DecodePlan plan_decode(const vkv_decode_params* p);
 int launch_decode(const vkv_decode_params* p, const DecodePlan& plan, void* workspace, hipStream_t st);
 
-// Prefill through the decode kernels: one row per query token with its causal
-// context; workspace holds the partials plus the row -> (sequence, context) map.
+// Causal chunked prefill.  fp16 queries with fp16 or FP8 keys at head_dim 64
+// or 128: sequences with >= 2 query tokens on the matrix-core kernel
+// (prefill.hip), single-token sequences through split-K decode.  Otherwise
+// every query row goes through the decode kernels with its causal context
+// (workspace: partials plus the row -> (sequence, context) map).
 DecodePlan plan_prefill(const vkv_prefill_params* p);
-int launch_prefill_rows(const vkv_prefill_params* p, const DecodePlan& plan, void* workspace, hipStream_t st);
+int launch_prefill(const vkv_prefill_params* p, const DecodePlan& plan, void* workspace, hipStream_t st);
+bool prefill_mfma_supported(const vkv_prefill_params* p);
+int launch_prefill_mfma(const vkv_prefill_params* p, hipStream_t st);
 
 struct PlaneSet {
     char* base[4];

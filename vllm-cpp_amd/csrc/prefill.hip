@@ -1,0 +1,411 @@
+// prefill.hip — causal chunked-prefill attention on the matrix cores (gfx950).
+//
+// Semantics follow the reference's prefill, which runs one decode per prompt
+// position (src/core/engine.cpp:157-164 over src/attention/paged_attention.cu:13-82):
+// query row j of a sequence with q_len new tokens and ctx keys (context_lens,
+// this step's tokens included) attends keys 0 .. ctx - q_len + j of the
+// sequence's paged cache, i.e. causal attention over the prior context plus
+// the chunk.  Keys are gathered through the block table like decode.
+//
+// Work decomposition.  A workgroup owns (sequence, kv head, block of kBQ = 32
+// query tokens); wave w computes query head kvh * G + w for those 32 tokens as
+// two 16-row MFMA tiles, so the G heads that share a kv head share every K/V
+// tile staged in LDS.  Keys are processed in tiles of kBK = 32:
+//   S^T = K Q^T   v_mfma_f32_16x16x32_f16, A = K rows (LDS), B = Q (registers);
+//                 lane l holds row (query token) l % 16 for keys 4 (l / 16) + e
+//                 of each 16-key half: softmax state (max, sum) is lane-local
+//                 per row after a two-step exchange across the lane groups.
+//   O^T += V^T P^T  A = V^T (LDS, stored transposed), B = P^T straight from
+//                 the S^T registers (the MFMA k index runs over keys in the
+//                 order the S^T layout holds them), so P never leaves the wave.
+// The output tile is O^T, again one row per lane, normalised at the end.
+//
+// Staging.  Each thread loads its share of the next tile's K rows and V rows
+// (16 bytes = 8 dims of one token per load) into registers while the current
+// tile is being computed, then writes K row-major (rows padded to spread LDS
+// banks) and V transposed ([dim][key], key pairs packed per 32-bit word).
+// FP8 caches are dequantised (code x per-token scale, fp32 -> fp16) on the way
+// into LDS.  Block ids of the sequence are cached in LDS, 1024 at a time.
+#include <type_traits>
+
+#include "common.hpp"
+#include "launch.hpp"
+
+namespace vkv {
+namespace {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kBQ = 32;        // query tokens per workgroup
+constexpr int kRT = kBQ / 16;  // 16-row MFMA tiles per wave
+constexpr int kBK = 32;        // keys per tile
+constexpr int kMaxWaves = 8;   // heads per workgroup (more: grid.z splits the group)
+constexpr int kMinWaves = 4;   // staging always has >= 256 threads
+constexpr int kBtCache = 1024; // block ids cached in LDS at a time
+
+struct PrefillArgs {
+    _Float16* out;
+    const char* q;
+    const char* kc;
+    const char* vc;
+    const float* ks;
+    const float* vs;
+    const int32_t* bt;
+    const int32_t* cl;
+    const int32_t* qsl;
+    int64_t q_stride;  // elements between query rows
+    int32_t num_heads;
+    int32_t num_kv_heads;
+    int32_t group;  // G = H / Hkv
+    int32_t heads_per_wg;
+    int32_t bs_log2;
+    int32_t max_blocks_per_seq;
+    int32_t num_blocks;
+    int32_t table_tokens;
+    int32_t qblocks;  // query blocks per sequence in the grid
+    float scale_log2;
+};
+
+template <int D, int KVT>
+struct Stage {
+    static constexpr int EB = KvTraits<KVT>::bytes;
+    static constexpr int COLS = D / 8;                // 8-dim columns per token row
+    static constexpr int KUNITS = kBK * COLS;         // (key, column) units of a K tile
+    static constexpr int VUNITS = (kBK / 2) * COLS;   // (key pair, column) units of a V tile
+    static constexpr int KPT = KUNITS / (64 * kMinWaves);  // K units per thread (max)
+    static constexpr int VPT = (VUNITS + 64 * kMinWaves - 1) / (64 * kMinWaves);
+    static constexpr int KSTR = D * 2 + 16;           // bytes per K row in LDS
+    static constexpr int VSTR = kBK * 2 + 16;         // bytes per V^T row (one dim)
+    static_assert(KUNITS % (64 * kMinWaves) == 0, "K tile must split evenly over 256 threads");
+    u32x4 k[KPT];
+    u32x4 v0[VPT], v1[VPT];
+};
+
+// Eight fp16 values of one token: fp16 cache bytes as they are, FP8 codes
+// dequantised with the token's scale (code * scale in fp32, rounded to fp16).
+template <int KVT>
+__device__ __forceinline__ u32x4 load8(const char* p, float scale) {
+    if constexpr (KVT == kF16) {
+        return load16_nt(p);
+    } else {
+        const u32x2 w = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+        const float sc = scale * kFp8HalfScale;
+        u32x4 r;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            uint32_t lo, hi;  // (b0, b2), (b1, b3)
+            fp8x4_to_half2x2_scaled(w[i], lo, hi);
+            const half2_t a = as_half2(lo), b = as_half2(hi);
+            const half2_t x0 = {static_cast<_Float16>(static_cast<float>(a[0]) * sc),
+                                static_cast<_Float16>(static_cast<float>(b[0]) * sc)};
+            const half2_t x1 = {static_cast<_Float16>(static_cast<float>(a[1]) * sc),
+                                static_cast<_Float16>(static_cast<float>(b[1]) * sc)};
+            r[2 * i] = __builtin_bit_cast(uint32_t, x0);
+            r[2 * i + 1] = __builtin_bit_cast(uint32_t, x1);
+        }
+        return r;
+    }
+}
+
+template <int D, int KVT>
+__global__ __launch_bounds__(64 * kMaxWaves) void prefill_mfma_kernel(PrefillArgs a) {
+    using St = Stage<D, KVT>;
+    constexpr int EB = St::EB;
+    constexpr int DT = D / 16;  // output dim tiles
+    constexpr int KS = D / 32;  // MFMA k-steps of Q K^T
+    __shared__ __attribute__((aligned(16))) char klds[kBK * St::KSTR];
+    __shared__ __attribute__((aligned(16))) char vlds[D * St::VSTR];
+    __shared__ int btc[kBtCache];
+
+    const int tid = threadIdx.x;
+    const int nthr = blockDim.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int col = lane & 15;   // query row within a 16-row tile
+    const int grp = lane >> 4;   // key group: keys 4 grp .. 4 grp + 3 of a 16-key half
+    const int s = blockIdx.x / a.qblocks;
+    const int qb = blockIdx.x - s * a.qblocks;
+    const int kvh = blockIdx.y;
+    const int g = blockIdx.z * a.heads_per_wg + wave;  // head within the GQA group
+    const bool computes = wave < a.heads_per_wg && g < a.group;
+
+    const int q0 = a.qsl[s];
+    const int qlen = a.qsl[s + 1] - q0;
+    if (qlen < 2 || qb * kBQ >= qlen) return;  // single-token rows belong to the decode kernel
+    const int prior = a.cl[s] - qlen;
+    const int jmax = min(qlen, qb * kBQ + kBQ);  // query rows j in [qb*kBQ, jmax)
+    int kend = prior + jmax;                     // keys any row of the block may see
+    kend = kend < a.table_tokens ? kend : a.table_tokens;
+    const int ntiles = kend > 0 ? (kend + kBK - 1) / kBK : 0;
+    const int h = kvh * a.group + g;
+
+    // ---------------- Q (B operand of S^T = K Q^T) and per-row context
+    const bool neg_scale = a.scale_log2 < 0.0f;
+    const float sc = neg_scale ? -a.scale_log2 : a.scale_log2;
+    half8_t qop[kRT][KS];
+    int rctx[kRT];
+#pragma unroll
+    for (int r = 0; r < kRT; ++r) {
+        const int j = qb * kBQ + 16 * r + col;
+        int c = prior + j + 1;
+        c = c < 0 ? 0 : (c > a.table_tokens ? a.table_tokens : c);
+        rctx[r] = (j < qlen) ? c : 0;
+#pragma unroll
+        for (int i = 0; i < KS; ++i) {
+            u32x4 w = {0u, 0u, 0u, 0u};
+            if (computes && j < qlen) {
+                w = load16(a.q + ((int64_t(q0) + j) * a.q_stride + int64_t(h) * D + 32 * i + 8 * grp) * 2);
+                if (neg_scale) w ^= u32x4{0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u};
+            }
+            qop[r][i] = __builtin_bit_cast(half8_t, w);
+        }
+    }
+
+    // ---------------- staging
+    const int bs_mask = (1 << a.bs_log2) - 1;
+    const int64_t row_bytes = int64_t(a.num_kv_heads) * D * EB;  // one slot (token) of the cache
+    const int32_t* table = a.bt + int64_t(s) * a.max_blocks_per_seq;
+    int win = -1;  // first block id index held in btc
+    auto ensure_window = [&](int first_block) __attribute__((always_inline)) {
+        // uniform across the workgroup; callers are between barriers
+        if (win < 0 || first_block < win || first_block + (kBK >> a.bs_log2) + 1 > win + kBtCache) {
+            __syncthreads();
+            win = first_block;
+            for (int i = tid; i < kBtCache; i += nthr) {
+                const int b = win + i;
+                int id = 0;
+                if (b < a.max_blocks_per_seq) {
+                    id = table[b];
+                    if (a.num_blocks > 0 && unsigned(id) >= unsigned(a.num_blocks)) id = 0;
+                }
+                btc[i] = id;
+            }
+            __syncthreads();
+        }
+    };
+    // address of token k's row in the K or V cache (block id from the LDS cache)
+    auto token_off = [&](int k) __attribute__((always_inline)) {
+        const int blk = btc[(k >> a.bs_log2) - win];
+        return ((int64_t(blk) << a.bs_log2) + (k & bs_mask)) * row_bytes + int64_t(kvh) * D * EB;
+    };
+    auto token_scale = [&](const float* scales, int k) __attribute__((always_inline)) {
+        if constexpr (KVT == kFp8) {
+            const int blk = btc[(k >> a.bs_log2) - win];
+            return scales[((int64_t(blk) << a.bs_log2) + (k & bs_mask)) * a.num_kv_heads + kvh];
+        } else {
+            return 1.0f;
+        }
+    };
+    auto fetch = [&](St& st, int k0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < St::KPT; ++i) {
+            const int u = tid + i * 64 * kMinWaves;
+            const int k = k0 + u / St::COLS;
+            const int c = u % St::COLS;
+            u32x4 w = {0u, 0u, 0u, 0u};
+            if (u < St::KUNITS && k < kend)
+                w = load8<KVT>(a.kc + token_off(k) + c * 8 * EB, token_scale(a.ks, k));
+            st.k[i] = w;
+        }
+#pragma unroll
+        for (int i = 0; i < St::VPT; ++i) {
+            const int u = tid + i * 64 * kMinWaves;
+            const int k = k0 + 2 * (u / St::COLS);
+            const int c = u % St::COLS;
+            u32x4 w0 = {0u, 0u, 0u, 0u}, w1 = {0u, 0u, 0u, 0u};
+            if (u < St::VUNITS) {
+                if (k < kend) w0 = load8<KVT>(a.vc + token_off(k) + c * 8 * EB, token_scale(a.vs, k));
+                if (k + 1 < kend) w1 = load8<KVT>(a.vc + token_off(k + 1) + c * 8 * EB, token_scale(a.vs, k + 1));
+            }
+            st.v0[i] = w0;
+            st.v1[i] = w1;
+        }
+    };
+    // threads beyond 256 only help when the tile has more units than 256 threads cover
+    auto put = [&](const St& st) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < St::KPT; ++i) {
+            const int u = tid + i * 64 * kMinWaves;
+            if (u < St::KUNITS) store16(klds + (u / St::COLS) * St::KSTR + (u % St::COLS) * 16, st.k[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < St::VPT; ++i) {
+            const int u = tid + i * 64 * kMinWaves;
+            if (u < St::VUNITS) {
+                const int kp = u / St::COLS;
+                const int c = u % St::COLS;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    // dims 8c + 2e and 8c + 2e + 1, keys 2kp and 2kp + 1
+                    const uint32_t lo = __builtin_amdgcn_perm(st.v1[i][e], st.v0[i][e], 0x05040100u);
+                    const uint32_t hi = __builtin_amdgcn_perm(st.v1[i][e], st.v0[i][e], 0x07060302u);
+                    *reinterpret_cast<uint32_t*>(vlds + (8 * c + 2 * e) * St::VSTR + kp * 4) = lo;
+                    *reinterpret_cast<uint32_t*>(vlds + (8 * c + 2 * e + 1) * St::VSTR + kp * 4) = hi;
+                }
+            }
+        }
+    };
+
+    // ---------------- main loop
+    float m[kRT], l[kRT];
+    float4_t o[kRT][DT];
+#pragma unroll
+    for (int r = 0; r < kRT; ++r) {
+        m[r] = -INFINITY;
+        l[r] = 0.0f;
+#pragma unroll
+        for (int t = 0; t < DT; ++t) o[r][t] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+
+    St st;
+    if (ntiles > 0) {
+        ensure_window(0);
+        if (tid < 64 * kMinWaves) fetch(st, 0);
+    }
+    for (int kt = 0; kt < ntiles; ++kt) {
+        if (tid < 64 * kMinWaves) put(st);
+        __syncthreads();
+        if (kt + 1 < ntiles) {
+            ensure_window(((kt + 1) * kBK) >> a.bs_log2);
+            if (tid < 64 * kMinWaves) fetch(st, (kt + 1) * kBK);
+        }
+        if (computes) {
+            // K operands of both 16-key halves, shared by the row tiles
+            half8_t kop[2][KS];
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                for (int i = 0; i < KS; ++i)
+                    kop[hh][i] = __builtin_bit_cast(
+                        half8_t, *reinterpret_cast<const u32x4*>(klds + (16 * hh + col) * St::KSTR + (32 * i + 8 * grp) * 2));
+            // V^T operands: dims 16 t + col, keys 4 grp .. +3 and 16 + 4 grp .. +3
+            half8_t vop[DT];
+#pragma unroll
+            for (int t = 0; t < DT; ++t) {
+                const char* vr = vlds + (16 * t + col) * St::VSTR;
+                const u32x2 lo = *reinterpret_cast<const u32x2*>(vr + 8 * grp);
+                const u32x2 hi = *reinterpret_cast<const u32x2*>(vr + 32 + 8 * grp);
+                vop[t] = __builtin_bit_cast(half8_t, u32x4{lo[0], lo[1], hi[0], hi[1]});
+            }
+            const int kbase = kt * kBK;
+#pragma unroll
+            for (int r = 0; r < kRT; ++r) {
+                float4_t sv[2];
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    float4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int i = 0; i < KS; ++i)
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop[hh][i], qop[r][i], acc, 0, 0, 0);
+                    sv[hh] = acc;
+                }
+                // causal / context mask: key index kbase + 16 hh + 4 grp + e < rctx
+                float x[8];
+                float mx = -INFINITY;
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int key = kbase + 16 * hh + 4 * grp + e;
+                        const float v = key < rctx[r] ? sv[hh][e] : -INFINITY;
+                        x[4 * hh + e] = v;
+                        mx = fmaxf(mx, v);
+                    }
+                mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+                mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+                const float mn = fmaxf(m[r], mx);
+                const float mref = mn == -INFINITY ? 0.0f : mn;  // rows with no key yet
+                const float alpha = __builtin_amdgcn_exp2f((m[r] - mref) * sc);
+                m[r] = mn;
+                l[r] *= alpha;
+#pragma unroll
+                for (int t = 0; t < DT; ++t) o[r][t] *= alpha;
+                // P^T operand: k slot (grp, e) = key 4 grp + e, slot (grp, 4 + e) = key 16 + 4 grp + e
+                half8_t pop;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const _Float16 pe = static_cast<_Float16>(__builtin_amdgcn_exp2f((x[e] - mref) * sc));
+                    pop[e] = pe;
+                    l[r] += static_cast<float>(pe);  // the sum uses the fp16 weights the MFMA uses
+                }
+#pragma unroll
+                for (int t = 0; t < DT; ++t) o[r][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop[t], pop, o[r][t], 0, 0, 0);
+            }
+        }
+        __syncthreads();
+    }
+
+    // ---------------- output: lane (row col) holds dims 16 t + 4 grp + e
+    if (!computes) return;
+#pragma unroll
+    for (int r = 0; r < kRT; ++r) {
+        float lt = l[r];
+        lt += __shfl_xor(lt, 16, kWave);
+        lt += __shfl_xor(lt, 32, kWave);
+        const int j = qb * kBQ + 16 * r + col;
+        if (j >= qlen) continue;
+        const float inv = (rctx[r] > 0 && lt > 0.0f) ? 1.0f / lt : 0.0f;
+        _Float16* orow = a.out + ((int64_t(q0) + j) * a.num_heads + h) * D;
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+            const half2_t lo = {static_cast<_Float16>(o[r][t][0] * inv), static_cast<_Float16>(o[r][t][1] * inv)};
+            const half2_t hi = {static_cast<_Float16>(o[r][t][2] * inv), static_cast<_Float16>(o[r][t][3] * inv)};
+            *reinterpret_cast<u32x2*>(orow + 16 * t + 4 * grp) =
+                u32x2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
+        }
+    }
+}
+
+int ilog2i(int x) {
+    int r = 0;
+    while ((1 << r) < x) ++r;
+    return r;
+}
+
+}  // namespace
+
+bool prefill_mfma_supported(const vkv_prefill_params* p) {
+    return p->io_dtype == VKV_DTYPE_F16 && (p->kv_dtype == VKV_DTYPE_F16 || p->kv_dtype == VKV_DTYPE_FP8_E4M3) &&
+           (p->head_dim == 64 || p->head_dim == 128) && p->max_query_len >= 2;
+}
+
+int launch_prefill_mfma(const vkv_prefill_params* p, hipStream_t st) {
+    PrefillArgs a;
+    a.out = static_cast<_Float16*>(p->output);
+    a.q = static_cast<const char*>(p->query);
+    a.kc = static_cast<const char*>(p->key_cache);
+    a.vc = static_cast<const char*>(p->value_cache);
+    a.ks = p->key_scales;
+    a.vs = p->value_scales;
+    a.bt = p->block_tables;
+    a.cl = p->context_lens;
+    a.qsl = p->query_start_loc;
+    a.q_stride = p->query_stride ? p->query_stride : int64_t(p->num_heads) * p->head_dim;
+    a.num_heads = p->num_heads;
+    a.num_kv_heads = p->num_kv_heads;
+    a.group = p->num_heads / p->num_kv_heads;
+    const int head_groups = (a.group + kMaxWaves - 1) / kMaxWaves;
+    a.heads_per_wg = (a.group + head_groups - 1) / head_groups;
+    a.bs_log2 = ilog2i(p->block_size);
+    a.max_blocks_per_seq = p->max_blocks_per_seq;
+    a.num_blocks = p->num_blocks;
+    const int64_t tt = int64_t(p->max_blocks_per_seq) * p->block_size;
+    a.table_tokens = int32_t(tt > 0x7FFFFFFF ? 0x7FFFFFFF : tt);
+    a.qblocks = (p->max_query_len + kBQ - 1) / kBQ;
+    a.scale_log2 = p->scale * 1.4426950408889634f;
+    const int waves = a.heads_per_wg < kMinWaves ? kMinWaves : a.heads_per_wg;
+    const dim3 grid(unsigned(int64_t(p->num_seqs) * a.qblocks), unsigned(p->num_kv_heads), unsigned(head_groups));
+    const dim3 block(unsigned(64 * waves));
+    if (p->head_dim == 128) {
+        if (p->kv_dtype == VKV_DTYPE_F16) hipLaunchKernelGGL((prefill_mfma_kernel<128, kF16>), grid, block, 0, st, a);
+        else hipLaunchKernelGGL((prefill_mfma_kernel<128, kFp8>), grid, block, 0, st, a);
+    } else {
+        if (p->kv_dtype == VKV_DTYPE_F16) hipLaunchKernelGGL((prefill_mfma_kernel<64, kF16>), grid, block, 0, st, a);
+        else hipLaunchKernelGGL((prefill_mfma_kernel<64, kFp8>), grid, block, 0, st, a);
+    }
+    return 0;
+}
+
+}  // namespace vkv
