@@ -283,7 +283,47 @@ def suite_c3(dev, steps, warmup):
             "step_us": round((t_app[0] + t_att[0]) * 1e3, 2)}
 
 
-SUITES = {"c3": suite_c3}
+def suite_c3_prefill_only(dev, steps, warmup):
+    """The 8 prefill sequences of C3 alone (matrix-core kernel only): TFLOP/s."""
+    import numpy as np
+    import torch
+    import vllm_kv_amd as vkv
+    from vllm_kv_amd import workloads
+    cfg = workloads.config3()
+    lay = cfg.layout
+    H, Hkv, D, bs = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim, cfg.block_size
+    npf = int((cfg.q_lens > 1).sum())
+    g = torch.Generator(device=dev).manual_seed(2)
+    kc = _rand_half((lay.num_blocks, bs, Hkv, D), g, dev, 0.3)
+    vc = _rand_half((lay.num_blocks, bs, Hkv, D), g, dev, 0.3)
+    ql = cfg.q_lens[:npf]
+    qsl_np = np.concatenate([[0], np.cumsum(ql)]).astype(np.int32)
+    Tq = int(qsl_np[-1])
+    q = _rand_half((Tq, H, D), g, dev, 0.3)
+    bt = torch.from_numpy(np.ascontiguousarray(lay.block_tables[:npf])).to(dev)
+    cl = torch.from_numpy(np.ascontiguousarray(lay.context_lens[:npf])).to(dev)
+    qsl = torch.from_numpy(qsl_np).to(dev)
+    out = torch.empty_like(q)
+    stream = torch.cuda.current_stream()
+
+    def attn():
+        vkv.paged_prefill(out, q, kc, vc, bt, cl, qsl, int(ql.max()), cfg.scale, stream=stream)
+
+    for _ in range(warmup):
+        attn()
+    torch.cuda.synchronize()
+    t = _events_ms(attn, steps, stream)
+    keys = sum(int(cfg.prior_lens[s]) * int(ql[s]) + int(ql[s]) * (int(ql[s]) + 1) // 2 for s in range(npf))
+    flops = 4.0 * D * H * keys
+    tf = flops / (t[0] * 1e-3) / 1e12
+    return {"row": "C3 prefill sequences alone", "workload": "the 8 x 512-token chunks of C3 (prior U[0,2048])",
+            "us_median": round(t[0] * 1e3, 2), "us_p10_p90": [round(t[1] * 1e3, 2), round(t[2] * 1e3, 2)],
+            "gflop": round(flops / 1e9, 2), "tflops": round(tf, 1),
+            "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": 2500.0, "unit": "TFLOP/s",
+                         "frac": round(tf / 2500.0, 4)}}
+
+
+SUITES = {"c3": suite_c3, "c3p": suite_c3_prefill_only}
 
 
 def run_suite(names, steps, warmup):

@@ -236,28 +236,11 @@ int vkv_paged_prefill(const vkv_prefill_params* p, vkv_stream_t stream) {
     if (p->num_seqs < 0 || p->num_query_tokens < 0) return fail(VKV_ERR_SHAPE, "negative size");
     if (p->num_seqs == 0 || p->num_query_tokens == 0) return VKV_OK;
     if (!p->query_start_loc) return fail(VKV_ERR_NULL, "query_start_loc is NULL");
-    // Shape/dtype rules are those of decode, with one row per query token.
-    vkv_decode_params d{};
-    d.output = p->output;
-    d.query = p->query;
-    d.key_cache = p->key_cache;
-    d.value_cache = p->value_cache;
-    d.key_scales = p->key_scales;
-    d.value_scales = p->value_scales;
-    d.block_tables = p->block_tables;
-    d.context_lens = p->context_lens;
-    d.query_stride = p->query_stride;
-    d.num_seqs = p->num_query_tokens;
-    d.num_heads = p->num_heads;
-    d.num_kv_heads = p->num_kv_heads;
-    d.head_dim = p->head_dim;
-    d.block_size = p->block_size;
-    d.max_context_len = 0x7FFFFFFF;
-    d.max_blocks_per_seq = p->max_blocks_per_seq;
-    d.num_blocks = p->num_blocks;
-    d.scale = p->scale;
-    d.io_dtype = p->io_dtype;
-    d.kv_dtype = p->kv_dtype;
+    if (p->max_query_len < 1) return fail(VKV_ERR_SHAPE, "max_query_len must be >= 1");
+    // Shape/dtype rules are those of decode; the decode rows are the
+    // sequences (mixed matrix-core path) or the query tokens (row path).
+    const bool mfma = vkv::prefill_mfma_supported(p);
+    const vkv_decode_params d = vkv::prefill_as_decode(p, mfma);
     int rc = check_decode(&d);
     if (rc != VKV_OK) return rc;
     const vkv::DecodePlan plan = vkv::plan_prefill(p);

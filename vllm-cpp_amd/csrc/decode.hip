@@ -1090,7 +1090,10 @@ DecodePlan plan_prefill(const vkv_prefill_params* p) {
     if (prefill_mfma_supported(p)) {
         // single-token sequences through split-K decode, one row per sequence
         const vkv_decode_params d = prefill_as_decode(p, true);
-        return plan_decode(&d);
+        DecodePlan plan = plan_decode(&d);
+        // the matrix-core kernel's work list follows the partials
+        plan.workspace_bytes = (plan.workspace_bytes + 255) / 256 * 256 + prefill_items_bytes(p);
+        return plan;
     }
     const vkv_decode_params d = prefill_as_decode(p, false);
     DecodePlan plan = plan_decode(&d);
@@ -1101,13 +1104,14 @@ DecodePlan plan_prefill(const vkv_prefill_params* p) {
 
 int launch_prefill(const vkv_prefill_params* p, const DecodePlan& plan, void* workspace, hipStream_t st) {
     if (prefill_mfma_supported(p)) {
-        // Mixed batch: the decode kernels take the sequences with one query
-        // token, the matrix-core kernel every sequence with two or more.  Each
+        // Mixed batch: the matrix-core kernel takes every sequence with two or
+        // more query tokens, the decode kernels the single-token ones; each
         // writes only its own output rows.
-        const vkv_decode_params d = prefill_as_decode(p, true);
-        const int rc = launch_rows(&d, plan, workspace, nullptr, nullptr, p->query_start_loc, st);
+        const size_t items_off = plan.workspace_bytes - prefill_items_bytes(p);
+        const int rc = launch_prefill_mfma(p, static_cast<char*>(workspace) + items_off, st);
         if (rc) return rc;
-        return launch_prefill_mfma(p, st);
+        const vkv_decode_params d = prefill_as_decode(p, true);
+        return launch_rows(&d, plan, workspace, nullptr, nullptr, p->query_start_loc, st);
     }
     // Every query row decoded like a sequence of a decode call, each with its
     // causal context (the reference's prefill is one decode per position,

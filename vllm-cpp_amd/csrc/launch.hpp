@@ -28,8 +28,10 @@ int launch_decode(const vkv_decode_params* p, const DecodePlan& plan, void* work
 // (workspace: partials plus the row -> (sequence, context) map).
 DecodePlan plan_prefill(const vkv_prefill_params* p);
 int launch_prefill(const vkv_prefill_params* p, const DecodePlan& plan, void* workspace, hipStream_t st);
+vkv_decode_params prefill_as_decode(const vkv_prefill_params* p, bool per_sequence);
 bool prefill_mfma_supported(const vkv_prefill_params* p);
-int launch_prefill_mfma(const vkv_prefill_params* p, hipStream_t st);
+size_t prefill_items_bytes(const vkv_prefill_params* p);
+int launch_prefill_mfma(const vkv_prefill_params* p, void* item_space, hipStream_t st);
 
 struct PlaneSet {
     char* base[4];

@@ -10,20 +10,22 @@
 // Work decomposition.  A workgroup owns (sequence, kv head, block of kBQ = 32
 // query tokens); wave w computes query head kvh * G + w for those 32 tokens as
 // two 16-row MFMA tiles, so the G heads that share a kv head share every K/V
-// tile staged in LDS.  Keys are processed in tiles of kBK = 32:
+// tile staged in LDS.  Keys are staged kBK = 64 at a time and computed in
+// 32-key steps:
 //   S^T = K Q^T   v_mfma_f32_16x16x32_f16, A = K rows (LDS), B = Q (registers);
 //                 lane l holds row (query token) l % 16 for keys 4 (l / 16) + e
 //                 of each 16-key half: softmax state (max, sum) is lane-local
 //                 per row after a two-step exchange across the lane groups.
-//   O^T += V^T P^T  A = V^T (LDS, stored transposed), B = P^T straight from
-//                 the S^T registers (the MFMA k index runs over keys in the
-//                 order the S^T layout holds them), so P never leaves the wave.
+//   O^T += V^T P^T  A = V^T, read from row-major V with ds_read_b64_tr_b16,
+//                 B = P^T straight from the S^T registers (the MFMA k index
+//                 runs over keys in the order the S^T layout holds them), so P
+//                 never leaves the wave.
 // The output tile is O^T, again one row per lane, normalised at the end.
 //
-// Staging.  Each thread loads its share of the next tile's K rows and V rows
-// (16 bytes = 8 dims of one token per load) into registers while the current
-// tile is being computed, then writes K row-major (rows padded to spread LDS
-// banks) and V transposed ([dim][key], key pairs packed per 32-bit word).
+// Staging.  Each of the first 256 threads loads its share of the next tile's K
+// and V rows (16 bytes = 8 dims of one token per load) into registers while
+// the current tile is computed, then writes both row-major into LDS (rows
+// padded by 16 bytes to spread the banks).
 // FP8 caches are dequantised (code x per-token scale, fp32 -> fp16) on the way
 // into LDS.  Block ids of the sequence are cached in LDS, 1024 at a time.
 #include <type_traits>
@@ -40,7 +42,7 @@ typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kBQ = 32;        // query tokens per workgroup
 constexpr int kRT = kBQ / 16;  // 16-row MFMA tiles per wave
-constexpr int kBK = 32;        // keys per tile
+constexpr int kBK = 64;        // keys staged per tile (computed 32 at a time)
 constexpr int kMaxWaves = 8;   // heads per workgroup (more: grid.z splits the group)
 constexpr int kMinWaves = 4;   // staging always has >= 256 threads
 constexpr int kBtCache = 1024; // block ids cached in LDS at a time
@@ -65,6 +67,9 @@ struct PrefillArgs {
     int32_t num_blocks;
     int32_t table_tokens;
     int32_t qblocks;  // query blocks per sequence in the grid
+    int32_t num_seqs;
+    const int2* items;       // work list (s, qb * Hkv + kvh)
+    const int32_t* item_count;
     float scale_log2;
 };
 
@@ -72,15 +77,12 @@ template <int D, int KVT>
 struct Stage {
     static constexpr int EB = KvTraits<KVT>::bytes;
     static constexpr int COLS = D / 8;                // 8-dim columns per token row
-    static constexpr int KUNITS = kBK * COLS;         // (key, column) units of a K tile
-    static constexpr int VUNITS = (kBK / 2) * COLS;   // (key pair, column) units of a V tile
-    static constexpr int KPT = KUNITS / (64 * kMinWaves);  // K units per thread (max)
-    static constexpr int VPT = (VUNITS + 64 * kMinWaves - 1) / (64 * kMinWaves);
-    static constexpr int KSTR = D * 2 + 16;           // bytes per K row in LDS
-    static constexpr int VSTR = kBK * 2 + 16;         // bytes per V^T row (one dim)
-    static_assert(KUNITS % (64 * kMinWaves) == 0, "K tile must split evenly over 256 threads");
-    u32x4 k[KPT];
-    u32x4 v0[VPT], v1[VPT];
+    static constexpr int UNITS = kBK * COLS;          // (key, column) units of a K or V tile
+    static constexpr int UPT = UNITS / (64 * kMinWaves);  // units per staging thread
+    static constexpr int STR = D * 2 + 16;            // bytes per K or V row in LDS
+    static_assert(UNITS % (64 * kMinWaves) == 0, "a tile must split evenly over 256 threads");
+    u32x4 k[UPT];
+    u32x4 v[UPT];
 };
 
 // Eight fp16 values of one token: fp16 cache bytes as they are, FP8 codes
@@ -109,15 +111,21 @@ __device__ __forceinline__ u32x4 load8(const char* p, float scale) {
     }
 }
 
+// ds_read_b64_tr_b16: 8 bytes per lane, transposed across 16-lane groups.
+__device__ __forceinline__ u32x2 tr_read(const char* lds) {
+    typedef __fp16 fp16x4_t __attribute__((__vector_size__(4 * sizeof(__fp16))));
+    typedef __attribute__((address_space(3))) fp16x4_t* lds_ptr;
+    return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_ptr)(lds)));
+}
+
+// One work item: query block qb (kBQ tokens) of sequence s against kv head kvh.
 template <int D, int KVT>
-__global__ __launch_bounds__(64 * kMaxWaves) void prefill_mfma_kernel(PrefillArgs a) {
+__device__ __forceinline__ void prefill_block(const PrefillArgs& a, const int s, const int qb, const int kvh,
+                                              char* klds, char* vlds, int* btc) {
     using St = Stage<D, KVT>;
     constexpr int EB = St::EB;
     constexpr int DT = D / 16;  // output dim tiles
     constexpr int KS = D / 32;  // MFMA k-steps of Q K^T
-    __shared__ __attribute__((aligned(16))) char klds[kBK * St::KSTR];
-    __shared__ __attribute__((aligned(16))) char vlds[D * St::VSTR];
-    __shared__ int btc[kBtCache];
 
     const int tid = threadIdx.x;
     const int nthr = blockDim.x;
@@ -125,15 +133,12 @@ __global__ __launch_bounds__(64 * kMaxWaves) void prefill_mfma_kernel(PrefillArg
     const int wave = tid >> 6;
     const int col = lane & 15;   // query row within a 16-row tile
     const int grp = lane >> 4;   // key group: keys 4 grp .. 4 grp + 3 of a 16-key half
-    const int s = blockIdx.x / a.qblocks;
-    const int qb = blockIdx.x - s * a.qblocks;
-    const int kvh = blockIdx.y;
     const int g = blockIdx.z * a.heads_per_wg + wave;  // head within the GQA group
     const bool computes = wave < a.heads_per_wg && g < a.group;
 
     const int q0 = a.qsl[s];
     const int qlen = a.qsl[s + 1] - q0;
-    if (qlen < 2 || qb * kBQ >= qlen) return;  // single-token rows belong to the decode kernel
+    if (qlen < 2 || qb * kBQ >= qlen) return;  // (the item list holds none of these)
     const int prior = a.cl[s] - qlen;
     const int jmax = min(qlen, qb * kBQ + kBQ);  // query rows j in [qb*kBQ, jmax)
     int kend = prior + jmax;                     // keys any row of the block may see
@@ -154,11 +159,17 @@ __global__ __launch_bounds__(64 * kMaxWaves) void prefill_mfma_kernel(PrefillArg
         rctx[r] = (j < qlen) ? c : 0;
 #pragma unroll
         for (int i = 0; i < KS; ++i) {
-            u32x4 w = {0u, 0u, 0u, 0u};
-            if (computes && j < qlen) {
-                w = load16(a.q + ((int64_t(q0) + j) * a.q_stride + int64_t(h) * D + 32 * i + 8 * grp) * 2);
-                if (neg_scale) w ^= u32x4{0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u};
-            }
+            // Unconditional load (row 0 / head 0 stand in for absent rows, then
+            // zeroed): a load under a branch makes the compiler wait for every
+            // outstanding load before the first use of Q inside the key loop,
+            // which would serialise the staging prefetch with the MFMAs.
+            const bool ok = computes && j < qlen;
+            const int64_t qrow = ok ? int64_t(q0) + j : int64_t(q0);
+            const int64_t qcol = ok ? int64_t(h) * D : 0;
+            u32x4 w = load16(a.q + (qrow * a.q_stride + qcol + 32 * i + 8 * grp) * 2);
+            const uint32_t keep = ok ? 0xFFFFFFFFu : 0u;
+            const uint32_t flip = neg_scale ? 0x80008000u : 0u;
+            w = (w ^ u32x4{flip, flip, flip, flip}) & u32x4{keep, keep, keep, keep};
             qop[r][i] = __builtin_bit_cast(half8_t, w);
         }
     }
@@ -200,51 +211,27 @@ __global__ __launch_bounds__(64 * kMaxWaves) void prefill_mfma_kernel(PrefillArg
     };
     auto fetch = [&](St& st, int k0) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < St::KPT; ++i) {
+        for (int i = 0; i < St::UPT; ++i) {
             const int u = tid + i * 64 * kMinWaves;
             const int k = k0 + u / St::COLS;
             const int c = u % St::COLS;
-            u32x4 w = {0u, 0u, 0u, 0u};
-            if (u < St::KUNITS && k < kend)
-                w = load8<KVT>(a.kc + token_off(k) + c * 8 * EB, token_scale(a.ks, k));
-            st.k[i] = w;
-        }
-#pragma unroll
-        for (int i = 0; i < St::VPT; ++i) {
-            const int u = tid + i * 64 * kMinWaves;
-            const int k = k0 + 2 * (u / St::COLS);
-            const int c = u % St::COLS;
-            u32x4 w0 = {0u, 0u, 0u, 0u}, w1 = {0u, 0u, 0u, 0u};
-            if (u < St::VUNITS) {
-                if (k < kend) w0 = load8<KVT>(a.vc + token_off(k) + c * 8 * EB, token_scale(a.vs, k));
-                if (k + 1 < kend) w1 = load8<KVT>(a.vc + token_off(k + 1) + c * 8 * EB, token_scale(a.vs, k + 1));
+            u32x4 wk = {0u, 0u, 0u, 0u}, wv = {0u, 0u, 0u, 0u};
+            if (k < kend) {
+                const int64_t off = token_off(k) + c * 8 * EB;
+                wk = load8<KVT>(a.kc + off, token_scale(a.ks, k));
+                wv = load8<KVT>(a.vc + off, token_scale(a.vs, k));
             }
-            st.v0[i] = w0;
-            st.v1[i] = w1;
+            st.k[i] = wk;
+            st.v[i] = wv;
         }
     };
-    // threads beyond 256 only help when the tile has more units than 256 threads cover
     auto put = [&](const St& st) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < St::KPT; ++i) {
+        for (int i = 0; i < St::UPT; ++i) {
             const int u = tid + i * 64 * kMinWaves;
-            if (u < St::KUNITS) store16(klds + (u / St::COLS) * St::KSTR + (u % St::COLS) * 16, st.k[i]);
-        }
-#pragma unroll
-        for (int i = 0; i < St::VPT; ++i) {
-            const int u = tid + i * 64 * kMinWaves;
-            if (u < St::VUNITS) {
-                const int kp = u / St::COLS;
-                const int c = u % St::COLS;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    // dims 8c + 2e and 8c + 2e + 1, keys 2kp and 2kp + 1
-                    const uint32_t lo = __builtin_amdgcn_perm(st.v1[i][e], st.v0[i][e], 0x05040100u);
-                    const uint32_t hi = __builtin_amdgcn_perm(st.v1[i][e], st.v0[i][e], 0x07060302u);
-                    *reinterpret_cast<uint32_t*>(vlds + (8 * c + 2 * e) * St::VSTR + kp * 4) = lo;
-                    *reinterpret_cast<uint32_t*>(vlds + (8 * c + 2 * e + 1) * St::VSTR + kp * 4) = hi;
-                }
-            }
+            const int off = (u / St::COLS) * St::STR + (u % St::COLS) * 16;
+            store16(klds + off, st.k[i]);
+            store16(vlds + off, st.v[i]);
         }
     };
 
@@ -259,18 +246,15 @@ __global__ __launch_bounds__(64 * kMaxWaves) void prefill_mfma_kernel(PrefillArg
         for (int t = 0; t < DT; ++t) o[r][t] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
     }
 
+    // One staging set: tile kt's registers go to LDS, then are refilled with
+    // tile kt + 1 while tile kt is computed in two 32-key steps.
     St st;
+    const bool stager = tid < 64 * kMinWaves;
     if (ntiles > 0) {
         ensure_window(0);
-        if (tid < 64 * kMinWaves) fetch(st, 0);
+        if (stager) fetch(st, 0);
     }
-    for (int kt = 0; kt < ntiles; ++kt) {
-        if (tid < 64 * kMinWaves) put(st);
-        __syncthreads();
-        if (kt + 1 < ntiles) {
-            ensure_window(((kt + 1) * kBK) >> a.bs_log2);
-            if (tid < 64 * kMinWaves) fetch(st, (kt + 1) * kBK);
-        }
+    auto step = [&](const int kt, const int sub) __attribute__((always_inline)) {
         if (computes) {
             // K operands of both 16-key halves, shared by the row tiles
             half8_t kop[2][KS];
@@ -279,17 +263,22 @@ __global__ __launch_bounds__(64 * kMaxWaves) void prefill_mfma_kernel(PrefillArg
 #pragma unroll
                 for (int i = 0; i < KS; ++i)
                     kop[hh][i] = __builtin_bit_cast(
-                        half8_t, *reinterpret_cast<const u32x4*>(klds + (16 * hh + col) * St::KSTR + (32 * i + 8 * grp) * 2));
-            // V^T operands: dims 16 t + col, keys 4 grp .. +3 and 16 + 4 grp .. +3
+                        half8_t, *reinterpret_cast<const u32x4*>(klds + (32 * sub + 16 * hh + col) * St::STR + (32 * i + 8 * grp) * 2));
+            // V^T operands (dims 16 t + col; keys 4 grp + e, then 16 + 4 grp + e)
+            // by transpose reads of row-major V: within each 16-lane group,
+            // lane i receives element i % 4 of the 8-byte chunks addressed by
+            // lanes i / 4 + 4 e, e = 0..3.  Lane m of group grp therefore
+            // addresses key 4 grp + m / 4 (+16), dims 16 t + 4 (m % 4) .. +3.
             half8_t vop[DT];
+            const int vrow = 32 * sub + 4 * grp + (col >> 2);
 #pragma unroll
             for (int t = 0; t < DT; ++t) {
-                const char* vr = vlds + (16 * t + col) * St::VSTR;
-                const u32x2 lo = *reinterpret_cast<const u32x2*>(vr + 8 * grp);
-                const u32x2 hi = *reinterpret_cast<const u32x2*>(vr + 32 + 8 * grp);
+                const int dcol = (16 * t + 4 * (col & 3)) * 2;
+                const u32x2 lo = tr_read(vlds + vrow * St::STR + dcol);
+                const u32x2 hi = tr_read(vlds + (16 + vrow) * St::STR + dcol);
                 vop[t] = __builtin_bit_cast(half8_t, u32x4{lo[0], lo[1], hi[0], hi[1]});
             }
-            const int kbase = kt * kBK;
+            const int kbase = kt * kBK + 32 * sub;
 #pragma unroll
             for (int r = 0; r < kRT; ++r) {
                 float4_t sv[2];
@@ -334,11 +323,21 @@ __global__ __launch_bounds__(64 * kMaxWaves) void prefill_mfma_kernel(PrefillArg
                 for (int t = 0; t < DT; ++t) o[r][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop[t], pop, o[r][t], 0, 0, 0);
             }
         }
+    };
+    for (int kt = 0; kt < ntiles; ++kt) {
+        if (stager) put(st);
+        __syncthreads();
+        if (kt + 1 < ntiles) {
+            ensure_window(((kt + 1) * kBK) >> a.bs_log2);
+            if (stager) fetch(st, (kt + 1) * kBK);
+        }
+        step(kt, 0);
+        if (kt * kBK + 32 < kend) step(kt, 1);
         __syncthreads();
     }
 
     // ---------------- output: lane (row col) holds dims 16 t + 4 grp + e
-    if (!computes) return;
+    if (!computes) return;  // (after the loop's last barrier)
 #pragma unroll
     for (int r = 0; r < kRT; ++r) {
         float lt = l[r];
@@ -358,6 +357,76 @@ __global__ __launch_bounds__(64 * kMaxWaves) void prefill_mfma_kernel(PrefillArg
     }
 }
 
+// Persistent workgroups walk the item list (built by prefill_items_kernel);
+// every item ends with a barrier, so LDS is free for the next one.
+template <int D, int KVT>
+__global__ __launch_bounds__(64 * kMaxWaves) void prefill_mfma_kernel(PrefillArgs a) {
+    using St = Stage<D, KVT>;
+    __shared__ __attribute__((aligned(16))) char klds[kBK * St::STR];
+    __shared__ __attribute__((aligned(16))) char vlds[kBK * St::STR];
+    __shared__ int btc[kBtCache];
+    const int count = *a.item_count;
+    for (int it = blockIdx.x; it < count; it += gridDim.x) {
+        const int2 item = a.items[it];
+        prefill_block<D, KVT>(a, item.x, item.y / a.num_kv_heads, item.y % a.num_kv_heads, klds, vlds, btc);
+        __syncthreads();
+    }
+}
+
+// Work list of the matrix-core kernel, in one workgroup: items (s, qb * Hkv +
+// kvh) of every sequence with >= 2 query tokens, ordered by distance from the
+// sequence's last query block (last blocks, which see the most keys, first),
+// so that short blocks fill in at the end.  Level L holds block qb = nqb - 1 - L
+// of every sequence with nqb > L blocks.
+__global__ __launch_bounds__(256) void prefill_items_kernel(const int32_t* qsl, int32_t num_seqs, int32_t hkv,
+                                                            int32_t max_qblocks, int2* items, int32_t* count) {
+    __shared__ int wave_sum[4];
+    __shared__ int level_total;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int per = (num_seqs + 255) / 256;
+    const int s0 = tid * per;
+    auto nqb = [&](int s) {
+        const int q = qsl[s + 1] - qsl[s];
+        const int n = q >= 2 ? (q + kBQ - 1) / kBQ : 0;
+        return n < max_qblocks ? n : max_qblocks;  // max_query_len bounds q_len (caller contract)
+    };
+    int total = 0;
+    for (int L = 0;; ++L) {
+        int local = 0;
+        for (int i = 0; i < per; ++i)
+            if (s0 + i < num_seqs && nqb(s0 + i) > L) local += hkv;
+        int incl = local;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += y;
+        }
+        if (lane == 63) wave_sum[wave] = incl;
+        __syncthreads();
+        int before = 0;
+        for (int w = 0; w < wave; ++w) before += wave_sum[w];
+        if (tid == 255) level_total = before + incl;
+        int pos = total + before + incl - local;
+        for (int i = 0; i < per; ++i) {
+            const int s = s0 + i;
+            if (s >= num_seqs) break;
+            const int n = nqb(s);
+            if (n > L) {
+                for (int k = 0; k < hkv; ++k) items[pos + k] = int2{s, (n - 1 - L) * hkv + k};
+                pos += hkv;
+            }
+        }
+        __syncthreads();
+        const int lt = level_total;
+        __syncthreads();
+        if (lt == 0) break;
+        total += lt;
+    }
+    if (tid == 0) *count = total;
+}
+
 int ilog2i(int x) {
     int r = 0;
     while ((1 << r) < x) ++r;
@@ -371,7 +440,12 @@ bool prefill_mfma_supported(const vkv_prefill_params* p) {
            (p->head_dim == 64 || p->head_dim == 128) && p->max_query_len >= 2;
 }
 
-int launch_prefill_mfma(const vkv_prefill_params* p, hipStream_t st) {
+size_t prefill_items_bytes(const vkv_prefill_params* p) {
+    const int64_t qblocks = (p->max_query_len + kBQ - 1) / kBQ;
+    return 256 + size_t(int64_t(p->num_seqs) * qblocks * p->num_kv_heads) * sizeof(int2);
+}
+
+int launch_prefill_mfma(const vkv_prefill_params* p, void* item_space, hipStream_t st) {
     PrefillArgs a;
     a.out = static_cast<_Float16*>(p->output);
     a.q = static_cast<const char*>(p->query);
@@ -394,9 +468,22 @@ int launch_prefill_mfma(const vkv_prefill_params* p, hipStream_t st) {
     const int64_t tt = int64_t(p->max_blocks_per_seq) * p->block_size;
     a.table_tokens = int32_t(tt > 0x7FFFFFFF ? 0x7FFFFFFF : tt);
     a.qblocks = (p->max_query_len + kBQ - 1) / kBQ;
+    a.num_seqs = p->num_seqs;
     a.scale_log2 = p->scale * 1.4426950408889634f;
+    int32_t* count = static_cast<int32_t*>(item_space);
+    int2* items = reinterpret_cast<int2*>(static_cast<char*>(item_space) + 256);
+    a.items = items;
+    a.item_count = count;
+    hipLaunchKernelGGL(prefill_items_kernel, dim3(1), dim3(256), 0, st, p->query_start_loc, p->num_seqs,
+                       p->num_kv_heads, a.qblocks, items, count);
+    // Persistent grid: two workgroups per CU (one runs, one waits), never more
+    // than there can be items.
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    const int64_t upper = int64_t(p->num_seqs) * a.qblocks * p->num_kv_heads;
+    const int64_t wgs = int64_t(cus) * 2 < upper ? int64_t(cus) * 2 : upper;
     const int waves = a.heads_per_wg < kMinWaves ? kMinWaves : a.heads_per_wg;
-    const dim3 grid(unsigned(int64_t(p->num_seqs) * a.qblocks), unsigned(p->num_kv_heads), unsigned(head_groups));
+    const dim3 grid(unsigned(wgs > 0 ? wgs : 1), 1u, unsigned(head_groups));
     const dim3 block(unsigned(64 * waves));
     if (p->head_dim == 128) {
         if (p->kv_dtype == VKV_DTYPE_F16) hipLaunchKernelGGL((prefill_mfma_kernel<128, kF16>), grid, block, 0, st, a);
