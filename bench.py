@@ -323,7 +323,215 @@ def suite_c3_prefill_only(dev, steps, warmup):
                          "frac": round(tf / 2500.0, 4)}}
 
 
-SUITES = {"c3": suite_c3, "c3p": suite_c3_prefill_only}
+def suite_c1(dev, steps, warmup):
+    """C1 (Qwen2.5-0.5B layer, 4 sequences): append + decode; launch-bound at this size."""
+    import numpy as np
+    import torch
+    import vllm_kv_amd as vkv
+    from vllm_kv_amd import workloads
+    cfg = workloads.config1()
+    lay = cfg.layout
+    S, H, Hkv, D, bs = cfg.num_seqs, cfg.num_heads, cfg.num_kv_heads, cfg.head_dim, cfg.block_size
+    g = torch.Generator(device=dev).manual_seed(0)
+    kc = _rand_half((lay.num_blocks, bs, Hkv, D), g, dev, cfg.sigma)
+    vc = _rand_half((lay.num_blocks, bs, Hkv, D), g, dev, cfg.sigma)
+    q = _rand_half((S, H, D), g, dev, cfg.sigma)
+    nk = _rand_half((S, Hkv, D), g, dev, cfg.sigma)
+    nv = _rand_half((S, Hkv, D), g, dev, cfg.sigma)
+    slots = torch.from_numpy(lay.slots(cfg.prev_lens, np.arange(S))).to(dev)
+    bt = torch.from_numpy(lay.block_tables).to(dev)
+    cl = torch.from_numpy(lay.context_lens).to(dev)
+    out = torch.empty_like(q)
+    stream = torch.cuda.current_stream()
+
+    def step():
+        vkv.reshape_and_cache(nk, nv, kc, vc, slots, stream=stream)
+        vkv.paged_decode(out, q, kc, vc, bt, cl, cfg.scale, stream=stream)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t = _events_ms(step, steps, stream)
+    kvb = cfg.kv_bytes(2)
+    return {"row": "C1 append + decode", "workload": "Qwen2.5-0.5B shape H14/Hkv2/D64 fp16 bs16, B=4, ctx U[1,512]",
+            "kv_bytes": kvb, "step_us_median": round(t[0] * 1e3, 2),
+            "step_us_p10_p90": [round(t[1] * 1e3, 2), round(t[2] * 1e3, 2)],
+            "note": "launch-bound: two kernels for 0.5 MB of KV"}
+
+
+def suite_c5(dev, steps, warmup):
+    """C5: FP8 (e4m3fn + per-token scales) append of 256 tokens and decode over
+    lognormal contexts (B=256, E[ctx] ~ 3.3k)."""
+    import numpy as np
+    import torch
+    import vllm_kv_amd as vkv
+    from vllm_kv_amd import workloads
+    cfg = workloads.config5()
+    lay = cfg.layout
+    S, H, Hkv, D, bs = cfg.num_seqs, cfg.num_heads, cfg.num_kv_heads, cfg.head_dim, cfg.block_size
+    g = torch.Generator(device=dev).manual_seed(4)
+    N = lay.num_blocks
+    kc = torch.empty((N, bs, Hkv, D), dtype=torch.uint8, device=dev)
+    vc = torch.empty_like(kc)
+    ks = torch.empty((N, bs, Hkv), dtype=torch.float32, device=dev)
+    vs = torch.empty_like(ks)
+    all_slots = torch.arange(N * bs, dtype=torch.int32, device=dev)
+    chunk = 1 << 20
+    for s0 in range(0, N * bs, chunk):  # fill the pool through the FP8 append: N(0,1), 1 % outliers x8
+        n = min(chunk, N * bs - s0)
+        x = torch.randn((2, n, Hkv, D), generator=g, device=dev)
+        x = torch.where(torch.rand(x.shape, generator=g, device=dev) < 0.01, x * 8, x).half()
+        vkv.reshape_and_cache(x[0], x[1], kc, vc, all_slots[s0:s0 + n], ks, vs)
+        del x
+    q = _rand_half((S, H, D), g, dev, 1.0)
+    nk = _rand_half((S, Hkv, D), g, dev, 1.0)
+    nv = _rand_half((S, Hkv, D), g, dev, 1.0)
+    slots = torch.from_numpy(lay.slots(cfg.prev_lens, np.arange(S))).to(dev)
+    bt = torch.from_numpy(lay.block_tables).to(dev)
+    cl = torch.from_numpy(lay.context_lens).to(dev)
+    out = torch.empty_like(q)
+    stream = torch.cuda.current_stream()
+
+    def append():
+        vkv.reshape_and_cache(nk, nv, kc, vc, slots, ks, vs, stream=stream)
+
+    def decode():
+        vkv.paged_decode(out, q, kc, vc, bt, cl, cfg.scale, key_scales=ks, value_scales=vs, stream=stream)
+
+    for _ in range(warmup):
+        append()
+        decode()
+    torch.cuda.synchronize()
+    ta = _events_ms(append, steps, stream)
+    td = _events_ms(decode, steps, stream)
+    kvb = cfg.kv_bytes(1, 4)
+    gbs = kvb / (td[0] * 1e-3) / 1e9
+    return {"row": "C5 FP8 append + decode", "workload": "H32/Hkv8/D128, bs16, B=256, ctx = clip(lognormal(7.6,1),128,32768)",
+            "context_tokens": int(lay.context_lens.astype(np.int64).sum()), "kv_bytes": kvb,
+            "decode_us_median": round(td[0] * 1e3, 2), "decode_us_p10_p90": [round(td[1] * 1e3, 2), round(td[2] * 1e3, 2)],
+            "append_us_median": round(ta[0] * 1e3, 2),
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4)}}
+
+
+def suite_append(dev, steps, warmup):
+    """reshape_and_cache T-sweep at the C2 shape (Hkv8, D128, bs16): fp16 -> fp16 and
+    fp16 -> FP8 (+ scales), slots a random permutation of a 1.25x pool."""
+    import numpy as np
+    import torch
+    import vllm_kv_amd as vkv
+    Hkv, D, bs = 8, 128, 16
+    rows = []
+    stream = torch.cuda.current_stream()
+    g = torch.Generator(device=dev).manual_seed(5)
+    for T in (4216, 65536, 262144):
+        N = (int(T * 1.25) + bs - 1) // bs
+        perm = torch.randperm(N * bs, generator=torch.Generator().manual_seed(T))[:T].int().to(dev)
+        k = _rand_half((T, Hkv, D), g, dev, 0.3)
+        v = _rand_half((T, Hkv, D), g, dev, 0.3)
+        for kind in ("f16", "fp8"):
+            if kind == "f16":
+                kc = torch.zeros((N, bs, Hkv, D), dtype=torch.float16, device=dev)
+                vc = torch.zeros_like(kc)
+                ks = vs = None
+                wbytes = T * Hkv * D * 2 * 2
+            else:
+                kc = torch.zeros((N, bs, Hkv, D), dtype=torch.uint8, device=dev)
+                vc = torch.zeros_like(kc)
+                ks = torch.zeros((N, bs, Hkv), dtype=torch.float32, device=dev)
+                vs = torch.zeros_like(ks)
+                wbytes = T * Hkv * (D + 4) * 2
+
+            def fn():
+                vkv.reshape_and_cache(k, v, kc, vc, perm, ks, vs, stream=stream)
+
+            for _ in range(warmup):
+                fn()
+            torch.cuda.synchronize()
+            t = _events_ms(fn, steps, stream)
+            nbytes = T * Hkv * D * 2 * 2 + wbytes + T * 4
+            gbs = nbytes / (t[0] * 1e-3) / 1e9
+            rows.append({"tokens": T, "cache": kind, "us_median": round(t[0] * 1e3, 2), "bytes": nbytes,
+                         "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)})
+            del kc, vc, ks, vs
+        del k, v
+        torch.cuda.empty_cache()
+    return {"row": "append (reshape_and_cache) T-sweep", "workload": "Hkv8/D128 fp16 source, bs16, random slots",
+            "sweep": rows, "roofline_bound": "hbm", "peak": HBM_PEAK_GBS}
+
+
+def suite_stream(dev, steps, warmup):
+    """Device-to-device copy of 1 GiB (read + write): the practical HBM ceiling."""
+    import torch
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        dst.copy_(src)
+    t = _events_ms(lambda: dst.copy_(src), steps, stream)
+    gbs = 2 * (1 << 30) / (t[0] * 1e-3) / 1e9
+    return {"row": "copy ceiling", "workload": "torch copy_ of 1 GiB on the device", "us_median": round(t[0] * 1e3, 1),
+            "gbs_read_plus_write": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def suite_c4(dev, steps, warmup):
+    """C4: copy_blocks of 4096 (src, dst) pairs over 32 layers x (K, V) of
+    [N=8192, bs64, Hkv8, D128] fp16 (random bits), then swap of 2048 blocks to
+    pinned host memory and back; bit-exact checks at full size."""
+    import numpy as np
+    import torch
+    import vllm_kv_amd as vkv
+    from vllm_kv_amd import workloads
+    cfg = workloads.config4()
+    L, N = cfg.num_layers, cfg.num_blocks
+    shape = (L, N, cfg.block_size, cfg.num_kv_heads, cfg.head_dim)
+    g = torch.Generator(device=dev).manual_seed(3)
+    planes = [torch.empty(shape, dtype=torch.int16, device=dev) for _ in range(2)]
+    for pl in planes:
+        for l in range(L):
+            pl[l].random_(-32768, 32767, generator=g)
+    pairs = torch.from_numpy(cfg.copy_pairs).to(dev)
+    stream = torch.cuda.current_stream()
+
+    def copy():
+        vkv.copy_blocks(planes, pairs, stream=stream)
+
+    for _ in range(max(1, warmup // 2)):
+        copy()
+    t = _events_ms(copy, max(3, steps // 4), stream)
+    src = pairs[:, 0].long()
+    dst = pairs[:, 1].long()
+    exact = all(torch.equal(pl[l][dst], pl[l][src]) for pl in planes for l in range(L))
+    copy_bytes = 2 * int(pairs.shape[0]) * L * 2 * cfg.block_bytes
+    copy_gbs = copy_bytes / (t[0] * 1e-3) / 1e9
+    # swap: blocks -> pinned host -> other device blocks
+    nsw = int(cfg.swap_blocks.shape[0])
+    hb = vkv.host_block_bytes(planes)
+    host = torch.empty(nsw * hb, dtype=torch.uint8, pin_memory=True)
+    out_pairs = torch.from_numpy(np.stack([cfg.swap_blocks, np.arange(nsw, dtype=np.int32)], 1)).to(dev)
+    free = np.setdiff1d(np.arange(N, dtype=np.int32), cfg.swap_blocks)[:nsw]
+    in_pairs = torch.from_numpy(np.stack([np.arange(nsw, dtype=np.int32), free], 1)).to(dev)
+    reps = 3
+    torch.cuda.synchronize()
+    t_out = _events_ms(lambda: vkv.swap_blocks(planes, host, nsw, out_pairs, 0, stream=stream), reps, stream)
+    t_in = _events_ms(lambda: vkv.swap_blocks(planes, host, nsw, in_pairs, 1, stream=stream), reps, stream)
+    a = torch.from_numpy(cfg.swap_blocks).long().to(dev)
+    b = torch.from_numpy(free).long().to(dev)
+    swap_exact = all(torch.equal(pl[l][b], pl[l][a]) for pl in planes for l in range(L))
+    swap_bytes = nsw * hb
+    return {"row": "C4 copy_blocks + swap_blocks", "workload": "32 layers x K,V x [8192, 64, 8, 128] fp16, 4096 copy pairs, 2048 swaps",
+            "copy_us_median": round(t[0] * 1e3, 1), "copy_bytes_read_plus_write": copy_bytes,
+            "copy_roofline": {"bound": "hbm", "achieved": round(copy_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                              "frac": round(copy_gbs / HBM_PEAK_GBS, 4)},
+            "copy_bit_exact": bool(exact),
+            "swap_bytes_per_direction": swap_bytes,
+            "swap_out_gbs": round(swap_bytes / (t_out[0] * 1e-3) / 1e9, 1),
+            "swap_in_gbs": round(swap_bytes / (t_in[0] * 1e-3) / 1e9, 1),
+            "swap_round_trip_bit_exact": bool(swap_exact)}
+
+
+SUITES = {"stream": suite_stream, "c1": suite_c1, "append": suite_append, "c3": suite_c3,
+          "c3p": suite_c3_prefill_only, "c5": suite_c5, "c4": suite_c4}
 
 
 def run_suite(names, steps, warmup):
