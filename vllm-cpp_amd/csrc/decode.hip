@@ -482,26 +482,33 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, const int s, co
     }
 }
 
-// MFMA variant of one work item, for fp16 query and fp16 keys with D = 128
-// and block_size a multiple of 16.  A chunk is 16 tokens of one block.
+// MFMA variant of one work item, for fp16 queries over fp16 or FP8 caches with
+// D = 128 and block_size a multiple of 16.  A chunk is 16 tokens of one block.
 //   QK^T on the matrix cores (v_mfma_f32_16x16x32_f16, 4 per chunk): rows =
-//   the chunk's 16 tokens (A operand = K, lane l loads token l%16, 16 bytes at
-//   dims 32i + 8(l/16)), columns = query heads (B operand = Q, head l%16 of
-//   the group, zero for l%16 >= G).  The accumulator gives lane l the logits
-//   of head l%16 for tokens 4(l/16)..+3.
+//   the chunk's 16 tokens (A operand = K, lane l holds token l%16 and 8 dims
+//   chosen by l/16 and the MFMA index), columns = query heads (B operand = Q,
+//   head l%16 of the group, zero for l%16 >= G, its dims in the same order).
+//   The accumulator gives lane l the logits of head l%16 for tokens
+//   4(l/16)..+3.  fp16 K: lane l loads dims 32i + 8(l/16) for MFMA i.  FP8 K:
+//   lane l loads 16 codes, dims 32(l/16) + 16j (two loads), feeding MFMAs 2j
+//   and 2j+1; codes are widened exactly to fp16 (times 2^-8) and the token's
+//   scale multiplies the logit.
 //   Softmax on that layout (running max per head, lanes sharing l%16 agree),
 //   probabilities through a 16 x G slice of LDS to the V layout, and p * V as
 //   packed fp16 dot products over token pairs (lane l: token 4u + l/16, dims
-//   8(l%16)..+7), as in the VALU variant.
+//   8(l%16)..+7), as in the VALU variant; FP8 V scales are folded into p.
 // This moves the 128 VALU instructions of the per-token dot products and their
 // cross-lane sums per chunk onto the matrix pipe.
-template <int G>
+template <int G, int KVT>
 __device__ __forceinline__ void decode_item_mfma(const DecodeArgs& a, const int s, const int kvh, const int part,
                                                  const int lane, float* plds) {
     constexpr int D = 128;
     constexpr int CH = 16;
+    constexpr bool FP8 = KVT == kFp8;
+    constexpr int EB = FP8 ? 1 : 2;
     typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
     typedef float float4_t __attribute__((ext_vector_type(4)));
+    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
     static_assert(G <= 16, "group size must fit the 16 MFMA columns");
 
     const int seq = a.row_seq ? a.row_seq[s] : s;
@@ -521,26 +528,35 @@ __device__ __forceinline__ void decode_item_mfma(const DecodeArgs& a, const int 
     }
 
     // Q as the B operand; a negative scale is moved into Q (exact sign flip).
+    // Loads are unconditional (head h0 stands in for the unused columns, which
+    // are then zeroed) so that they overlap instead of each being awaited.
     const int h0 = kvh * G;
     const bool neg_scale = a.scale_log2 < 0.0f;
+    const uint32_t qkeep = col < G ? 0xFFFFFFFFu : 0u;
+    const uint32_t qflip = neg_scale ? 0x80008000u : 0u;
+    const char* qrow = static_cast<const char*>(a.q) +
+                       (query_row(a, s) * a.q_stride + int64_t(h0 + (col < G ? col : 0)) * D) * 2;
     half8_t qb[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        u32x4 w = {0u, 0u, 0u, 0u};
-        if (col < G) {
-            const char* qp = static_cast<const char*>(a.q) +
-                             (query_row(a, s) * a.q_stride + int64_t(h0 + col) * D + 32 * i + 8 * quad) * 2;
-            w = load16(qp);
-            if (neg_scale) w ^= u32x4{0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u};
+        // dims of MFMA i: fp16 32i + 8 quad; FP8 32 quad + 16 (i / 2) + 8 (i % 2)
+        const int d0 = FP8 ? 32 * quad + 16 * (i >> 1) + 8 * (i & 1) : 32 * i + 8 * quad;
+        u32x4 w = load16(qrow + d0 * 2);
+        w = (w ^ u32x4{qflip, qflip, qflip, qflip}) & u32x4{qkeep, qkeep, qkeep, qkeep};
+        if constexpr (FP8) {
+            // widened FP8 codes come as (b0, b2), (b1, b3) per 4 bytes: same order for Q
+            w = u32x4{__builtin_amdgcn_perm(w[1], w[0], 0x05040100u), __builtin_amdgcn_perm(w[1], w[0], 0x07060302u),
+                      __builtin_amdgcn_perm(w[3], w[2], 0x05040100u), __builtin_amdgcn_perm(w[3], w[2], 0x07060302u)};
         }
         qb[i] = __builtin_bit_cast(half8_t, w);
     }
     const float sc = neg_scale ? -a.scale_log2 : a.scale_log2;
 
-    const uint32_t slot_stride = uint32_t(a.num_kv_heads) * D * 2;
+    const uint32_t slot_stride = uint32_t(a.num_kv_heads) * D * EB;
     const int64_t block_stride = int64_t(slot_stride) << a.bs_log2;
-    const uint32_t koff = uint32_t(col) * slot_stride + uint32_t(kvh * D + 8 * quad) * 2;
-    const uint32_t voff = uint32_t(quad) * slot_stride + uint32_t(kvh * D + 8 * col) * 2;
+    const uint32_t koff = FP8 ? uint32_t(col) * slot_stride + uint32_t(kvh * D + 32 * quad)
+                              : uint32_t(col) * slot_stride + uint32_t(kvh * D + 8 * quad) * 2;
+    const uint32_t voff = uint32_t(quad) * slot_stride + uint32_t(kvh * D + 8 * col) * EB;
 
     float m = -INFINITY;  // running max of this lane's head (col), raw units
     float l = 0.0f;       // this lane's share of the head's weight sum
@@ -551,8 +567,11 @@ __device__ __forceinline__ void decode_item_mfma(const DecodeArgs& a, const int 
         for (int e = 0; e < 8; ++e) acc[h][e] = 0.0f;
 
     struct Chunk {
-        u32x4 k[4];
-        u32x4 v[4];
+        u32x4 k[FP8 ? 2 : 4];
+        u32x4 v[FP8 ? 1 : 4];
+        u32x2 v8[FP8 ? 4 : 1];
+        float ks[FP8 ? 4 : 1];  // scales of tokens 4 quad + k (x 256)
+        float vs[FP8 ? 4 : 1];  // scales of tokens 4 u + quad (x 256)
     };
     // Issue the K (A-operand layout) and V (row layout) loads of the 16 tokens
     // at c.  Addresses are always valid (block ids past the partition are 0).
@@ -561,29 +580,64 @@ __device__ __forceinline__ void decode_item_mfma(const DecodeArgs& a, const int 
         const int64_t boff = int64_t(blk) * block_stride + int64_t(c & bs_mask) * slot_stride;
         const char* kb = a.kc + boff;
         const char* vb = a.vc + boff;
-#pragma unroll
         // K lines are read in two halves by different instructions: ordinary
         // loads keep the line for the second half; V rows stream (non-temporal).
-        for (int i = 0; i < 4; ++i) ch.k[i] = load16(kb + koff + 64 * i);
+        if constexpr (FP8) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) ch.v[u] = load16_nt(vb + voff + u * 4 * slot_stride);
+            for (int j = 0; j < 2; ++j) ch.k[j] = load16(kb + koff + 16 * j);
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                ch.v8[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(vb + voff + u * 4 * slot_stride));
+            const int64_t sbase = ((int64_t(blk) << a.bs_log2) + (c & bs_mask)) * a.num_kv_heads + kvh;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                ch.ks[k] = a.ks[sbase + int64_t(4 * quad + k) * a.num_kv_heads];
+                ch.vs[k] = a.vs[sbase + int64_t(4 * k + quad) * a.num_kv_heads];
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) ch.k[i] = load16(kb + koff + 64 * i);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) ch.v[u] = load16_nt(vb + voff + u * 4 * slot_stride);
+        }
     };
 
     auto compute_chunk = [&](Chunk& ch, const int c, auto tail_tag) __attribute__((always_inline)) {
         constexpr bool TAIL = decltype(tail_tag)::value;
-        u32x4* kr = ch.k;
-        u32x4* vr = ch.v;
+        u32x4* vr = ch.v;  // (fp16 only)
         float4_t cc = {0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (FP8) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, kr[i]), qb[i], cc, 0, 0, 0);
+            for (int i = 0; i < 4; ++i) {
+                uint32_t w[4];
+                fp8x4_to_half2x2_scaled(ch.k[i >> 1][2 * (i & 1)], w[0], w[1]);
+                fp8x4_to_half2x2_scaled(ch.k[i >> 1][2 * (i & 1) + 1], w[2], w[3]);
+                cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    __builtin_bit_cast(half8_t, u32x4{w[0], w[1], w[2], w[3]}), qb[i], cc, 0, 0, 0);
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k) cc[k] *= ch.ks[k] * kFp8HalfScale;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, ch.k[i]), qb[i], cc, 0, 0, 0);
+        }
         float r[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) r[k] = (TAIL && c + 4 * quad + k >= n) ? -INFINITY : cc[k];
         if constexpr (TAIL) {
+            // past n: V zero and (FP8) scale zero, whatever the slots hold
 #pragma unroll
-            for (int u = 0; u < 4; ++u)
-                if (c + 4 * u + quad >= n) vr[u] = u32x4{0u, 0u, 0u, 0u};
+            for (int u = 0; u < 4; ++u) {
+                if (c + 4 * u + quad >= n) {
+                    if constexpr (FP8) {
+                        ch.v8[u] = u32x2{0u, 0u};  // code 0 widens to +0
+                        ch.vs[u] = 0.0f;
+                    } else {
+                        vr[u] = u32x4{0u, 0u, 0u, 0u};
+                    }
+                }
+            }
         }
 
         // running max per head: lanes sharing col hold the same value after the exchange
@@ -624,14 +678,33 @@ __device__ __forceinline__ void decode_item_mfma(const DecodeArgs& a, const int 
 #pragma unroll
         for (int u = 0; u < 4; u += 2) {
             half2_t pp[G];
+            const float v0 = FP8 ? ch.vs[u] * kFp8HalfScale : 1.0f;
+            const float v1 = FP8 ? ch.vs[u + 1] * kFp8HalfScale : 1.0f;
 #pragma unroll
             for (int h = 0; h < G; ++h)
-                pp[h] = half2_t{static_cast<_Float16>(plds[(4 * u + quad) * G + h]),
-                                static_cast<_Float16>(plds[(4 * (u + 1) + quad) * G + h])};
+                pp[h] = half2_t{static_cast<_Float16>(plds[(4 * u + quad) * G + h] * v0),
+                                static_cast<_Float16>(plds[(4 * (u + 1) + quad) * G + h] * v1)};
+            u32x4 va, vb;
+            if constexpr (!FP8) {
+                va = vr[u];
+                vb = vr[u + 1];
+            } else {
+                // widen the two tokens' codes to fp16 in dim order: (b0, b1), (b2, b3)
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    uint32_t lo, hi;
+                    fp8x4_to_half2x2_scaled(ch.v8[u][h], lo, hi);
+                    va[2 * h] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+                    va[2 * h + 1] = __builtin_amdgcn_perm(hi, lo, 0x07060302u);
+                    fp8x4_to_half2x2_scaled(ch.v8[u + 1][h], lo, hi);
+                    vb[2 * h] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+                    vb[2 * h + 1] = __builtin_amdgcn_perm(hi, lo, 0x07060302u);
+                }
+            }
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const uint32_t lo = __builtin_amdgcn_perm(vr[u + 1][i], vr[u][i], 0x05040100u);
-                const uint32_t hi = __builtin_amdgcn_perm(vr[u + 1][i], vr[u][i], 0x07060302u);
+                const uint32_t lo = __builtin_amdgcn_perm(vb[i], va[i], 0x05040100u);
+                const uint32_t hi = __builtin_amdgcn_perm(vb[i], va[i], 0x07060302u);
 #pragma unroll
                 for (int h = 0; h < G; ++h) {
                     acc[h][2 * i] = dot2(pp[h], as_half2(lo), acc[h][2 * i]);
@@ -642,11 +715,24 @@ __device__ __forceinline__ void decode_item_mfma(const DecodeArgs& a, const int 
         wave_lds_sync();
     };
 
-    // Two chunks (32 tokens, 16 KiB of K/V per wave at D=128) are loaded
-    // before either is computed, doubling the bytes in flight per wave.
+    // Two chunks (32 tokens, 16 KiB of K/V per wave at D=128 fp16) are loaded
+    // before either is computed, doubling the bytes in flight per wave.  Groups
+    // above 6 heads (3 for FP8, whose chunks carry scales) load one chunk at a
+    // time so that the 8 G accumulators per lane fit without spilling.
     const int nc = (n + CH - 1) / CH;
     const bool ragged = (n % CH) != 0;
     int ci = 0;
+    if constexpr (G > (FP8 ? 3 : 6)) {
+        for (; ci + 1 < nc; ++ci) {
+            Chunk x;
+            load_chunk(x, ci * CH);
+            compute_chunk(x, ci * CH, std::false_type{});
+        }
+        Chunk x;
+        load_chunk(x, ci * CH);
+        if (ragged) compute_chunk(x, ci * CH, std::true_type{});
+        else compute_chunk(x, ci * CH, std::false_type{});
+    } else {
     for (; ci + 2 < nc; ci += 2) {
         Chunk x, y;
         load_chunk(x, ci * CH);
@@ -666,6 +752,7 @@ __device__ __forceinline__ void decode_item_mfma(const DecodeArgs& a, const int 
         load_chunk(x, ci * CH);
         if (ragged) compute_chunk(x, ci * CH, std::true_type{});
         else compute_chunk(x, ci * CH, std::false_type{});
+    }
     }
 
     // head sums: lanes sharing col; accumulators: lanes sharing col (token groups)
@@ -769,7 +856,7 @@ void decode_partition_kernel(DecodeArgs a) {
                 if (prefix[mid] <= pair) lo = mid;
                 else hi = mid - 1;
             }
-            if constexpr (MFMA) decode_item_mfma<G>(a, lo, kvh, pair - prefix[lo], lane, plds[wave]);
+            if constexpr (MFMA) decode_item_mfma<G, KVT>(a, lo, kvh, pair - prefix[lo], lane, plds[wave]);
             else decode_item<IO, KVT, D, G>(a, lo, kvh, pair - prefix[lo], lane);
         }
         if (g0 >= num_groups) break;  // the grid covers every group: nothing to claim
@@ -890,7 +977,7 @@ template <typename IO, int KVT, int D, int G>
 void launch_g(const DecodeArgs& args, int grid_x, int grid_y, int grid_z, size_t lds, hipStream_t st) {
     // Matrix-core QK^T for fp16 query and keys at D = 128 with blocks of a
     // multiple of 16 tokens; the VALU variant covers everything else.
-    constexpr bool kMfmaShape = std::is_same<IO, _Float16>::value && KVT == kF16 && D == 128;
+    constexpr bool kMfmaShape = std::is_same<IO, _Float16>::value && KVT != kF32 && D == 128;
     // grid_x arrives as the number of item groups (an upper bound).  Up to
     // kGridBlocksPerCu workgroups per CU are launched, one group each, and the
     // hardware dispatcher starts them as slots free up; groups beyond the grid
