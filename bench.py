@@ -207,19 +207,23 @@ def main():
 # --suite: the other rows of the path, one JSON line each (not the headline).
 
 
-def _events_ms(fn, n, stream):
+def _events_ms(fn, n, stream, groups=5):
+    """Median, p10 and p90 over `groups` samples of the mean time of n
+    back-to-back calls (HIP events on the launch stream), in ms."""
+    import numpy as np
     import torch
-    ts = []
-    for _ in range(n):
+    n = max(1, n // groups)
+    v = []
+    for _ in range(groups):
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         e0.record(stream)
-        fn()
+        for _ in range(n):
+            fn()
         e1.record(stream)
-        ts.append((e0, e1))
-    torch.cuda.synchronize()
-    import numpy as np
-    v = np.array([a.elapsed_time(b) for a, b in ts])
+        torch.cuda.synchronize()
+        v.append(e0.elapsed_time(e1) / n)
+    v = np.array(v)
     return float(np.median(v)), float(np.percentile(v, 10)), float(np.percentile(v, 90))
 
 
@@ -547,6 +551,6 @@ def run_suite(names, steps, warmup):
 
 if __name__ == "__main__":
     if len(sys.argv) > 1 and sys.argv[1] == "--suite":
-        run_suite(sys.argv[2].split(",") if len(sys.argv) > 2 else list(SUITES), 20, 3)
+        run_suite(sys.argv[2].split(",") if len(sys.argv) > 2 else list(SUITES), 50, 5)
         sys.exit(0)
     main()

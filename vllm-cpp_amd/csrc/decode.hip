@@ -1039,7 +1039,9 @@ int ilog2(int x) {
 DecodePlan plan_decode(const vkv_decode_params* p) {
     DecodePlan plan;
     const int bs = p->block_size;
-    int P = p->partition_size > 0 ? p->partition_size : 512;
+    // Default 768 tokens: the best of a 384..1024 sweep for both the C2
+    // (B=64, ctx U[512,4096]) and C5 (B=256, lognormal ctx) decode batches.
+    int P = p->partition_size > 0 ? p->partition_size : 768;
     // A partition starts on a block boundary and holds at most 64 blocks
     // (one block id per lane).
     if (P < bs) P = bs;
