@@ -163,7 +163,12 @@ int vkv_paged_decode(const vkv_decode_params* p, vkv_stream_t stream);
  * sequence.  This entry point does all of a step's query tokens at once;
  * the chunk's own K/V must already be in the cache (vkv_reshape_and_cache).
  * query_start_loc[s]..query_start_loc[s+1] are sequence s's rows of query.
- * Rows with q_len 1 are plain decode.
+ * Rows with q_len 1 are plain decode.  max_query_len must bound every q_len
+ * (rows past it are not computed).  fp16 queries at head_dim 64/128 over fp16
+ * or FP8 caches run sequences with q_len >= 2 on the matrix cores and the
+ * q_len 1 ones through split-K decode; other combinations decode every row
+ * with its causal context.  Uses the library's per-device workspace (calls
+ * that may run concurrently on one device race on it).
  * ------------------------------------------------------------------------- */
 typedef struct vkv_prefill_params {
     void* output;               /* [num_query_tokens, num_heads, head_dim] io_dtype */
