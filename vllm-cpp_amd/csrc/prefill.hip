@@ -236,12 +236,14 @@ __device__ __forceinline__ void prefill_block(const PrefillArgs& a, const int s,
     };
 
     // ---------------- main loop
-    float m[kRT], l[kRT];
+    float m[kRT];
+    float4_t lsum[kRT];  // row sums (every element the same), see below
     float4_t o[kRT][DT];
+    const half8_t kOnes = {1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16};
 #pragma unroll
     for (int r = 0; r < kRT; ++r) {
         m[r] = -INFINITY;
-        l[r] = 0.0f;
+        lsum[r] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int t = 0; t < DT; ++t) o[r][t] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
     }
@@ -255,73 +257,73 @@ __device__ __forceinline__ void prefill_block(const PrefillArgs& a, const int s,
         if (stager) fetch(st, 0);
     }
     auto step = [&](const int kt, const int sub) __attribute__((always_inline)) {
-        if (computes) {
-            // K operands of both 16-key halves, shared by the row tiles
-            half8_t kop[2][KS];
+        if (!computes) return;
+        const int kbase = kt * kBK + 32 * sub;
+        // S^T of both row tiles; each K operand (one LDS read) feeds both.
+        float4_t sv[kRT][2];
+#pragma unroll
+        for (int r = 0; r < kRT; ++r) sv[r][0] = sv[r][1] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+            for (int i = 0; i < KS; ++i) {
+                const half8_t kop = __builtin_bit_cast(
+                    half8_t, *reinterpret_cast<const u32x4*>(klds + (32 * sub + 16 * hh + col) * St::STR + (32 * i + 8 * grp) * 2));
+#pragma unroll
+                for (int r = 0; r < kRT; ++r)
+                    sv[r][hh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qop[r][i], sv[r][hh], 0, 0, 0);
+            }
+        half8_t pop[kRT];
+#pragma unroll
+        for (int r = 0; r < kRT; ++r) {
+            // causal / context mask (key kbase + 16 hh + 4 grp + e < rctx), only
+            // on tiles that reach past some row's context (wave-uniform test)
+            float x[8];
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-                for (int i = 0; i < KS; ++i)
-                    kop[hh][i] = __builtin_bit_cast(
-                        half8_t, *reinterpret_cast<const u32x4*>(klds + (32 * sub + 16 * hh + col) * St::STR + (32 * i + 8 * grp) * 2));
-            // V^T operands (dims 16 t + col; keys 4 grp + e, then 16 + 4 grp + e)
-            // by transpose reads of row-major V: within each 16-lane group,
-            // lane i receives element i % 4 of the 8-byte chunks addressed by
-            // lanes i / 4 + 4 e, e = 0..3.  Lane m of group grp therefore
-            // addresses key 4 grp + m / 4 (+16), dims 16 t + 4 (m % 4) .. +3.
-            half8_t vop[DT];
-            const int vrow = 32 * sub + 4 * grp + (col >> 2);
-#pragma unroll
-            for (int t = 0; t < DT; ++t) {
-                const int dcol = (16 * t + 4 * (col & 3)) * 2;
-                const u32x2 lo = tr_read(vlds + vrow * St::STR + dcol);
-                const u32x2 hi = tr_read(vlds + (16 + vrow) * St::STR + dcol);
-                vop[t] = __builtin_bit_cast(half8_t, u32x4{lo[0], lo[1], hi[0], hi[1]});
-            }
-            const int kbase = kt * kBK + 32 * sub;
-#pragma unroll
-            for (int r = 0; r < kRT; ++r) {
-                float4_t sv[2];
-#pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
-                    float4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                    for (int i = 0; i < KS; ++i)
-                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop[hh][i], qop[r][i], acc, 0, 0, 0);
-                    sv[hh] = acc;
-                }
-                // causal / context mask: key index kbase + 16 hh + 4 grp + e < rctx
-                float x[8];
-                float mx = -INFINITY;
+                for (int e = 0; e < 4; ++e) x[4 * hh + e] = sv[r][hh][e];
+            if (__builtin_amdgcn_ballot_w64(kbase + 32 > rctx[r])) {
 #pragma unroll
                 for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int key = kbase + 16 * hh + 4 * grp + e;
-                        const float v = key < rctx[r] ? sv[hh][e] : -INFINITY;
-                        x[4 * hh + e] = v;
-                        mx = fmaxf(mx, v);
-                    }
-                mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
-                mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+                    for (int e = 0; e < 4; ++e)
+                        if (kbase + 16 * hh + 4 * grp + e >= rctx[r]) x[4 * hh + e] = -INFINITY;
+            }
+            float mx = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
+            mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+            // rescale only when some row's max grows (each lane owns its row)
+            if (__builtin_amdgcn_ballot_w64(mx > m[r])) {
                 const float mn = fmaxf(m[r], mx);
-                const float mref = mn == -INFINITY ? 0.0f : mn;  // rows with no key yet
-                const float alpha = __builtin_amdgcn_exp2f((m[r] - mref) * sc);
+                const float alpha = mn > m[r] ? __builtin_amdgcn_exp2f((m[r] - mn) * sc) : 1.0f;
                 m[r] = mn;
-                l[r] *= alpha;
+                lsum[r] *= alpha;
 #pragma unroll
                 for (int t = 0; t < DT; ++t) o[r][t] *= alpha;
-                // P^T operand: k slot (grp, e) = key 4 grp + e, slot (grp, 4 + e) = key 16 + 4 grp + e
-                half8_t pop;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const _Float16 pe = static_cast<_Float16>(__builtin_amdgcn_exp2f((x[e] - mref) * sc));
-                    pop[e] = pe;
-                    l[r] += static_cast<float>(pe);  // the sum uses the fp16 weights the MFMA uses
-                }
-#pragma unroll
-                for (int t = 0; t < DT; ++t) o[r][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop[t], pop, o[r][t], 0, 0, 0);
             }
+            const float mref = m[r] == -INFINITY ? 0.0f : m[r];  // rows with no key yet
+            const float msc = mref * sc;
+            // P^T operand: k slot (grp, e) = key 4 grp + e, slot (grp, 4 + e) = key 16 + 4 grp + e
+#pragma unroll
+            for (int e = 0; e < 8; ++e) pop[r][e] = static_cast<_Float16>(__builtin_amdgcn_exp2f(fmaf(x[e], sc, -msc)));
+            // row sums on the matrix pipe: a V^T tile of ones gives sum_k p in every lane
+            lsum[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kOnes, pop[r], lsum[r], 0, 0, 0);
+        }
+        // O^T += V^T P^T; each V^T operand (two transpose reads of row-major V:
+        // within each 16-lane group, lane i receives element i % 4 of the 8-byte
+        // chunks addressed by lanes i / 4 + 4 e, e = 0..3, so lane m of group
+        // grp addresses key 4 grp + m / 4 (+16), dims 16 t + 4 (m % 4) .. +3)
+        // feeds both row tiles.
+        const int vrow = 32 * sub + 4 * grp + (col >> 2);
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+            const int dcol = (16 * t + 4 * (col & 3)) * 2;
+            const u32x2 lo = tr_read(vlds + vrow * St::STR + dcol);
+            const u32x2 hi = tr_read(vlds + (16 + vrow) * St::STR + dcol);
+            const half8_t vop = __builtin_bit_cast(half8_t, u32x4{lo[0], lo[1], hi[0], hi[1]});
+#pragma unroll
+            for (int r = 0; r < kRT; ++r) o[r][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, pop[r], o[r][t], 0, 0, 0);
         }
     };
     for (int kt = 0; kt < ntiles; ++kt) {
@@ -340,9 +342,7 @@ __device__ __forceinline__ void prefill_block(const PrefillArgs& a, const int s,
     if (!computes) return;  // (after the loop's last barrier)
 #pragma unroll
     for (int r = 0; r < kRT; ++r) {
-        float lt = l[r];
-        lt += __shfl_xor(lt, 16, kWave);
-        lt += __shfl_xor(lt, 32, kWave);
+        const float lt = lsum[r][0];  // already summed over every key of the row
         const int j = qb * kBQ + 16 * r + col;
         if (j >= qlen) continue;
         const float inv = (rctx[r] > 0 && lt > 0.0f) ? 1.0f / lt : 0.0f;
