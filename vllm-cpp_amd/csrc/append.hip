@@ -44,28 +44,46 @@ __device__ __forceinline__ u32x4 f32x8_to_f16x8(u32x4 a, u32x4 b) {
 }
 
 // Same-type append (bit copy, SRC_PER_DST = 1) or f32 -> f16 (SRC_PER_DST = 2,
-// 32 source bytes per 16 destination bytes).
+// 32 source bytes per 16 destination bytes).  Each thread takes kAppendUnroll
+// grid-strided chunks per iteration so that their slot ids, loads and stores
+// are in flight together; sources and cache rows are streamed (non-temporal:
+// each byte is touched once).
+constexpr int kAppendUnroll = 4;
 template <int SRC_PER_DST>
 __global__ __launch_bounds__(256) void append_rows_kernel(AppendArgs a) {
     const int64_t stride = int64_t(gridDim.x) * blockDim.x;
-    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < a.total; i += stride) {
-        const int64_t t = i / a.chunks_per_row;
-        const int64_t c = i - t * a.chunks_per_row;
-        const int64_t slot = a.slot_mapping[t];
-        if (slot < 0 || slot >= a.num_slots) continue;
-        const int64_t dst = slot * a.row_bytes + c * 16;
-        const char* ks = a.key + t * a.key_stride_bytes + c * 16 * SRC_PER_DST;
-        const char* vs = a.value + t * a.value_stride_bytes + c * 16 * SRC_PER_DST;
-        if constexpr (SRC_PER_DST == 1) {
-            const u32x4 k = load16(ks);
-            const u32x4 v = load16(vs);
-            store16(a.key_cache + dst, k);
-            store16(a.value_cache + dst, v);
-        } else {
-            const u32x4 k0 = load16(ks), k1 = load16(ks + 16);
-            const u32x4 v0 = load16(vs), v1 = load16(vs + 16);
-            store16(a.key_cache + dst, f32x8_to_f16x8(k0, k1));
-            store16(a.value_cache + dst, f32x8_to_f16x8(v0, v1));
+    for (int64_t i0 = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i0 < a.total; i0 += stride * kAppendUnroll) {
+        int64_t slot[kAppendUnroll], t[kAppendUnroll], c[kAppendUnroll];
+#pragma unroll
+        for (int u = 0; u < kAppendUnroll; ++u) {
+            const int64_t i = i0 + u * stride;
+            t[u] = i / a.chunks_per_row;
+            c[u] = i - t[u] * a.chunks_per_row;
+            slot[u] = i < a.total ? int64_t(a.slot_mapping[t[u]]) : -1;
+        }
+        u32x4 k[kAppendUnroll][SRC_PER_DST], v[kAppendUnroll][SRC_PER_DST];
+#pragma unroll
+        for (int u = 0; u < kAppendUnroll; ++u) {
+            if (slot[u] < 0 || slot[u] >= a.num_slots) continue;
+            const char* ks = a.key + t[u] * a.key_stride_bytes + c[u] * 16 * SRC_PER_DST;
+            const char* vs = a.value + t[u] * a.value_stride_bytes + c[u] * 16 * SRC_PER_DST;
+#pragma unroll
+            for (int j = 0; j < SRC_PER_DST; ++j) {
+                k[u][j] = load16_nt(ks + 16 * j);
+                v[u][j] = load16_nt(vs + 16 * j);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kAppendUnroll; ++u) {
+            if (slot[u] < 0 || slot[u] >= a.num_slots) continue;
+            const int64_t dst = slot[u] * a.row_bytes + c[u] * 16;
+            if constexpr (SRC_PER_DST == 1) {
+                store16_nt(a.key_cache + dst, k[u][0]);
+                store16_nt(a.value_cache + dst, v[u][0]);
+            } else {
+                store16_nt(a.key_cache + dst, f32x8_to_f16x8(k[u][0], k[u][1]));
+                store16_nt(a.value_cache + dst, f32x8_to_f16x8(v[u][0], v[u][1]));
+            }
         }
     }
 }

@@ -333,8 +333,9 @@ __device__ __forceinline__ void prefill_block(const PrefillArgs& a, const int s,
             ensure_window(((kt + 1) * kBK) >> a.bs_log2);
             if (stager) fetch(st, (kt + 1) * kBK);
         }
-        step(kt, 0);
-        if (kt * kBK + 32 < kend) step(kt, 1);
+#pragma unroll
+        for (int sub = 0; sub < kBK / 32; ++sub)
+            if (sub == 0 || kt * kBK + 32 * sub < kend) step(kt, sub);
         __syncthreads();
     }
 
