@@ -227,6 +227,22 @@ def _events_ms(fn, n, stream, groups=5):
     return float(np.median(v)), float(np.percentile(v, 10)), float(np.percentile(v, 90))
 
 
+def _cpu_time(fn, min_seconds=3.0):
+    """Seconds per call of a CPU oracle function, repeated for >= min_seconds."""
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        fn()
+        reps += 1
+        dt = time.perf_counter() - t0
+        if dt >= min_seconds:
+            return dt / reps, reps
+
+
+def _cpu_threads():
+    return max(1, min(16, os.cpu_count() or 1))
+
+
 def _rand_half(shape, g, dev, sigma):
     import torch
     return (torch.randn(shape, generator=g, device=dev) * sigma).half()
@@ -320,11 +336,28 @@ def suite_c3_prefill_only(dev, steps, warmup):
     keys = sum(int(cfg.prior_lens[s]) * int(ql[s]) + int(ql[s]) * (int(ql[s]) + 1) // 2 for s in range(npf))
     flops = 4.0 * D * H * keys
     tf = flops / (t[0] * 1e-3) / 1e12
+    # CPU: the oracle's prefill (one decode per query row, as the reference) of sequence 0
+    from oracle import oracle
+    n0 = int(lay.context_lens[0])
+    nb0 = (n0 + bs - 1) // bs
+    ids = torch.from_numpy(lay.block_tables[0, :nb0]).long().to(dev)
+    hk = kc[ids].cpu().numpy().view(np.uint16)
+    hv = vc[ids].cpu().numpy().view(np.uint16)
+    hq = q[:int(ql[0])].float().cpu().numpy()
+    thr = _cpu_threads()
+    fn_cpu = lambda: oracle.paged_prefill(hq, hk, hv, np.arange(nb0, dtype=np.int32)[None, :],
+                                          np.array([n0], np.int32), np.array([0, int(ql[0])], np.int32),
+                                          cfg.scale, nthreads=thr)
+    sec, reps = _cpu_time(fn_cpu)
+    keys0 = int(cfg.prior_lens[0]) * int(ql[0]) + int(ql[0]) * (int(ql[0]) + 1) // 2
     return {"row": "C3 prefill sequences alone", "workload": "the 8 x 512-token chunks of C3 (prior U[0,2048])",
             "us_median": round(t[0] * 1e3, 2), "us_p10_p90": [round(t[1] * 1e3, 2), round(t[2] * 1e3, 2)],
             "gflop": round(flops / 1e9, 2), "tflops": round(tf, 1),
             "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": 2500.0, "unit": "TFLOP/s",
-                         "frac": round(tf / 2500.0, 4)}}
+                         "frac": round(tf / 2500.0, 4)},
+            "cpu_baseline": {"tflops": round(4.0 * D * H * keys0 / sec / 1e12, 5), "cores": thr, "kind": "port",
+                             "sample": f"oracle prefill (one decode per query row) of sequence 0 "
+                                       f"({int(ql[0])} queries on {n0 - int(ql[0])} prior keys), {reps} calls"}}
 
 
 def suite_c1(dev, steps, warmup):
@@ -357,10 +390,23 @@ def suite_c1(dev, steps, warmup):
     torch.cuda.synchronize()
     t = _events_ms(step, steps, stream)
     kvb = cfg.kv_bytes(2)
+    from oracle import oracle
+    hk, hv = kc.cpu().numpy().view(np.uint16), vc.cpu().numpy().view(np.uint16)
+    hnk, hnv = nk.cpu().numpy().view(np.uint16), nv.cpu().numpy().view(np.uint16)
+    hq = q.float().cpu().numpy()
+    hs = slots.cpu().numpy()
+
+    def cpu_step():
+        oracle.reshape_and_cache(hnk, hnv, hk, hv, hs)
+        oracle.paged_decode(hq, hk, hv, lay.block_tables, lay.context_lens, cfg.scale, nthreads=1)
+
+    sec, reps = _cpu_time(cpu_step)
     return {"row": "C1 append + decode", "workload": "Qwen2.5-0.5B shape H14/Hkv2/D64 fp16 bs16, B=4, ctx U[1,512]",
             "kv_bytes": kvb, "step_us_median": round(t[0] * 1e3, 2),
             "step_us_p10_p90": [round(t[1] * 1e3, 2), round(t[2] * 1e3, 2)],
-            "note": "launch-bound: two kernels for 0.5 MB of KV"}
+            "note": "launch-bound: two kernels for 0.5 MB of KV",
+            "cpu_baseline": {"us_per_step": round(sec * 1e6, 1), "cores": 1, "kind": "port",
+                             "sample": f"oracle append + decode of the whole step, {reps} steps"}}
 
 
 def suite_c5(dev, steps, warmup):
@@ -410,12 +456,32 @@ def suite_c5(dev, steps, warmup):
     td = _events_ms(decode, steps, stream)
     kvb = cfg.kv_bytes(1, 4)
     gbs = kvb / (td[0] * 1e-3) / 1e9
+    from oracle import oracle
+    idx = list(range(16))
+    ctx = lay.context_lens[idx]
+    nblk = (ctx + bs - 1) // bs
+    ids_np = np.concatenate([lay.block_tables[s_, :n_] for s_, n_ in zip(idx, nblk)])
+    ids = torch.from_numpy(ids_np).long().to(dev)
+    hk, hv = kc[ids].cpu().numpy(), vc[ids].cpu().numpy()
+    hks, hvs = ks[ids].cpu().numpy(), vs[ids].cpu().numpy()
+    tabs = np.zeros((16, int(nblk.max())), np.int32)
+    off = 0
+    for i_, n_ in enumerate(nblk):
+        tabs[i_, :n_] = np.arange(off, off + n_)
+        off += int(n_)
+    hq = q[idx].float().cpu().numpy()
+    thr = _cpu_threads()
+    sec, reps = _cpu_time(lambda: oracle.paged_decode(hq, hk, hv, tabs, ctx, cfg.scale, key_scales=hks,
+                                                      value_scales=hvs, nthreads=thr))
+    cpu_bytes = int(ctx.astype(np.int64).sum()) * Hkv * (2 * D + 8)
     return {"row": "C5 FP8 append + decode", "workload": "H32/Hkv8/D128, bs16, B=256, ctx = clip(lognormal(7.6,1),128,32768)",
             "context_tokens": int(lay.context_lens.astype(np.int64).sum()), "kv_bytes": kvb,
             "decode_us_median": round(td[0] * 1e3, 2), "decode_us_p10_p90": [round(td[1] * 1e3, 2), round(td[2] * 1e3, 2)],
             "append_us_median": round(ta[0] * 1e3, 2),
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(gbs / HBM_PEAK_GBS, 4)}}
+                         "frac": round(gbs / HBM_PEAK_GBS, 4)},
+            "cpu_baseline": {"gbs": round(cpu_bytes / sec / 1e9, 3), "cores": thr, "kind": "port",
+                             "sample": f"oracle FP8 decode of sequences 0-15 ({int(ctx.sum())} tokens), {reps} calls"}}
 
 
 def suite_append(dev, steps, warmup):
@@ -455,8 +521,28 @@ def suite_append(dev, steps, warmup):
             t = _events_ms(fn, steps, stream)
             nbytes = T * Hkv * D * 2 * 2 + wbytes + T * 4
             gbs = nbytes / (t[0] * 1e-3) / 1e9
-            rows.append({"tokens": T, "cache": kind, "us_median": round(t[0] * 1e3, 2), "bytes": nbytes,
-                         "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)})
+            row = {"tokens": T, "cache": kind, "us_median": round(t[0] * 1e3, 2), "bytes": nbytes,
+                   "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+            if T == 65536:
+                from oracle import oracle
+                hk = k.cpu().numpy().view(np.uint16)
+                hv = v.cpu().numpy().view(np.uint16)
+                hp = perm.cpu().numpy()
+                if kind == "f16":
+                    hkc = np.zeros((N, bs, Hkv, D), np.uint16)
+                    hvc = np.zeros_like(hkc)
+                    fn_cpu = lambda: oracle.reshape_and_cache(hk, hv, hkc, hvc, hp)
+                else:
+                    hkc = np.zeros((N, bs, Hkv, D), np.uint8)
+                    hvc = np.zeros_like(hkc)
+                    hks = np.zeros((N, bs, Hkv), np.float32)
+                    hvs = np.zeros_like(hks)
+                    fn_cpu = lambda: oracle.reshape_and_cache(hk, hv, hkc, hvc, hp, hks, hvs)
+                sec, reps = _cpu_time(fn_cpu)
+                row["cpu_baseline"] = {"gbs": round(nbytes / sec / 1e9, 3), "cores": 1, "kind": "port",
+                                       "sample": f"oracle append (the reference's per-token row copy) of the same "
+                                                 f"{T} tokens, {reps} calls"}
+            rows.append(row)
             del kc, vc, ks, vs
         del k, v
         torch.cuda.empty_cache()
@@ -523,6 +609,15 @@ def suite_c4(dev, steps, warmup):
     b = torch.from_numpy(free).long().to(dev)
     swap_exact = all(torch.equal(pl[l][b], pl[l][a]) for pl in planes for l in range(L))
     swap_bytes = nsw * hb
+    from oracle import oracle
+    Ls, Ps = 4, 256
+    sub_ids = np.unique(np.concatenate([cfg.copy_pairs[:Ps, 0], cfg.copy_pairs[:Ps, 1]]))
+    remap = {int(b): i for i, b in enumerate(sub_ids)}
+    sub_pairs = np.array([[remap[int(a_)], remap[int(b_)]] for a_, b_ in cfg.copy_pairs[:Ps]], np.int32)
+    sid = torch.from_numpy(sub_ids).long().to(dev)
+    host_planes = [np.ascontiguousarray(pl[:Ls][:, sid].cpu().numpy()) for pl in planes]
+    sec, reps = _cpu_time(lambda: oracle.copy_blocks(host_planes, sub_pairs))
+    cpu_copy_bytes = 2 * Ps * Ls * 2 * cfg.block_bytes
     return {"row": "C4 copy_blocks + swap_blocks", "workload": "32 layers x K,V x [8192, 64, 8, 128] fp16, 4096 copy pairs, 2048 swaps",
             "copy_us_median": round(t[0] * 1e3, 1), "copy_bytes_read_plus_write": copy_bytes,
             "copy_roofline": {"bound": "hbm", "achieved": round(copy_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -531,7 +626,9 @@ def suite_c4(dev, steps, warmup):
             "swap_bytes_per_direction": swap_bytes,
             "swap_out_gbs": round(swap_bytes / (t_out[0] * 1e-3) / 1e9, 1),
             "swap_in_gbs": round(swap_bytes / (t_in[0] * 1e-3) / 1e9, 1),
-            "swap_round_trip_bit_exact": bool(swap_exact)}
+            "swap_round_trip_bit_exact": bool(swap_exact),
+            "cpu_baseline": {"copy_gbs": round(cpu_copy_bytes / sec / 1e9, 3), "cores": 1, "kind": "port",
+                             "sample": f"oracle copy_blocks of {Ps} pairs x {Ls} layers x K,V, {reps} calls"}}
 
 
 SUITES = {"stream": suite_stream, "c1": suite_c1, "append": suite_append, "c3": suite_c3,
