@@ -69,7 +69,7 @@ struct PrefillArgs {
     int32_t qblocks;  // query blocks per sequence in the grid
     int32_t num_seqs;
     const int2* items;       // work list (s, qb * Hkv + kvh)
-    const int32_t* item_count;
+    int32_t* item_count;     // [0] items, [1] claim counter (zeroed by the list kernel)
     float scale_log2;
 };
 
@@ -358,16 +358,25 @@ __device__ __forceinline__ void prefill_block(const PrefillArgs& a, const int s,
     }
 }
 
-// Persistent workgroups walk the item list (built by prefill_items_kernel);
-// every item ends with a barrier, so LDS is free for the next one.
+// Persistent workgroups claim items of the list (built by
+// prefill_items_kernel, longest first) one at a time through a counter, so a
+// workgroup that finishes a short item takes the next one (greedy
+// longest-processing-time balance).  Every item ends with a barrier, so LDS is
+// free for the next one; every workgroup leaves once the list is exhausted.
 template <int D, int KVT>
 __global__ __launch_bounds__(64 * kMaxWaves) void prefill_mfma_kernel(PrefillArgs a) {
     using St = Stage<D, KVT>;
     __shared__ __attribute__((aligned(16))) char klds[kBK * St::STR];
     __shared__ __attribute__((aligned(16))) char vlds[kBK * St::STR];
     __shared__ int btc[kBtCache];
-    const int count = *a.item_count;
-    for (int it = blockIdx.x; it < count; it += gridDim.x) {
+    __shared__ int claimed;
+    const int count = a.item_count[0];
+    for (;;) {
+        if (threadIdx.x == 0) claimed = atomicAdd(a.item_count + 1, 1);
+        __syncthreads();
+        const int it = claimed;
+        __syncthreads();  // every thread has read `claimed` before thread 0 may overwrite it
+        if (it >= count) break;
         const int2 item = a.items[it];
         prefill_block<D, KVT>(a, item.x, item.y / a.num_kv_heads, item.y % a.num_kv_heads, klds, vlds, btc);
         __syncthreads();
@@ -425,7 +434,10 @@ __global__ __launch_bounds__(256) void prefill_items_kernel(const int32_t* qsl, 
         if (lt == 0) break;
         total += lt;
     }
-    if (tid == 0) *count = total;
+    if (tid == 0) {
+        count[0] = total;
+        count[1] = 0;  // claim counter of the prefill kernel
+    }
 }
 
 int ilog2i(int x) {
@@ -477,8 +489,8 @@ int launch_prefill_mfma(const vkv_prefill_params* p, void* item_space, hipStream
     a.item_count = count;
     hipLaunchKernelGGL(prefill_items_kernel, dim3(1), dim3(256), 0, st, p->query_start_loc, p->num_seqs,
                        p->num_kv_heads, a.qblocks, items, count);
-    // Persistent grid: two workgroups per CU (one runs, one waits), never more
-    // than there can be items.
+    // Persistent grid: two workgroups per CU (at D = 128 one is resident, the
+    // other starts when a CU frees up), never more than there can be items.
     int dev = 0, cus = 256;
     if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     const int64_t upper = int64_t(p->num_seqs) * a.qblocks * p->num_kv_heads;
