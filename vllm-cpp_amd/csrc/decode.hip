@@ -55,6 +55,18 @@ constexpr int kUnroll = VKV_DECODE_UNROLL;
 #define VKV_DECODE_MIN_WAVES 3
 #endif
 constexpr int kMinWavesPerSimd = VKV_DECODE_MIN_WAVES;
+// MFMA variant: FP8 groups above kOneChunkAboveGFp8 heads load one 16-token
+// chunk per step instead of two (their chunks carry scales); fp16 groups above
+// kOneChunkAboveG heads keep two chunks at a lower occupancy target.
+// Build-time tuning knobs.
+#ifndef VKV_DECODE_ONE_CHUNK_ABOVE_G
+#define VKV_DECODE_ONE_CHUNK_ABOVE_G 6
+#endif
+#ifndef VKV_DECODE_ONE_CHUNK_ABOVE_G_FP8
+#define VKV_DECODE_ONE_CHUNK_ABOVE_G_FP8 3
+#endif
+constexpr int kOneChunkAboveG = VKV_DECODE_ONE_CHUNK_ABOVE_G;
+constexpr int kOneChunkAboveGFp8 = VKV_DECODE_ONE_CHUNK_ABOVE_G_FP8;
 constexpr float kLog2e = 1.4426950408889634f;
 // Launch cap in workgroups per CU.  A grid holding every item group lets the
 // hardware dispatcher balance the CUs; claims through the counters only serve
@@ -716,13 +728,13 @@ __device__ __forceinline__ void decode_item_mfma(const DecodeArgs& a, const int 
     };
 
     // Two chunks (32 tokens, 16 KiB of K/V per wave at D=128 fp16) are loaded
-    // before either is computed, doubling the bytes in flight per wave.  Groups
-    // above 6 heads (3 for FP8, whose chunks carry scales) load one chunk at a
+    // before either is computed, doubling the bytes in flight per wave.  FP8
+    // groups above 3 heads (their chunks carry scales) load one chunk at a
     // time so that the 8 G accumulators per lane fit without spilling.
     const int nc = (n + CH - 1) / CH;
     const bool ragged = (n % CH) != 0;
     int ci = 0;
-    if constexpr (G > (FP8 ? 3 : 6)) {
+    if constexpr (FP8 && G > kOneChunkAboveGFp8) {
         for (; ci + 1 < nc; ++ci) {
             Chunk x;
             load_chunk(x, ci * CH);
@@ -786,8 +798,17 @@ __device__ __forceinline__ void decode_item_mfma(const DecodeArgs& a, const int 
 // workgroup hold adjacent kv heads of the same blocks.  Workgroups claim item
 // groups dynamically, so all stay busy until the list runs out.  Nothing
 // waits on another workgroup.
+// Register budget per instantiation: the fp16 matrix-core variant with 7-8
+// heads per group keeps two chunks in flight at 2 waves per SIMD (measured
+// faster than one chunk at 3), and FP8 groups of 7-8 fit their one chunk
+// without spilling at 2; everything else targets kMinWavesPerSimd.
+template <int KVT, int G, bool MFMA>
+constexpr int min_waves_per_simd() {
+    return (MFMA && ((KVT == kF16 && G > kOneChunkAboveG) || (KVT == kFp8 && G > 6))) ? 2 : kMinWavesPerSimd;
+}
+
 template <typename IO, int KVT, int D, int G, bool MFMA>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kMinWavesPerSimd)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(min_waves_per_simd<KVT, G, MFMA>())))
 void decode_partition_kernel(DecodeArgs a) {
     extern __shared__ int prefix[];  // [num_rows + 1] exclusive prefix of partitions per row
     const int lane = threadIdx.x & (kWave - 1);
