@@ -124,3 +124,49 @@ def test_append_then_gather_is_identity_c2(vkv, cuda):
     assert torch.equal(got_v.view(torch.int16), v.view(torch.int16))
     # nothing else was written
     assert int((kc != 0).sum()) == int((k != 0).sum())
+
+
+def test_append_fp8_rounding_boundaries(vkv, oracle, cuda):
+    """x / scale landing on e4m3 rounding midpoints (ties to even) and a few fp32
+    ulps either side, with scales that are not powers of two: codes must equal
+    the oracle's correctly rounded quotient, whatever shortcut the kernel takes."""
+    import torch
+    codes = np.arange(0x7F, dtype=np.int64)
+    vals = np.array([oracle.fp8_decode(int(c)) for c in codes], np.float64)
+    mids = (vals[:-1] + vals[1:]) / 2.0
+    Hkv, D, N, bs = 4, 128, 16, 16
+    rows = []
+    for c in (3.0, 5.0, 7.0, 1.1, 0.3, 13.7, 1.0 / 3.0, 100.25):
+        amax = np.float32(448.0 * c)
+        sc = np.float32(amax / np.float32(448.0))
+        base = (mids * np.float64(sc)).astype(np.float32)
+        for nudge in (0, 1, -1, 2, -2, 3, -3):
+            x = base.copy()
+            for _ in range(abs(nudge)):
+                x = np.nextafter(x, np.float32(np.inf if nudge > 0 else -np.inf)).astype(np.float32)
+            x = np.clip(x, -amax, amax)
+            sign = np.where(np.arange(len(x)) % 2 == 0, 1.0, -1.0).astype(np.float32)
+            row = np.zeros(D, np.float32)
+            row[0] = amax
+            row[1:1 + min(len(x), D - 1)] = (x * sign)[:D - 1]
+            rows.append(row)
+    T = (len(rows) + Hkv - 1) // Hkv
+    k = np.zeros((T * Hkv, D), np.float32)
+    k[:len(rows)] = np.stack(rows)
+    k = k.reshape(T, Hkv, D)
+    v = -k[::-1].copy()
+    slots = np.arange(T, dtype=np.int32) * 3 % (N * bs)
+    kc_ref = np.zeros((N, bs, Hkv, D), np.uint8)
+    vc_ref = np.zeros_like(kc_ref)
+    ks_ref = np.zeros((N, bs, Hkv), np.float32)
+    vs_ref = np.zeros_like(ks_ref)
+    oracle.reshape_and_cache(k, v, kc_ref, vc_ref, slots, ks_ref, vs_ref)
+    kc = torch.zeros((N, bs, Hkv, D), dtype=torch.uint8, device=cuda)
+    vc = torch.zeros_like(kc)
+    ks = torch.zeros((N, bs, Hkv), dtype=torch.float32, device=cuda)
+    vs = torch.zeros_like(ks)
+    vkv.reshape_and_cache(to_dev(k, cuda), to_dev(v, cuda), kc, vc, to_dev(slots, cuda), ks, vs)
+    torch.cuda.synchronize()
+    assert np.array_equal(to_np(ks).view(np.uint32), ks_ref.view(np.uint32))
+    assert np.array_equal(to_np(kc), kc_ref)
+    assert np.array_equal(to_np(vc), vc_ref)

@@ -88,6 +88,20 @@ __global__ __launch_bounds__(256) void append_rows_kernel(AppendArgs a) {
     }
 }
 
+// x / s exactly as the correctly rounded fp32 quotient would encode to e4m3.
+// z = x * fl(1/s) is within 2 fp32 ulps of fl(x / s), so the two can only
+// encode differently when an e4m3 rounding midpoint is within that distance of
+// z: normal e4m3 range midpoints are the fp32 values whose 20 mantissa bits
+// below the kept 3 equal 0x80000.  Those cases, the e4m3 subnormal range
+// (|z| < 2^-6, other midpoints) and non-finite values take the IEEE division.
+__device__ __forceinline__ float quotient(float x, float s, float rinv) {
+    const float z = x * rinv;
+    const uint32_t b = as_u32(z) & 0x7FFFFFFFu;
+    const int d = int(b & 0xFFFFFu) - 0x80000;
+    if (b < 0x3C800000u || b >= 0x7F800000u || (d >= -4 && d <= 4)) return x / s;
+    return z;
+}
+
 // Quantise-on-append to e4m3fn.  A group of LPT = head_dim/16 consecutive
 // lanes holds one (token, kv head) vector, 16 elements per lane; the group's
 // amax comes from a DPP max reduction, then every lane divides its elements by
@@ -127,12 +141,13 @@ __global__ __launch_bounds__(256) void append_fp8_kernel(AppendArgs a) {
             for (int e = 0; e < 16; ++e) amax = fmaxf(amax, fabsf(x[e]));
             amax = group_max<LPT>(amax);
             const float scale = fp8_scale_from_amax(amax);
+            const float rinv = 1.0f / scale;  // correctly rounded
             u32x4 q;
 #pragma unroll
             for (int w = 0; w < 4; ++w) {
                 uint32_t packed = 0;
 #pragma unroll
-                for (int b = 0; b < 4; ++b) packed |= f32_to_fp8_sat(x[4 * w + b] / scale) << (8 * b);
+                for (int b = 0; b < 4; ++b) packed |= f32_to_fp8_sat(quotient(x[4 * w + b], scale, rinv)) << (8 * b);
                 q[w] = packed;
             }
             char* cache = kv ? a.value_cache : a.key_cache;
