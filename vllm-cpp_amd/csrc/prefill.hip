@@ -256,11 +256,10 @@ __device__ __forceinline__ void prefill_block(const PrefillArgs& a, const int s,
         ensure_window(0);
         if (stager) fetch(st, 0);
     }
-    auto step = [&](const int kt, const int sub) __attribute__((always_inline)) {
-        if (!computes) return;
-        const int kbase = kt * kBK + 32 * sub;
+    // One 32-key step in three parts, so that a tile's second S^T (matrix
+    // pipe) is issued before the first step's softmax (VALU) and overlaps it.
+    auto qk = [&](const int sub, float4_t (&sv)[kRT][2]) __attribute__((always_inline)) {
         // S^T of both row tiles; each K operand (one LDS read) feeds both.
-        float4_t sv[kRT][2];
 #pragma unroll
         for (int r = 0; r < kRT; ++r) sv[r][0] = sv[r][1] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -273,7 +272,8 @@ __device__ __forceinline__ void prefill_block(const PrefillArgs& a, const int s,
                 for (int r = 0; r < kRT; ++r)
                     sv[r][hh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qop[r][i], sv[r][hh], 0, 0, 0);
             }
-        half8_t pop[kRT];
+    };
+    auto softmax = [&](const int kbase, const float4_t (&sv)[kRT][2], half8_t (&pop)[kRT]) __attribute__((always_inline)) {
 #pragma unroll
         for (int r = 0; r < kRT; ++r) {
             // causal / context mask (key kbase + 16 hh + 4 grp + e < rctx), only
@@ -310,6 +310,8 @@ __device__ __forceinline__ void prefill_block(const PrefillArgs& a, const int s,
             // row sums on the matrix pipe: a V^T tile of ones gives sum_k p in every lane
             lsum[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kOnes, pop[r], lsum[r], 0, 0, 0);
         }
+    };
+    auto pv = [&](const int sub, const half8_t (&pop)[kRT]) __attribute__((always_inline)) {
         // O^T += V^T P^T; each V^T operand (two transpose reads of row-major V:
         // within each 16-lane group, lane i receives element i % 4 of the 8-byte
         // chunks addressed by lanes i / 4 + 4 e, e = 0..3, so lane m of group
@@ -326,6 +328,7 @@ __device__ __forceinline__ void prefill_block(const PrefillArgs& a, const int s,
             for (int r = 0; r < kRT; ++r) o[r][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, pop[r], o[r][t], 0, 0, 0);
         }
     };
+    static_assert(kBK == 64, "the tile loop below computes two 32-key steps");
     for (int kt = 0; kt < ntiles; ++kt) {
         if (stager) put(st);
         __syncthreads();
@@ -333,9 +336,19 @@ __device__ __forceinline__ void prefill_block(const PrefillArgs& a, const int s,
             ensure_window(((kt + 1) * kBK) >> a.bs_log2);
             if (stager) fetch(st, (kt + 1) * kBK);
         }
-#pragma unroll
-        for (int sub = 0; sub < kBK / 32; ++sub)
-            if (sub == 0 || kt * kBK + 32 * sub < kend) step(kt, sub);
+        if (computes) {
+            const bool second = kt * kBK + 32 < kend;
+            float4_t sa[kRT][2], sb[kRT][2];
+            half8_t pa[kRT], pb[kRT];
+            qk(0, sa);
+            if (second) qk(1, sb);
+            softmax(kt * kBK, sa, pa);
+            pv(0, pa);
+            if (second) {
+                softmax(kt * kBK + 32, sb, pb);
+                pv(1, pb);
+            }
+        }
         __syncthreads();
     }
 
