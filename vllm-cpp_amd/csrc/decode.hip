@@ -582,8 +582,12 @@ __device__ __forceinline__ void decode_item_mfma(const DecodeArgs& a, const int 
         u32x4 k[FP8 ? 2 : 4];
         u32x4 v[FP8 ? 1 : 4];
         u32x2 v8[FP8 ? 4 : 1];
-        float ks[FP8 ? 4 : 1];  // scales of tokens 4 quad + k (x 256)
-        float vs[FP8 ? 4 : 1];  // scales of tokens 4 u + quad (x 256)
+        // FP8: one scale per lane (lanes 0-15: K scale of token l, lanes
+        // 16-31: V scale of token l - 16), shuffled to the lanes that use it;
+        // after compute starts, ks/vs hold the per-lane values.
+        float sc1;
+        float ks[FP8 ? 4 : 1];  // scales of tokens 4 quad + k
+        float vs[FP8 ? 4 : 1];  // scales of tokens 4 u + quad
     };
     // Issue the K (A-operand layout) and V (row layout) loads of the 16 tokens
     // at c.  Addresses are always valid (block ids past the partition are 0).
@@ -601,11 +605,7 @@ __device__ __forceinline__ void decode_item_mfma(const DecodeArgs& a, const int 
             for (int u = 0; u < 4; ++u)
                 ch.v8[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(vb + voff + u * 4 * slot_stride));
             const int64_t sbase = ((int64_t(blk) << a.bs_log2) + (c & bs_mask)) * a.num_kv_heads + kvh;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                ch.ks[k] = a.ks[sbase + int64_t(4 * quad + k) * a.num_kv_heads];
-                ch.vs[k] = a.vs[sbase + int64_t(4 * k + quad) * a.num_kv_heads];
-            }
+            ch.sc1 = ((lane & 16) ? a.vs : a.ks)[sbase + int64_t(col) * a.num_kv_heads];
         } else {
 #pragma unroll
             for (int i = 0; i < 4; ++i) ch.k[i] = load16(kb + koff + 64 * i);
@@ -628,7 +628,11 @@ __device__ __forceinline__ void decode_item_mfma(const DecodeArgs& a, const int 
                     __builtin_bit_cast(half8_t, u32x4{w[0], w[1], w[2], w[3]}), qb[i], cc, 0, 0, 0);
             }
 #pragma unroll
-            for (int k = 0; k < 4; ++k) cc[k] *= ch.ks[k] * kFp8HalfScale;
+            for (int k = 0; k < 4; ++k) {
+                ch.ks[k] = __shfl(ch.sc1, 4 * quad + k, kWave);
+                ch.vs[k] = __shfl(ch.sc1, 16 + 4 * k + quad, kWave);
+                cc[k] *= ch.ks[k] * kFp8HalfScale;
+            }
         } else {
 #pragma unroll
             for (int i = 0; i < 4; ++i)
