@@ -525,9 +525,13 @@ def suite_append(dev, steps, warmup):
                    "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
             if T == 65536:
                 from oracle import oracle
-                hk = k.cpu().numpy().view(np.uint16)
-                hv = v.cpu().numpy().view(np.uint16)
-                hp = perm.cpu().numpy()
+                # the FP8 oracle encodes by brute force (nearest of 127 magnitudes): time a
+                # 4096-token slice of the same workload for it
+                Tc = T if kind == "f16" else 4096
+                hk = k[:Tc].cpu().numpy().view(np.uint16)
+                hv = v[:Tc].cpu().numpy().view(np.uint16)
+                hp = perm[:Tc].cpu().numpy()
+                cpu_bytes = nbytes * Tc // T
                 if kind == "f16":
                     hkc = np.zeros((N, bs, Hkv, D), np.uint16)
                     hvc = np.zeros_like(hkc)
@@ -539,15 +543,73 @@ def suite_append(dev, steps, warmup):
                     hvs = np.zeros_like(hks)
                     fn_cpu = lambda: oracle.reshape_and_cache(hk, hv, hkc, hvc, hp, hks, hvs)
                 sec, reps = _cpu_time(fn_cpu)
-                row["cpu_baseline"] = {"gbs": round(nbytes / sec / 1e9, 3), "cores": 1, "kind": "port",
-                                       "sample": f"oracle append (the reference's per-token row copy) of the same "
-                                                 f"{T} tokens, {reps} calls"}
+                row["cpu_baseline"] = {"gbs": round(cpu_bytes / sec / 1e9, 3), "cores": 1, "kind": "port",
+                                       "sample": f"oracle append (the reference's per-token row copy) of the first "
+                                                 f"{Tc} of the same {T} tokens, {reps} calls"}
             rows.append(row)
             del kc, vc, ks, vs
         del k, v
         torch.cuda.empty_cache()
     return {"row": "append (reshape_and_cache) T-sweep", "workload": "Hkv8/D128 fp16 source, bs16, random slots",
             "sweep": rows, "roofline_bound": "hbm", "peak": HBM_PEAK_GBS}
+
+
+def suite_rope(dev, steps, warmup):
+    """Fused RoPE + append (vkv_rope_reshape_and_cache) at the C2 head shape (H32/Hkv8/D128
+    fp16, bs16), fp16 and FP8 caches, T in {64 (C2's step), 4216, 65536}; beside it the
+    unfused pair (rope in place, then reshape_and_cache) on the same inputs."""
+    import numpy as np
+    import torch
+    import vllm_kv_amd as vkv
+    H, Hkv, D, bs, P = 32, 8, 128, 16, 8192
+    cs = torch.from_numpy(vkv.rope_cos_sin_host(500000.0, D, P)).to(dev)
+    stream = torch.cuda.current_stream()
+    g = torch.Generator(device=dev).manual_seed(6)
+    rows = []
+    for T in (64, 4216, 65536):
+        N = (int(T * 1.25) + bs - 1) // bs
+        perm = torch.randperm(N * bs, generator=torch.Generator().manual_seed(T))[:T].int().to(dev)
+        pos = torch.randint(0, P, (T,), generator=torch.Generator().manual_seed(T + 1)).int().to(dev)
+        q = _rand_half((T, H, D), g, dev, 0.3)
+        k = _rand_half((T, Hkv, D), g, dev, 0.3)
+        v = _rand_half((T, Hkv, D), g, dev, 0.3)
+        for kind in ("f16", "fp8"):
+            cdt = torch.float16 if kind == "f16" else torch.uint8
+            kc = torch.zeros((N, bs, Hkv, D), dtype=cdt, device=dev)
+            vc = torch.zeros_like(kc)
+            ks = vs = None
+            if kind == "fp8":
+                ks = torch.zeros((N, bs, Hkv), dtype=torch.float32, device=dev)
+                vs = torch.zeros_like(ks)
+
+            def fused():
+                vkv.rope_reshape_and_cache(q, k, v, cs, positions=pos, key_cache=kc, value_cache=vc,
+                                           slot_mapping=perm, key_scales=ks, value_scales=vs, stream=stream)
+
+            def unfused():
+                vkv.rope_reshape_and_cache(q, k, None, cs, positions=pos, stream=stream)
+                vkv.reshape_and_cache(k, v, kc, vc, perm, ks, vs, stream=stream)
+
+            for _ in range(warmup):
+                fused()
+                unfused()
+            torch.cuda.synchronize()
+            tf = _events_ms(fused, steps, stream)
+            tu = _events_ms(unfused, steps, stream)
+            ceb = 2 if kind == "f16" else 1
+            nbytes = (T * H * D * 2 * 2 + T * Hkv * D * 2 * 2 + T * Hkv * (D * ceb + (4 if kind == "fp8" else 0)) * 2
+                      + T * D * 4 + T * 8)
+            gbs = nbytes / (tf[0] * 1e-3) / 1e9
+            rows.append({"tokens": T, "cache": kind, "fused_us": round(tf[0] * 1e3, 2),
+                         "unfused_us": round(tu[0] * 1e3, 2), "bytes": nbytes, "gbs": round(gbs, 1),
+                         "frac": round(gbs / HBM_PEAK_GBS, 4)})
+            del kc, vc, ks, vs
+        del q, k, v
+        torch.cuda.empty_cache()
+    return {"row": "fused RoPE + append", "workload": "H32/Hkv8/D128 fp16 q/k/v, bs16, random slots and positions",
+            "sweep": rows, "roofline_bound": "hbm", "peak": HBM_PEAK_GBS,
+            "bytes_counted": "q read+write, k and v read, cache rows (+ FP8 scales) written, one table row "
+                             "(D fp32) and slot + position per token"}
 
 
 def suite_stream(dev, steps, warmup):
@@ -631,7 +693,7 @@ def suite_c4(dev, steps, warmup):
                              "sample": f"oracle copy_blocks of {Ps} pairs x {Ls} layers x K,V, {reps} calls"}}
 
 
-SUITES = {"stream": suite_stream, "c1": suite_c1, "append": suite_append, "c3": suite_c3,
+SUITES = {"stream": suite_stream, "c1": suite_c1, "append": suite_append, "rope": suite_rope, "c3": suite_c3,
           "c3p": suite_c3_prefill_only, "c5": suite_c5, "c4": suite_c4}
 
 

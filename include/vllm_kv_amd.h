@@ -101,6 +101,62 @@ int vkv_slot_mapping_host(const int32_t* block_table, int32_t table_len, int32_t
                           int32_t context_len, int32_t num_tokens, int32_t* slot_mapping);
 
 /* -------------------------------------------------------------------------
+ * Rotary position embedding fused with the KV append.
+ *
+ * Replaces the reference's rope_forward (src/kernels/rotary_embedding.cu:37-45,
+ * declared in include/vllm/kernels/rotary_embedding.cuh:9-12) followed by the
+ * append loop of AttentionLayer::forward (src/layers/attention.cpp:79-102).
+ * For token t at position pos = positions[t] (positions == NULL: start_pos + t,
+ * the reference's form) and every dim pair (d, d + head_dim/2), d < head_dim/2,
+ * with c = cos_sin[pos][d][0], s = cos_sin[pos][d][1]:
+ *   x[d] <- fma(x[d], c, -(x[d+D/2] * s));  x[d+D/2] <- fma(x[d], s, x[d+D/2] * c)
+ * in fp32, rounded to src_dtype.  Every query head is rotated in place.
+ *   key_cache != NULL (fused): the rotated key and the value rows are stored to
+ *     slot slot_mapping[t] exactly as vkv_reshape_and_cache stores its source
+ *     (same skip rule, dtype rules and FP8 quantisation); key is not written.
+ *   key_cache == NULL (rope only): key heads are rotated in place as well;
+ *     value, slot_mapping and the cache fields are ignored.
+ * Positions are clamped to [0, max_position) (the reference reads out of its
+ * table there).  cos_sin is [max_position][head_dim/2][2] fp32, the
+ * reference's table layout (src/model/qwen.cpp:119-128);
+ * vkv_rope_cos_sin_host() fills it as the reference does.  head_dim 64, 128
+ * or 256; query/key/value/cos_sin 16-byte aligned with 16-byte token strides.
+ * ------------------------------------------------------------------------- */
+typedef struct vkv_rope_append_params {
+    void* query;                /* [num_tokens, num_heads, head_dim] src_dtype, rotated in place */
+    void* key;                  /* [num_tokens, num_kv_heads, head_dim] src_dtype */
+    const void* value;          /* [num_tokens, num_kv_heads, head_dim] src_dtype (fused only) */
+    int64_t query_stride;       /* elements between tokens; 0 = dense */
+    int64_t key_stride;
+    int64_t value_stride;
+    const float* cos_sin;       /* [max_position, head_dim/2, 2] */
+    const int32_t* positions;   /* [num_tokens] device, or NULL */
+    int32_t start_pos;          /* used when positions == NULL */
+    int32_t max_position;
+    void* key_cache;            /* NULL: rope only */
+    void* value_cache;
+    float* key_scales;          /* FP8 only */
+    float* value_scales;
+    const int32_t* slot_mapping;/* [num_tokens] device (fused only) */
+    int32_t num_tokens;
+    int32_t num_heads;
+    int32_t num_kv_heads;
+    int32_t head_dim;
+    int32_t block_size;
+    int32_t num_blocks;
+    int32_t src_dtype;          /* VKV_DTYPE_F32 / F16 (query, key, value) */
+    int32_t cache_dtype;        /* as vkv_append_params.cache_dtype (fused only) */
+} vkv_rope_append_params;
+
+int vkv_rope_reshape_and_cache(const vkv_rope_append_params* p, vkv_stream_t stream);
+
+/* Host helper: the reference's RoPE table (src/model/qwen.cpp:119-128):
+ * cos_sin[pos][d] = {cosf(f), sinf(f)}, f = pos / powf(theta, 2.0f*d/head_dim),
+ * all in fp32 with the C library's powf/cosf/sinf, for pos < max_position and
+ * d < head_dim/2.  Pure host code. */
+int vkv_rope_cos_sin_host(float theta, int32_t head_dim, int32_t max_position, float* cos_sin);
+
+/* -------------------------------------------------------------------------
  * Paged decode attention.
  *
  * Replaces vllm::paged_attention_forward (src/attention/paged_attention.cu:85-93,

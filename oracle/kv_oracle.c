@@ -117,6 +117,47 @@ static size_t dtype_bytes(int32_t dtype) {
     return dtype == OR_F32 ? 4u : dtype == OR_F16 ? 2u : 1u;
 }
 
+/* ---------------------------------------------------------------- rope */
+
+static void store_elem(void* base, int64_t i, int32_t dtype, float x) {
+    if (dtype == OR_F32) ((float*)base)[i] = x;
+    else ((uint16_t*)base)[i] = oracle_f32_to_f16(x);
+}
+
+/* src/kernels/rotary_embedding.cu:13-34, one (token, head, dim pair) at a time:
+ * x0 = x[d], x1 = x[d + D/2], c/s from the interleaved table row of pos;
+ * x[d] = x0*c - x1*s, x[d+D/2] = x0*s + x1*c, each evaluated as one fused
+ * multiply-add over a rounded product (fmaf(x0, c, -(x1*s)), fmaf(x0, s, x1*c)). */
+static void rope_vec(void* base, int64_t off, int32_t head_dim, const float* row, int32_t dtype) {
+    const int32_t half = head_dim / 2;
+    for (int32_t d = 0; d < half; ++d) {
+        const float c = row[2 * d], s = row[2 * d + 1];
+        const float x0 = load_elem(base, off + d, dtype);
+        const float x1 = load_elem(base, off + d + half, dtype);
+        store_elem(base, off + d, dtype, fmaf(x0, c, -(x1 * s)));
+        store_elem(base, off + d + half, dtype, fmaf(x0, s, x1 * c));
+    }
+}
+
+void oracle_rope(void* query, void* key, int64_t query_stride, int64_t key_stride,
+                 const float* cos_sin, const int32_t* positions, int32_t start_pos,
+                 int32_t max_position, int32_t num_tokens, int32_t num_heads,
+                 int32_t num_kv_heads, int32_t head_dim, int32_t src_dtype) {
+    pthread_once(&g_tables_once, fill_tables);
+    if (query_stride == 0) query_stride = (int64_t)num_heads * head_dim;
+    if (key_stride == 0) key_stride = (int64_t)num_kv_heads * head_dim;
+    for (int32_t t = 0; t < num_tokens; ++t) {
+        int32_t pos = positions ? positions[t] : start_pos + t;
+        if (pos < 0) pos = 0;
+        if (pos >= max_position) pos = max_position - 1;
+        const float* row = cos_sin + (int64_t)pos * head_dim;
+        for (int32_t h = 0; h < num_heads; ++h) {
+            rope_vec(query, t * query_stride + (int64_t)h * head_dim, head_dim, row, src_dtype);
+            if (h < num_kv_heads) rope_vec(key, t * key_stride + (int64_t)h * head_dim, head_dim, row, src_dtype);
+        }
+    }
+}
+
 /* ---------------------------------------------------------------- append */
 
 void oracle_reshape_and_cache(const void* key, const void* value, int64_t key_stride,

@@ -55,6 +55,18 @@ void oracle_reshape_and_cache(const void* key, const void* value, int64_t key_st
                               int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
                               int32_t num_blocks, int32_t src_dtype, int32_t cache_dtype);
 
+/* RoPE in place.  Restates src/kernels/rotary_embedding.cu:13-34 (pairs d and
+ * d + D/2, interleaved [pos][D/2][cos, sin] table rows of head_dim floats,
+ * q heads h < num_heads, k heads h < num_kv_heads) with pos = positions[t]
+ * (NULL: start_pos + t, the reference's form) clamped to [0, max_position).
+ * Each output is fmaf(x0, c, -(x1*s)) / fmaf(x0, s, x1*c) in fp32, rounded to
+ * src_dtype (F32/F16).  Pinned: numpy fp64 rotation of the same inputs,
+ * position 0 = identity, pair norms preserved, in tests. */
+void oracle_rope(void* query, void* key, int64_t query_stride, int64_t key_stride,
+                 const float* cos_sin, const int32_t* positions, int32_t start_pos,
+                 int32_t max_position, int32_t num_tokens, int32_t num_heads,
+                 int32_t num_kv_heads, int32_t head_dim, int32_t src_dtype);
+
 /* Paged decode.  Restates src/attention/paged_attention.cu:13-82: GQA map
  * h/(H/Hkv), ctx = min(context_lens[s], max_context_len), 32-lane strided
  * partial dots (fused multiply-add) reduced by the shfl_down 16..1 tree,

@@ -42,6 +42,8 @@ def load() -> ctypes.CDLL:
         lib.oracle_paged_decode.restype = None
         lib.oracle_paged_prefill.argtypes = [P, P, P, P, P, P, P, P, P, i32, i32, i32, i32, i32, i32, f32, i32, i32]
         lib.oracle_paged_prefill.restype = None
+        lib.oracle_rope.argtypes = [P, P, i64, i64, P, P, i32, i32, i32, i32, i32, i32, i32]
+        lib.oracle_rope.restype = None
         lib.oracle_copy_blocks.argtypes = [P, i32, i32, i32, P, i32]
         lib.oracle_copy_blocks.restype = None
         lib.oracle_swap_blocks.argtypes = [P, i32, i32, i32, P, i32, P, i32, i32]
@@ -97,6 +99,17 @@ def reshape_and_cache(key, value, key_cache, value_cache, slot_mapping, key_scal
     load().oracle_reshape_and_cache(_p(key), _p(value), 0, 0, _p(key_cache), _p(value_cache),
                                     _p(key_scales), _p(value_scales), _p(slot_mapping), T, Hkv, D, bs, N,
                                     dtype_code(key), dtype_code(key_cache))
+
+
+def rope(query, key, cos_sin, positions=None, start_pos=0):
+    """In place on query [T, H, D] and key [T, Hkv, D] (fp32 or fp16 bits as uint16);
+    cos_sin fp32 [P, D/2, 2]."""
+    T, H, D = query.shape
+    Hkv = key.shape[1]
+    cs = np.ascontiguousarray(cos_sin, dtype=np.float32)
+    pos = None if positions is None else np.ascontiguousarray(positions, dtype=np.int32)
+    load().oracle_rope(_p(query), _p(key), 0, 0, _p(cs), _p(pos), start_pos, cs.shape[0], T, H, Hkv, D,
+                       dtype_code(query))
 
 
 def paged_decode(query, key_cache, value_cache, block_tables, context_lens, scale, key_scales=None,

@@ -33,6 +33,7 @@ def test_struct_sizes_match_header_layout(vkv):
     assert ctypes.sizeof(vkv.AppendParams) == 9 * 8 + 7 * 4 + 4  # trailing pad to 8
     assert ctypes.sizeof(vkv.DecodeParams) == 8 * 8 + 8 + 14 * 4 + 8 + 8
     assert ctypes.sizeof(vkv.BlockPlane) == 24
+    assert ctypes.sizeof(vkv.RopeAppendParams) == 3 * 8 + 3 * 8 + 2 * 8 + 2 * 4 + 5 * 8 + 8 * 4
 
 
 def _decode_params(vkv, **over):
@@ -113,3 +114,27 @@ def test_copy_pairs_check(vkv):
     assert lib.vkv_check_block_pairs_host(bad.ctypes.data, 2, 8) == -2
     oob = np.array([[0, 8]], np.int32)
     assert lib.vkv_check_block_pairs_host(oob.ctypes.data, 1, 8) == -2
+
+
+def test_rope_argument_errors(vkv):
+    lib = vkv.load()
+    base = dict(query=16, key=16, value=16, cos_sin=16, max_position=100, key_cache=16, value_cache=16,
+                slot_mapping=16, num_tokens=4, num_heads=32, num_kv_heads=8, head_dim=128, block_size=16,
+                num_blocks=10, src_dtype=1, cache_dtype=1)
+
+    def call(**over):
+        p = vkv.RopeAppendParams(**{**base, **over})
+        return lib.vkv_rope_reshape_and_cache(ctypes.byref(p), None)
+
+    assert call(head_dim=96) == -3
+    assert call(cos_sin=0) == -1
+    assert call(max_position=0) == -2
+    assert call(cache_dtype=2) == -1              # FP8 needs scales
+    assert call(cache_dtype=0) == -3              # fp32 cache from fp16 source
+    assert call(query=24) == -5                   # misaligned
+    assert call(query_stride=100) == -2           # shorter than a token's heads
+    assert call(value=0) == -1                    # fused mode needs the value rows
+    assert call(num_tokens=0) == 0
+    # rope-only mode ignores the value and cache fields
+    p = vkv.RopeAppendParams(**{**base, "key_cache": 0, "value": 0, "slot_mapping": 0, "num_tokens": 0})
+    assert lib.vkv_rope_reshape_and_cache(ctypes.byref(p), None) == 0

@@ -6,6 +6,7 @@
 // split-K workspace used when the caller passes none.
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -163,6 +164,50 @@ int check_append(const vkv_append_params* p) {
     return VKV_OK;
 }
 
+int check_rope(const vkv_rope_append_params* p) {
+    if (!p) return fail(VKV_ERR_NULL, "vkv_rope_reshape_and_cache: params is NULL");
+    if (p->num_tokens < 0) return fail(VKV_ERR_SHAPE, "num_tokens < 0");
+    if (p->num_tokens == 0) return VKV_OK;
+    const bool fused = p->key_cache != nullptr;
+    if (!p->query || !p->key || !p->cos_sin || (fused && (!p->value || !p->value_cache || !p->slot_mapping)))
+        return fail(VKV_ERR_NULL, "vkv_rope_reshape_and_cache: a required pointer is NULL");
+    if (p->num_heads <= 0 || p->num_kv_heads <= 0 || p->max_position <= 0)
+        return fail(VKV_ERR_SHAPE, "num_heads, num_kv_heads and max_position must be > 0");
+    if (p->head_dim != 64 && p->head_dim != 128 && p->head_dim != 256)
+        return fail(VKV_ERR_UNSUPPORTED, "head_dim %d not built (64, 128, 256)", p->head_dim);
+    if (p->src_dtype != VKV_DTYPE_F32 && p->src_dtype != VKV_DTYPE_F16)
+        return fail(VKV_ERR_UNSUPPORTED, "src_dtype %d unsupported", p->src_dtype);
+    if (p->query_stride < 0 || p->key_stride < 0 || p->value_stride < 0) return fail(VKV_ERR_SHAPE, "negative stride");
+    const int seb = p->src_dtype == VKV_DTYPE_F32 ? 4 : 2;
+    const int64_t qrow = int64_t(p->num_heads) * p->head_dim, kvrow = int64_t(p->num_kv_heads) * p->head_dim;
+    const int64_t qs = p->query_stride ? p->query_stride : qrow;
+    const int64_t ks = p->key_stride ? p->key_stride : kvrow;
+    const int64_t vs = p->value_stride ? p->value_stride : kvrow;
+    if (qs < qrow || ks < kvrow || (fused && vs < kvrow))
+        return fail(VKV_ERR_SHAPE, "token stride smaller than the token's heads * head_dim");
+    uintptr_t bits = reinterpret_cast<uintptr_t>(p->query) | reinterpret_cast<uintptr_t>(p->key) |
+                     reinterpret_cast<uintptr_t>(p->cos_sin) | uintptr_t(qs * seb) | uintptr_t(ks * seb);
+    if (fused)
+        bits |= reinterpret_cast<uintptr_t>(p->value) | uintptr_t(vs * seb) |
+                reinterpret_cast<uintptr_t>(p->key_cache) | reinterpret_cast<uintptr_t>(p->value_cache);
+    if (bits & 15u) return fail(VKV_ERR_ALIGN, "query/key/value/cos_sin/caches and token strides must be 16-byte aligned");
+    if (!fused) return VKV_OK;
+    if (p->block_size <= 0 || p->num_blocks <= 0) return fail(VKV_ERR_SHAPE, "block_size and num_blocks must be > 0");
+    switch (p->cache_dtype) {
+        case VKV_DTYPE_F32:
+            if (p->src_dtype != VKV_DTYPE_F32) return fail(VKV_ERR_UNSUPPORTED, "fp32 cache needs fp32 source");
+            break;
+        case VKV_DTYPE_F16:
+            break;
+        case VKV_DTYPE_FP8_E4M3:
+            if (!p->key_scales || !p->value_scales) return fail(VKV_ERR_NULL, "FP8 cache needs scale arrays");
+            break;
+        default:
+            return fail(VKV_ERR_UNSUPPORTED, "cache_dtype %d unsupported", p->cache_dtype);
+    }
+    return VKV_OK;
+}
+
 int fill_planes(const vkv_block_plane* planes, int32_t num_planes, vkv::PlaneSet* out) {
     if (!planes) return fail(VKV_ERR_NULL, "planes is NULL");
     if (num_planes < 1 || num_planes > 4) return fail(VKV_ERR_SHAPE, "num_planes must be 1..4");
@@ -191,6 +236,28 @@ int vkv_reshape_and_cache(const vkv_append_params* p, vkv_stream_t stream) {
     int rc = check_append(p);
     if (rc != VKV_OK || p->num_tokens == 0) return rc;
     return after_launch(vkv::launch_append(p, reinterpret_cast<hipStream_t>(stream)), "vkv_reshape_and_cache");
+}
+
+int vkv_rope_reshape_and_cache(const vkv_rope_append_params* p, vkv_stream_t stream) {
+    int rc = check_rope(p);
+    if (rc != VKV_OK || p->num_tokens == 0) return rc;
+    return after_launch(vkv::launch_rope_append(p, reinterpret_cast<hipStream_t>(stream)),
+                        "vkv_rope_reshape_and_cache");
+}
+
+int vkv_rope_cos_sin_host(float theta, int32_t head_dim, int32_t max_position, float* cos_sin) {
+    if (!cos_sin) return fail(VKV_ERR_NULL, "vkv_rope_cos_sin_host: cos_sin is NULL");
+    if (head_dim <= 0 || head_dim % 2 || max_position < 0 || !(theta > 0.0f))
+        return fail(VKV_ERR_SHAPE, "vkv_rope_cos_sin_host: bad theta/head_dim/max_position");
+    const int half = head_dim / 2;
+    for (int32_t pos = 0; pos < max_position; ++pos) {
+        for (int d = 0; d < half; ++d) {
+            const float f = float(pos) / powf(theta, 2.0f * float(d) / float(head_dim));
+            cos_sin[int64_t(pos) * head_dim + 2 * d] = cosf(f);
+            cos_sin[int64_t(pos) * head_dim + 2 * d + 1] = sinf(f);
+        }
+    }
+    return VKV_OK;
 }
 
 int vkv_slot_mapping_host(const int32_t* block_table, int32_t table_len, int32_t block_size, int32_t context_len,

@@ -10,6 +10,7 @@
 namespace vkv {
 
 int launch_append(const vkv_append_params* p, hipStream_t st);
+int launch_rope_append(const vkv_rope_append_params* p, hipStream_t st);
 
 // Split-K decode: partition kernel + reduce kernel.  part_o / part_ml point into
 // a workspace of decode_workspace_bytes(); partition_size already normalised.

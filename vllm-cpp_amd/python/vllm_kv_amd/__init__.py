@@ -6,6 +6,7 @@ fallback: if the library is missing or no GPU is present the calls raise.
 
 Entry points and the reference interfaces they replace:
   reshape_and_cache  -> per-token cudaMemcpyAsync pair, src/layers/attention.cpp:84-102
+  rope_reshape_and_cache -> rope_forward (src/kernels/rotary_embedding.cu:37-45) + that append
   paged_decode       -> vllm::paged_attention_forward, src/attention/paged_attention.cu:85-93
   paged_prefill      -> token-by-token prefill through decode, src/core/engine.cpp:157-164
   copy_blocks / swap_blocks -> no reference counterpart (fork / offload)
@@ -33,7 +34,7 @@ EXPORTED = [
     "vkv_last_error", "vkv_abi_version", "vkv_reshape_and_cache", "vkv_slot_mapping_host",
     "vkv_paged_decode_workspace_size", "vkv_paged_decode", "vkv_paged_prefill",
     "vkv_copy_blocks", "vkv_check_block_pairs_host", "vkv_swap_host_block_bytes",
-    "vkv_swap_blocks",
+    "vkv_swap_blocks", "vkv_rope_reshape_and_cache", "vkv_rope_cos_sin_host",
 ]
 
 
@@ -54,6 +55,22 @@ class AppendParams(ctypes.Structure):
         ("head_dim", ctypes.c_int32), ("block_size", ctypes.c_int32),
         ("num_blocks", ctypes.c_int32), ("src_dtype", ctypes.c_int32),
         ("cache_dtype", ctypes.c_int32),
+    ]
+
+
+class RopeAppendParams(ctypes.Structure):
+    _fields_ = [
+        ("query", ctypes.c_void_p), ("key", ctypes.c_void_p), ("value", ctypes.c_void_p),
+        ("query_stride", ctypes.c_int64), ("key_stride", ctypes.c_int64), ("value_stride", ctypes.c_int64),
+        ("cos_sin", ctypes.c_void_p), ("positions", ctypes.c_void_p),
+        ("start_pos", ctypes.c_int32), ("max_position", ctypes.c_int32),
+        ("key_cache", ctypes.c_void_p), ("value_cache", ctypes.c_void_p),
+        ("key_scales", ctypes.c_void_p), ("value_scales", ctypes.c_void_p),
+        ("slot_mapping", ctypes.c_void_p),
+        ("num_tokens", ctypes.c_int32), ("num_heads", ctypes.c_int32),
+        ("num_kv_heads", ctypes.c_int32), ("head_dim", ctypes.c_int32),
+        ("block_size", ctypes.c_int32), ("num_blocks", ctypes.c_int32),
+        ("src_dtype", ctypes.c_int32), ("cache_dtype", ctypes.c_int32),
     ]
 
 
@@ -119,7 +136,8 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.vkv_last_error.restype = ctypes.c_char_p
     lib.vkv_abi_version.restype = ctypes.c_int
     for name, ptype in (("vkv_reshape_and_cache", AppendParams), ("vkv_paged_decode", DecodeParams),
-                        ("vkv_paged_prefill", PrefillParams)):
+                        ("vkv_paged_prefill", PrefillParams),
+                        ("vkv_rope_reshape_and_cache", RopeAppendParams)):
         f = getattr(lib, name)
         f.argtypes = [ctypes.POINTER(ptype), ctypes.c_void_p]
         f.restype = ctypes.c_int
@@ -128,6 +146,8 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.vkv_slot_mapping_host.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
                                           ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]
     lib.vkv_slot_mapping_host.restype = ctypes.c_int
+    lib.vkv_rope_cos_sin_host.argtypes = [ctypes.c_float, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]
+    lib.vkv_rope_cos_sin_host.restype = ctypes.c_int
     lib.vkv_copy_blocks.argtypes = [ctypes.POINTER(BlockPlane), ctypes.c_int32, ctypes.c_int32,
                                     ctypes.c_int32, ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p]
     lib.vkv_copy_blocks.restype = ctypes.c_int
@@ -197,6 +217,40 @@ def reshape_and_cache(key, value, key_cache, value_cache, slot_mapping,
         slot_mapping=_ptr(slot_mapping), num_tokens=T, num_kv_heads=Hkv, head_dim=D,
         block_size=bs, num_blocks=N, src_dtype=_dtype_code(key), cache_dtype=_dtype_code(key_cache))
     check(load().vkv_reshape_and_cache(ctypes.byref(p), _stream(stream)))
+
+
+def rope_cos_sin_host(theta: float, head_dim: int, max_position: int):
+    """The reference's RoPE table [max_position, head_dim/2, 2] fp32 (numpy), built by the library."""
+    import numpy as np
+    t = np.zeros((max_position, head_dim // 2, 2), np.float32)
+    check(load().vkv_rope_cos_sin_host(theta, head_dim, max_position, t.ctypes.data))
+    return t
+
+
+def rope_reshape_and_cache(query, key, value, cos_sin, positions=None, start_pos=0,
+                           key_cache=None, value_cache=None, slot_mapping=None,
+                           key_scales=None, value_scales=None, stream=None) -> None:
+    """query [T, H, D], key/value [T, Hkv, D] (f32 or f16); cos_sin [P, D/2, 2] fp32 on the GPU;
+    positions int32 [T] or None (start_pos + t).  With caches: query rotated in place, rotated
+    key and value stored through slot_mapping.  Without: query and key rotated in place."""
+    _require_cuda(query, key, value, cos_sin, positions, key_cache, value_cache, slot_mapping,
+                  key_scales, value_scales)
+    T, H, D = query.shape
+    Hkv = key.shape[1]
+    N = bs = 0
+    cache_dtype = DTYPE_F16
+    if key_cache is not None:
+        N, bs = key_cache.shape[0], key_cache.shape[1]
+        cache_dtype = _dtype_code(key_cache)
+    p = RopeAppendParams(
+        query=_ptr(query), key=_ptr(key), value=_ptr(value), query_stride=query.stride(0),
+        key_stride=key.stride(0), value_stride=0 if value is None else value.stride(0),
+        cos_sin=_ptr(cos_sin), positions=_ptr(positions), start_pos=start_pos,
+        max_position=cos_sin.shape[0], key_cache=_ptr(key_cache), value_cache=_ptr(value_cache),
+        key_scales=_ptr(key_scales), value_scales=_ptr(value_scales), slot_mapping=_ptr(slot_mapping),
+        num_tokens=T, num_heads=H, num_kv_heads=Hkv, head_dim=D, block_size=bs, num_blocks=N,
+        src_dtype=_dtype_code(query), cache_dtype=cache_dtype)
+    check(load().vkv_rope_reshape_and_cache(ctypes.byref(p), _stream(stream)))
 
 
 def decode_params(out, query, key_cache, value_cache, block_tables, context_lens, scale,
