@@ -26,3 +26,10 @@ def test_block_manager_cpp():
 def test_host_api_gpu():
     """KVCache / paged_attention_forward through the C++ API on the GPU."""
     _run("test_host_gpu", 120)
+
+
+@pytest.mark.gpu
+def test_attention_step_gpu():
+    """AttentionMetadata + PagedAttentionLayer (batched RoPE + append + attention of a
+    whole step) against the oracle's per-token restatement of the reference."""
+    _run("test_attention_step", 120)
