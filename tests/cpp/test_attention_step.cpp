@@ -56,70 +56,98 @@ float get(const std::vector<uint8_t>& buf, size_t i, vllm::KVDtype t) {
     return x;
 }
 
-void run_scenario(const Geometry& g, uint32_t seed) {
-    using vllm::KVDtype;
-    std::printf("  scenario H%d Hkv%d D%d bs%d io %zuB kv %zuB\n", g.H, g.Hkv, g.D, g.bs, eb(g.io), eb(g.kv));
-    const bool fp8 = g.kv == KVDtype::kFP8E4M3;
-    vllm::KVCache cache(g.L, g.N, g.bs, g.Hkv, g.D, nullptr, nullptr, g.kv);
-    vllm::BlockManager bm(g.bs, g.N, 0);
-    const int P = 256;  // RoPE positions
-    std::vector<float> cs(size_t(P) * g.D);
-    VLLM_KV_CHECK(vkv_rope_cos_sin_host(10000.0f, g.D, P, cs.data()));
-    float* dcs;
-    VLLM_HIP_CHECK(hipMalloc(&dcs, cs.size() * 4));
-    VLLM_HIP_CHECK(hipMemcpy(dcs, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
-    vllm::PagedAttentionLayer layer(g.H, g.Hkv, g.D, P);
-    layer.attach_rope_table(dcs, P);
-    const int max_mb = 8;
-    vllm::AttentionMetadata md(8, 128, max_mb, g.bs);
+// The GPU cache and layer plus a host mirror of every layer's cache bytes,
+// kept equal to the oracle's view of the same history.
+struct Harness {
+    Geometry g;
+    bool fp8;
+    vllm::KVCache cache;
+    vllm::BlockManager bm;
+    vllm::PagedAttentionLayer layer;
+    vllm::AttentionMetadata md;
+    static constexpr int P = 256;   // RoPE positions
+    static constexpr int MB = 8;    // block-table row length
+    static constexpr int MS = 8;    // sequences per step
+    std::vector<float> cs;
+    float* dcs = nullptr;
+    size_t row, layer_elems;
+    std::vector<std::vector<uint8_t>> hk, hv;
+    std::vector<std::vector<float>> hks, hvs;
+    std::mt19937 gen;
+    std::normal_distribution<float> nd{0.f, 0.6f};
 
-    // host mirror of both layers' caches
-    const size_t row = size_t(g.Hkv) * g.D;
-    const size_t layer_elems = size_t(g.N) * g.bs * row;
-    std::vector<std::vector<uint8_t>> hk(g.L), hv(g.L);
-    std::vector<std::vector<float>> hks(g.L), hvs(g.L);
-    for (int l = 0; l < g.L; ++l) {
-        hk[l].assign(layer_elems * eb(g.kv), 0);
-        hv[l].assign(layer_elems * eb(g.kv), 0);
-        if (fp8) {
-            hks[l].assign(size_t(g.N) * g.bs * g.Hkv, 0.f);
-            hvs[l].assign(size_t(g.N) * g.bs * g.Hkv, 0.f);
+    Harness(const Geometry& geo, uint32_t seed, int cpu_blocks = 0)
+        : g(geo),
+          fp8(geo.kv == vllm::KVDtype::kFP8E4M3),
+          cache(geo.L, geo.N, geo.bs, geo.Hkv, geo.D, nullptr, nullptr, geo.kv),
+          bm(geo.bs, geo.N, cpu_blocks),
+          layer(geo.H, geo.Hkv, geo.D, P),
+          md(MS, 128, MB, geo.bs),
+          cs(size_t(P) * geo.D),
+          gen(seed) {
+        std::printf("  scenario H%d Hkv%d D%d bs%d io %zuB kv %zuB\n", g.H, g.Hkv, g.D, g.bs, eb(g.io), eb(g.kv));
+        VLLM_KV_CHECK(vkv_rope_cos_sin_host(10000.0f, g.D, P, cs.data()));
+        VLLM_HIP_CHECK(hipMalloc(&dcs, cs.size() * 4));
+        VLLM_HIP_CHECK(hipMemcpy(dcs, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
+        layer.attach_rope_table(dcs, P);
+        row = size_t(g.Hkv) * g.D;
+        layer_elems = size_t(g.N) * g.bs * row;
+        hk.resize(g.L);
+        hv.resize(g.L);
+        hks.resize(g.L);
+        hvs.resize(g.L);
+        for (int l = 0; l < g.L; ++l) {
+            hk[l].assign(layer_elems * eb(g.kv), 0);
+            hv[l].assign(layer_elems * eb(g.kv), 0);
+            if (fp8) {
+                hks[l].assign(size_t(g.N) * g.bs * g.Hkv, 0.f);
+                hvs[l].assign(size_t(g.N) * g.bs * g.Hkv, 0.f);
+            }
+        }
+    }
+    ~Harness() { (void)hipFree(dcs); }
+
+    size_t block_elems() const { return size_t(g.bs) * row; }
+
+    // Host mirror of a device block move (copy-on-write or a swap round trip).
+    void mirror_copy(int32_t src, int32_t dst) {
+        const size_t be = block_elems() * eb(g.kv), se = size_t(g.bs) * g.Hkv;
+        for (int l = 0; l < g.L; ++l) {
+            std::memcpy(hk[l].data() + size_t(dst) * be, hk[l].data() + size_t(src) * be, be);
+            std::memcpy(hv[l].data() + size_t(dst) * be, hv[l].data() + size_t(src) * be, be);
+            if (fp8) {
+                std::memcpy(hks[l].data() + size_t(dst) * se, hks[l].data() + size_t(src) * se, se * 4);
+                std::memcpy(hvs[l].data() + size_t(dst) * se, hvs[l].data() + size_t(src) * se, se * 4);
+            }
         }
     }
 
-    std::vector<int> ctx = {0, 0, 0, 0};
-    std::vector<int> prompt = {5, 33, 1, 18};
-    std::vector<std::vector<int32_t>> tables(4);
-    for (int s = 0; s < 4; ++s) {
-        tables[s] = bm.allocate_for_sequence(size_t(prompt[s]));
-        CHECK(!tables[s].empty());
-    }
-    const std::vector<std::vector<int>> steps = {{5, 33, 1, 18}, {1, 1, 1, 1}, {1, 1, 1, 1}, {1, 7, 1, 1}};
-    std::mt19937 gen(seed);
-    std::normal_distribution<float> nd(0.f, 0.6f);
-    for (size_t step = 0; step < steps.size(); ++step) {
+    // One step: new[s] tokens for sequence s on top of ctx[s] cached ones;
+    // every layer runs and is checked against the oracle.
+    void step(const std::vector<std::vector<int32_t>*>& tables, const std::vector<int>& ctx, const std::vector<int>& nnew,
+              const char* what) {
+        using vllm::KVDtype;
+        const int S = int(tables.size());
         std::vector<vllm::StepSequence> ss;
         std::vector<int32_t> qsl = {0};
-        for (int s = 0; s < 4; ++s) {
-            const int n = steps[step][s];
-            CHECK(bm.ensure_sequence_capacity(tables[s], size_t(ctx[s] + n)));
-            ss.push_back({tables[s].data(), int32_t(tables[s].size()), ctx[s], n});
-            qsl.push_back(qsl.back() + n);
+        for (int s = 0; s < S; ++s) {
+            ss.push_back({tables[s]->data(), int32_t(tables[s]->size()), ctx[s], nnew[s]});
+            qsl.push_back(qsl.back() + nnew[s]);
         }
         const int T = qsl.back();
         md.build(ss, nullptr);
         CHECK_EQ(md.num_tokens(), T);
-        CHECK_EQ(md.max_query_len(), *std::max_element(steps[step].begin(), steps[step].end()));
-        std::vector<int32_t> slots(T), pos(T), cl(4);
-        for (int s = 0, t = 0; s < 4; ++s) {
-            for (int j = 0; j < steps[step][s]; ++j, ++t) {
+        CHECK_EQ(md.max_query_len(), *std::max_element(nnew.begin(), nnew.end()));
+        std::vector<int32_t> slots(T), pos(T), cl(S);
+        for (int s = 0, t = 0; s < S; ++s) {
+            for (int j = 0; j < nnew[s]; ++j, ++t) {
                 pos[t] = ctx[s] + j;
-                slots[t] = tables[s][pos[t] / g.bs] * g.bs + pos[t] % g.bs;  // attention.cpp:85-94
+                slots[t] = (*tables[s])[pos[t] / g.bs] * g.bs + pos[t] % g.bs;  // attention.cpp:85-94
             }
-            cl[s] = ctx[s] + steps[step][s];
+            cl[s] = ctx[s] + nnew[s];
         }
-        std::vector<int32_t> bt(4 * max_mb, 0);
-        for (int s = 0; s < 4; ++s) std::copy(tables[s].begin(), tables[s].end(), bt.begin() + s * max_mb);
+        std::vector<int32_t> bt(size_t(S) * MB, 0);
+        for (int s = 0; s < S; ++s) std::copy(tables[s]->begin(), tables[s]->end(), bt.begin() + s * MB);
 
         for (int l = 0; l < g.L; ++l) {
             std::vector<uint8_t> q(size_t(T) * g.H * g.D * eb(g.io)), k(size_t(T) * row * eb(g.io)),
@@ -147,8 +175,8 @@ void run_scenario(const Geometry& g, uint32_t seed) {
             std::vector<float> qf(size_t(T) * g.H * g.D), ref(qf.size());
             for (size_t i = 0; i < qf.size(); ++i) qf[i] = get(q, i, g.io);
             oracle_paged_prefill(ref.data(), qf.data(), hk[l].data(), hv[l].data(), fp8 ? hks[l].data() : nullptr,
-                                 fp8 ? hvs[l].data() : nullptr, bt.data(), cl.data(), qsl.data(), 4, g.H, g.Hkv, g.D,
-                                 g.bs, max_mb, 1.0f / std::sqrt(float(g.D)), int32_t(g.kv), 1);
+                                 fp8 ? hvs[l].data() : nullptr, bt.data(), cl.data(), qsl.data(), S, g.H, g.Hkv, g.D,
+                                 g.bs, MB, 1.0f / std::sqrt(float(g.D)), int32_t(g.kv), 1);
 
             std::vector<uint8_t> gq(q.size()), gout(q.size()), gk(hk[l].size()), gv(hv[l].size());
             VLLM_HIP_CHECK(hipMemcpy(gq.data(), dq, q.size(), hipMemcpyDeviceToHost));
@@ -171,16 +199,108 @@ void run_scenario(const Geometry& g, uint32_t seed) {
             double worst = 0;
             for (size_t i = 0; i < ref.size(); ++i)
                 worst = std::max(worst, std::fabs(double(get(gout, i, g.io)) - ref[i]) / (atol + rtol * std::fabs(ref[i])));
-            if (worst > 1.0) std::printf("    step %zu layer %d: worst error ratio %.3f\n", step, l, worst);
+            if (worst > 1.0) std::printf("    %s layer %d: worst error ratio %.3f\n", what, l, worst);
             CHECK(worst <= 1.0);
             (void)hipFree(dq);
             (void)hipFree(dk);
             (void)hipFree(dv);
             (void)hipFree(dout);
         }
-        for (int s = 0; s < 4; ++s) ctx[s] += steps[step][s];
     }
-    (void)hipFree(dcs);
+};
+
+void run_scenario(const Geometry& g, uint32_t seed) {
+    Harness h(g, seed);
+    std::vector<int> ctx = {0, 0, 0, 0};
+    std::vector<int> prompt = {5, 33, 1, 18};
+    std::vector<std::vector<int32_t>> tables(4);
+    for (int s = 0; s < 4; ++s) {
+        tables[s] = h.bm.allocate_for_sequence(size_t(prompt[s]));
+        CHECK(!tables[s].empty());
+    }
+    std::vector<std::vector<int32_t>*> tp = {&tables[0], &tables[1], &tables[2], &tables[3]};
+    const std::vector<std::vector<int>> steps = {{5, 33, 1, 18}, {1, 1, 1, 1}, {1, 1, 1, 1}, {1, 7, 1, 1}};
+    for (size_t st = 0; st < steps.size(); ++st) {
+        for (int s = 0; s < 4; ++s) CHECK(h.bm.ensure_sequence_capacity(tables[s], size_t(ctx[s] + steps[st][s])));
+        h.step(tp, ctx, steps[st], "step");
+        for (int s = 0; s < 4; ++s) ctx[s] += steps[st][s];
+    }
+}
+
+// Fork (copy-on-write through KVCache::copy_blocks) and preemption by swap
+// (KVCache::swap_blocks to pinned host memory and back into other block ids),
+// driven by BlockManager; attention stays equal to the oracle's on the
+// mirrored history throughout.
+void run_fork_swap_scenario(const Geometry& g, uint32_t seed) {
+    Harness h(g, seed, 16);
+    std::vector<int32_t> a = h.bm.allocate_for_sequence(20);  // 2 blocks, the second partial
+    std::vector<int> ctx = {0};
+    h.step({&a}, ctx, {20}, "prefill A");
+    std::vector<int32_t> b = h.bm.fork_sequence(a);  // B shares A's 20 tokens
+    CHECK_EQ(h.bm.ref_count(a[1]), 2);
+
+    // both append at position 20, inside the shared partial block
+    std::vector<int32_t> pairs;
+    CHECK(h.bm.make_writable(a, 20, pairs));
+    CHECK(h.bm.make_writable(b, 20, pairs));
+    CHECK_EQ(pairs.size(), 2u);  // only the first writer copies; B then owns the old block
+    CHECK(a[1] != b[1]);
+    int32_t* dpairs;
+    VLLM_HIP_CHECK(hipMalloc(&dpairs, pairs.size() * 4));
+    VLLM_HIP_CHECK(hipMemcpy(dpairs, pairs.data(), pairs.size() * 4, hipMemcpyHostToDevice));
+    h.cache.copy_blocks(dpairs, int32_t(pairs.size() / 2), nullptr);
+    h.mirror_copy(pairs[0], pairs[1]);
+    std::vector<int> c2 = {20, 20};
+    for (int i = 0; i < 3; ++i) {  // three decode steps of the two branches
+        CHECK(h.bm.ensure_sequence_capacity(a, size_t(c2[0] + 1)));
+        CHECK(h.bm.ensure_sequence_capacity(b, size_t(c2[1] + 1)));
+        h.step({&a, &b}, c2, {1, 1}, "fork decode");
+        c2[0] += 1;
+        c2[1] += 1;
+    }
+
+    // preempt A by swapping it out; B runs a 9-token chunk meanwhile (the
+    // freed ids are reused), then A comes back into fresh ids and decodes.
+    const size_t hbb = h.cache.host_block_bytes();
+    void* host = nullptr;
+    VLLM_HIP_CHECK(hipHostMalloc(&host, hbb * 16, hipHostMallocDefault));
+    std::vector<int32_t> out_pairs;
+    const std::vector<int32_t> a_gpu = a;
+    CHECK(h.bm.swap_out(a, out_pairs));
+    CHECK_EQ(out_pairs.size(), 2 * a_gpu.size());
+    int32_t* dswap;
+    VLLM_HIP_CHECK(hipMalloc(&dswap, out_pairs.size() * 4));
+    VLLM_HIP_CHECK(hipMemcpy(dswap, out_pairs.data(), out_pairs.size() * 4, hipMemcpyHostToDevice));
+    h.cache.swap_blocks(host, 16, dswap, int32_t(out_pairs.size() / 2), VKV_SWAP_OUT, nullptr);
+    VLLM_HIP_CHECK(hipDeviceSynchronize());
+    // host mirror: remember A's blocks by CPU id
+    std::vector<std::vector<uint8_t>> saved_k(a_gpu.size() * size_t(g.L)), saved_v(saved_k.size());
+    const size_t be = h.block_elems() * eb(g.kv);
+    for (size_t i = 0; i < a_gpu.size(); ++i)
+        for (int l = 0; l < g.L; ++l) {
+            const uint8_t* sk = h.hk[l].data() + size_t(a_gpu[i]) * be;
+            const uint8_t* sv = h.hv[l].data() + size_t(a_gpu[i]) * be;
+            saved_k[i * g.L + l].assign(sk, sk + be);
+            saved_v[i * g.L + l].assign(sv, sv + be);
+        }
+    CHECK(h.bm.ensure_sequence_capacity(b, size_t(c2[1] + 9)));
+    h.step({&b}, {c2[1]}, {9}, "chunk while A is swapped out");
+    c2[1] += 9;
+    std::vector<int32_t> in_pairs;
+    CHECK(h.bm.swap_in(a, in_pairs));
+    VLLM_HIP_CHECK(hipMemcpy(dswap, in_pairs.data(), in_pairs.size() * 4, hipMemcpyHostToDevice));
+    h.cache.swap_blocks(host, 16, dswap, int32_t(in_pairs.size() / 2), VKV_SWAP_IN, nullptr);
+    for (size_t i = 0; i < a.size(); ++i)
+        for (int l = 0; l < g.L; ++l) {
+            std::memcpy(h.hk[l].data() + size_t(a[i]) * be, saved_k[i * g.L + l].data(), be);
+            std::memcpy(h.hv[l].data() + size_t(a[i]) * be, saved_v[i * g.L + l].data(), be);
+        }
+    CHECK(h.bm.ensure_sequence_capacity(a, size_t(c2[0] + 1)));
+    CHECK(h.bm.ensure_sequence_capacity(b, size_t(c2[1] + 1)));
+    h.step({&a, &b}, c2, {1, 1}, "decode after swap-in");
+    (void)hipFree(dpairs);
+    (void)hipFree(dswap);
+    (void)hipHostFree(host);
 }
 
 }  // namespace
@@ -199,6 +319,10 @@ TEST_CASE(attention_step_f32_reference_types) {
 
 TEST_CASE(attention_step_f16_qwen7b_shape_bs32) {
     run_scenario({1, 24, 32, 28, 4, 128, vllm::KVDtype::kF16, vllm::KVDtype::kF16}, 4);
+}
+
+TEST_CASE(fork_copy_on_write_and_swap_f16) {
+    run_fork_swap_scenario({2, 24, 16, 14, 2, 64, vllm::KVDtype::kF16, vllm::KVDtype::kF16}, 5);
 }
 
 int main() { return check::run_all(); }

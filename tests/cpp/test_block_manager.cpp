@@ -126,4 +126,100 @@ TEST_CASE(out_of_range_ids_ignored) {
     CHECK(bm.find_prefix_blocks({1, 2, 3}, 4).empty());
 }
 
+// ---- sharing, copy-on-write, swap and the prefix cache (no reference counterpart)
+
+TEST_CASE(fork_shares_every_block) {
+    BlockManager bm(4, 8, 0);
+    auto parent = bm.allocate_for_sequence(10);  // 3 blocks: 7, 6, 5
+    auto child = bm.fork_sequence(parent);
+    CHECK(child == parent);
+    for (int32_t id : parent) CHECK_EQ(bm.ref_count(id), 2);
+    CHECK_EQ(bm.num_free_gpu_blocks(), 5u);
+    bm.free_sequence(parent);  // the child keeps them
+    for (int32_t id : child) CHECK_EQ(bm.ref_count(id), 1);
+    CHECK_EQ(bm.num_free_gpu_blocks(), 5u);
+}
+
+TEST_CASE(copy_on_write_of_the_shared_tail) {
+    BlockManager bm(4, 8, 0);
+    auto parent = bm.allocate_for_sequence(10);  // ids 7, 6, 5; tokens 8..9 in block 5
+    auto child = bm.fork_sequence(parent);
+    std::vector<int32_t> pairs;
+    CHECK(bm.make_writable(child, 10, pairs));   // token 10 goes into the shared block 5
+    CHECK_EQ(pairs.size(), 2u);
+    CHECK_EQ(pairs[0], 5);
+    CHECK_EQ(pairs[1], 4);                       // the next fresh id (LIFO)
+    CHECK_EQ(child[2], 4);
+    CHECK_EQ(parent[2], 5);
+    CHECK_EQ(bm.ref_count(5), 1);
+    CHECK_EQ(bm.ref_count(4), 1);
+    CHECK_EQ(bm.ref_count(7), 2);                // full blocks stay shared
+    pairs.clear();
+    CHECK(bm.make_writable(child, 11, pairs));   // now exclusive: no copy
+    CHECK(pairs.empty());
+    CHECK(!bm.make_writable(child, 12, pairs));  // past the table
+    // no free block: nothing changes
+    BlockManager small(4, 2, 0);
+    auto a = small.allocate_for_sequence(8);
+    auto b = small.fork_sequence(a);
+    CHECK(!small.make_writable(b, 5, pairs));
+    CHECK(b == a);
+    CHECK_EQ(small.ref_count(a[1]), 2);
+}
+
+TEST_CASE(swap_out_and_back_in) {
+    BlockManager bm(4, 6, 4);
+    auto seq = bm.allocate_for_sequence(12);  // gpu 5, 4, 3
+    auto other = bm.fork_sequence(seq);       // shared: swap-out drops one reference
+    std::vector<int32_t> pairs;
+    CHECK(bm.swap_out(seq, pairs));
+    CHECK_EQ(pairs.size(), 6u);
+    CHECK_EQ(pairs[0], 5);
+    CHECK_EQ(pairs[1], 3);  // cpu ids LIFO from 3
+    CHECK_EQ(pairs[3], 2);
+    CHECK_EQ(pairs[5], 1);
+    CHECK_EQ(seq[0], 3);
+    CHECK_EQ(bm.num_free_cpu_blocks(), 1u);
+    for (int32_t id : other) CHECK_EQ(bm.ref_count(id), 1);
+    bm.free_sequence(other);
+    CHECK_EQ(bm.num_free_gpu_blocks(), 6u);
+    std::vector<int32_t> back;
+    CHECK(bm.swap_in(seq, back));
+    CHECK_EQ(back.size(), 6u);
+    CHECK_EQ(back[0], 3);
+    CHECK_EQ(back[1], 3);   // gpu ids LIFO: 3 was freed last
+    CHECK_EQ(bm.num_free_cpu_blocks(), 4u);
+    CHECK_EQ(bm.num_free_gpu_blocks(), 3u);
+    // not enough CPU blocks: nothing changes
+    auto big = bm.allocate_for_sequence(12);
+    auto copy = big;
+    std::vector<int32_t> p2;
+    BlockManager tiny(4, 6, 2);
+    auto t = tiny.allocate_for_sequence(12);
+    auto t0 = t;
+    CHECK(!tiny.swap_out(t, p2));
+    CHECK(t == t0 && p2.empty());
+    CHECK(big == copy);
+}
+
+TEST_CASE(prefix_cache_hits_live_blocks_only) {
+    BlockManager bm(4, 8, 0);
+    std::vector<int32_t> tokens = {1, 2, 3, 4, 5, 6, 7, 8, 9, 10};
+    CHECK(bm.find_prefix_blocks(tokens, 8).empty());  // nothing registered: the reference's {}
+    auto table = bm.allocate_for_sequence(tokens.size());
+    bm.cache_prefix_blocks(tokens, table);            // 2 full blocks registered
+    std::vector<int32_t> same = {1, 2, 3, 4, 5, 6, 7, 8, 42};
+    auto hit = bm.find_prefix_blocks(same, 8);
+    CHECK_EQ(hit.size(), 2u);
+    CHECK_EQ(hit[0], table[0]);
+    CHECK_EQ(hit[1], table[1]);
+    CHECK_EQ(bm.find_prefix_blocks(same, 1).size(), 1u);
+    std::vector<int32_t> diverge = {1, 2, 3, 4, 5, 6, 0, 8};
+    CHECK_EQ(bm.find_prefix_blocks(diverge, 8).size(), 1u);
+    std::vector<int32_t> shifted = {5, 6, 7, 8};      // same block content, other parent
+    CHECK(bm.find_prefix_blocks(shifted, 8).empty());
+    bm.free_sequence(table);                          // freed blocks leave the cache
+    CHECK(bm.find_prefix_blocks(same, 8).empty());
+}
+
 int main() { return check::run_all(); }
