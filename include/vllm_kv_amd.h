@@ -100,6 +100,21 @@ int vkv_reshape_and_cache(const vkv_append_params* p, vkv_stream_t stream);
 int vkv_slot_mapping_host(const int32_t* block_table, int32_t table_len, int32_t block_size,
                           int32_t context_len, int32_t num_tokens, int32_t* slot_mapping);
 
+/* Host helpers for sizing the KV pool with its element type.  The reference
+ * sizes the pool in src/model/qwen.cpp:72-73 and 94-104 with sizeof(float)
+ * hard-coded: kv_bytes_per_block = 2 * block_size * num_kv_heads * head_dim *
+ * 4 * num_layers, and num_blocks = min(max_num_seqs * ceil(max_model_len /
+ * block_size), (budget - non_kv) / kv_bytes_per_block).
+ * vkv_kv_block_bytes is that per-block figure for kv_dtype (FP8 adds its two
+ * fp32 scales per slot and kv head); vkv_kv_pool_num_blocks is the block count
+ * (0 when budget_bytes <= non_kv_bytes, as the reference then refuses to
+ * start).  Negative VKV_ERR_SHAPE / VKV_ERR_UNSUPPORTED on bad arguments. */
+int64_t vkv_kv_block_bytes(int32_t num_layers, int32_t block_size, int32_t num_kv_heads, int32_t head_dim,
+                           int32_t kv_dtype);
+int64_t vkv_kv_pool_num_blocks(uint64_t budget_bytes, uint64_t non_kv_bytes, int32_t num_layers, int32_t block_size,
+                               int32_t num_kv_heads, int32_t head_dim, int32_t kv_dtype, int32_t max_num_seqs,
+                               int32_t max_model_len);
+
 /* -------------------------------------------------------------------------
  * Rotary position embedding fused with the KV append.
  *

@@ -138,3 +138,26 @@ def test_rope_argument_errors(vkv):
     # rope-only mode ignores the value and cache fields
     p = vkv.RopeAppendParams(**{**base, "key_cache": 0, "value": 0, "slot_mapping": 0, "num_tokens": 0})
     assert lib.vkv_rope_reshape_and_cache(ctypes.byref(p), None) == 0
+
+
+def test_kv_pool_sizing_with_element_type(vkv):
+    """src/model/qwen.cpp:72-73,94-104 restated: fp32 equals the reference's formula exactly;
+    fp16 / FP8 use their element bytes (FP8 + one fp32 scale per slot and kv head)."""
+    L, bs, Hkv, D = 32, 16, 8, 128
+    ref_per_block = 2 * bs * Hkv * D * 4 * L  # sizeof(float) in the reference
+    assert vkv.kv_block_bytes(L, bs, Hkv, D, vkv.DTYPE_F32) == ref_per_block
+    assert vkv.kv_block_bytes(L, bs, Hkv, D, vkv.DTYPE_F16) == ref_per_block // 2
+    assert vkv.kv_block_bytes(L, bs, Hkv, D, vkv.DTYPE_FP8) == 2 * bs * Hkv * (D + 4) * L
+    budget, non_kv = 250 * 2**30, 20 * 2**30
+    for dt in (vkv.DTYPE_F32, vkv.DTYPE_F16, vkv.DTYPE_FP8):
+        per = vkv.kv_block_bytes(L, bs, Hkv, D, dt)
+        want = min(256 * ((32768 + bs - 1) // bs), (budget - non_kv) // per)
+        assert vkv.kv_pool_num_blocks(budget, non_kv, L, bs, Hkv, D, dt, 256, 32768) == want
+    f32 = vkv.kv_pool_num_blocks(budget, non_kv, L, bs, Hkv, D, vkv.DTYPE_F32, 10**6, 10**6)
+    f16 = vkv.kv_pool_num_blocks(budget, non_kv, L, bs, Hkv, D, vkv.DTYPE_F16, 10**6, 10**6)
+    fp8 = vkv.kv_pool_num_blocks(budget, non_kv, L, bs, Hkv, D, vkv.DTYPE_FP8, 10**6, 10**6)
+    assert f16 in (2 * f32, 2 * f32 + 1) and 3.8 * f32 < fp8 < 4 * f32 + 4
+    assert vkv.kv_pool_num_blocks(non_kv, non_kv, L, bs, Hkv, D, vkv.DTYPE_F16, 8, 4096) == 0
+    assert vkv.kv_pool_num_blocks(budget, non_kv, L, bs, Hkv, D, vkv.DTYPE_F16, 2, 100) == 2 * 7
+    with pytest.raises(vkv.VkvError):
+        vkv.kv_block_bytes(L, bs, Hkv, D, 7)

@@ -238,6 +238,34 @@ int vkv_reshape_and_cache(const vkv_append_params* p, vkv_stream_t stream) {
     return after_launch(vkv::launch_append(p, reinterpret_cast<hipStream_t>(stream)), "vkv_reshape_and_cache");
 }
 
+int64_t vkv_kv_block_bytes(int32_t num_layers, int32_t block_size, int32_t num_kv_heads, int32_t head_dim,
+                           int32_t kv_dtype) {
+    if (num_layers <= 0 || block_size <= 0 || num_kv_heads <= 0 || head_dim <= 0)
+        return fail(VKV_ERR_SHAPE, "vkv_kv_block_bytes: sizes must be > 0");
+    int64_t per_slot_head;  // bytes of one (slot, kv head) for K or V
+    switch (kv_dtype) {
+        case VKV_DTYPE_F32: per_slot_head = int64_t(head_dim) * 4; break;
+        case VKV_DTYPE_F16: per_slot_head = int64_t(head_dim) * 2; break;
+        case VKV_DTYPE_FP8_E4M3: per_slot_head = int64_t(head_dim) + 4; break;  // codes + scale
+        default: return fail(VKV_ERR_UNSUPPORTED, "vkv_kv_block_bytes: kv_dtype %d", kv_dtype);
+    }
+    return 2 * int64_t(block_size) * num_kv_heads * per_slot_head * num_layers;
+}
+
+int64_t vkv_kv_pool_num_blocks(uint64_t budget_bytes, uint64_t non_kv_bytes, int32_t num_layers, int32_t block_size,
+                               int32_t num_kv_heads, int32_t head_dim, int32_t kv_dtype, int32_t max_num_seqs,
+                               int32_t max_model_len) {
+    const int64_t per_block = vkv_kv_block_bytes(num_layers, block_size, num_kv_heads, head_dim, kv_dtype);
+    if (per_block < 0) return per_block;
+    if (max_num_seqs <= 0 || max_model_len <= 0)
+        return fail(VKV_ERR_SHAPE, "vkv_kv_pool_num_blocks: max_num_seqs and max_model_len must be > 0");
+    if (budget_bytes <= non_kv_bytes) return 0;
+    const int64_t per_seq = (int64_t(max_model_len) + block_size - 1) / block_size;
+    const int64_t by_seqs = per_seq * max_num_seqs;
+    const int64_t by_memory = int64_t((budget_bytes - non_kv_bytes) / uint64_t(per_block));
+    return by_seqs < by_memory ? by_seqs : by_memory;
+}
+
 int vkv_rope_reshape_and_cache(const vkv_rope_append_params* p, vkv_stream_t stream) {
     int rc = check_rope(p);
     if (rc != VKV_OK || p->num_tokens == 0) return rc;

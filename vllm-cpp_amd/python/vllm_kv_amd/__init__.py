@@ -35,6 +35,7 @@ EXPORTED = [
     "vkv_paged_decode_workspace_size", "vkv_paged_decode", "vkv_paged_prefill",
     "vkv_copy_blocks", "vkv_check_block_pairs_host", "vkv_swap_host_block_bytes",
     "vkv_swap_blocks", "vkv_rope_reshape_and_cache", "vkv_rope_cos_sin_host",
+    "vkv_kv_block_bytes", "vkv_kv_pool_num_blocks",
 ]
 
 
@@ -148,6 +149,11 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.vkv_slot_mapping_host.restype = ctypes.c_int
     lib.vkv_rope_cos_sin_host.argtypes = [ctypes.c_float, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]
     lib.vkv_rope_cos_sin_host.restype = ctypes.c_int
+    i32 = ctypes.c_int32
+    lib.vkv_kv_block_bytes.argtypes = [i32, i32, i32, i32, i32]
+    lib.vkv_kv_block_bytes.restype = ctypes.c_int64
+    lib.vkv_kv_pool_num_blocks.argtypes = [ctypes.c_uint64, ctypes.c_uint64, i32, i32, i32, i32, i32, i32, i32]
+    lib.vkv_kv_pool_num_blocks.restype = ctypes.c_int64
     lib.vkv_copy_blocks.argtypes = [ctypes.POINTER(BlockPlane), ctypes.c_int32, ctypes.c_int32,
                                     ctypes.c_int32, ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p]
     lib.vkv_copy_blocks.restype = ctypes.c_int
@@ -217,6 +223,24 @@ def reshape_and_cache(key, value, key_cache, value_cache, slot_mapping,
         slot_mapping=_ptr(slot_mapping), num_tokens=T, num_kv_heads=Hkv, head_dim=D,
         block_size=bs, num_blocks=N, src_dtype=_dtype_code(key), cache_dtype=_dtype_code(key_cache))
     check(load().vkv_reshape_and_cache(ctypes.byref(p), _stream(stream)))
+
+
+def kv_pool_num_blocks(budget_bytes: int, non_kv_bytes: int, num_layers: int, block_size: int,
+                       num_kv_heads: int, head_dim: int, kv_dtype: int, max_num_seqs: int,
+                       max_model_len: int) -> int:
+    """KV blocks that fit the budget (the reference's pool sizing with the element type)."""
+    n = load().vkv_kv_pool_num_blocks(budget_bytes, non_kv_bytes, num_layers, block_size, num_kv_heads,
+                                      head_dim, kv_dtype, max_num_seqs, max_model_len)
+    if n < 0:
+        check(int(n))
+    return int(n)
+
+
+def kv_block_bytes(num_layers: int, block_size: int, num_kv_heads: int, head_dim: int, kv_dtype: int) -> int:
+    n = load().vkv_kv_block_bytes(num_layers, block_size, num_kv_heads, head_dim, kv_dtype)
+    if n < 0:
+        check(int(n))
+    return int(n)
 
 
 def rope_cos_sin_host(theta: float, head_dim: int, max_position: int):
