@@ -84,3 +84,60 @@ def test_prefill_f32_rows(vkv, oracle, cuda):
                       to_dev(ctx, cuda), to_dev(qsl, cuda), 20, scale)
     torch.cuda.synchronize()
     assert_close(to_np(out), ref, F32_ATOL, F32_RTOL, "fp32 prefill")
+
+
+@pytest.mark.parametrize("kvt", ["f16", "fp8"])
+def test_prefill_growing_logits(vkv, oracle, cuda, kvt):
+    """Large logits whose running maximum keeps growing along the keys (key norms
+    ramp up with position): every rescale of the online softmax, and the
+    cross-lane row maximum, must be right for the weights to stay finite."""
+    import torch
+    rng = np.random.default_rng(31)
+    H, Hkv, D, bs = 28, 4, 128, 16
+    q_lens = np.array([96, 40], np.int32)
+    prior = np.array([700, 130], np.int32)
+    ctx = prior + q_lens
+    from vllm_kv_amd import workloads
+    lay = workloads.make_layout(ctx, bs, rng, slack=0.2)
+    N = lay.num_blocks
+    k = rng.standard_normal((N, bs, Hkv, D), dtype=np.float32)
+    v = rng.standard_normal((N, bs, Hkv, D), dtype=np.float32)
+    # key norm grows with the token's position in its sequence: logits up to ~150
+    for s in range(len(ctx)):
+        for t in range(int(ctx[s])):
+            blk = lay.block_tables[s, t // bs]
+            k[blk, t % bs] *= 0.2 + 2.5 * t / int(ctx[s])
+    k, v = k.astype(np.float16), v.astype(np.float16)
+    qsl = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    q = rng.standard_normal((int(qsl[-1]), H, D)).astype(np.float16)
+    scale = 0.35
+    tq = to_dev(q, cuda)
+    if kvt == "f16":
+        kc, vc, ks, vs = to_dev(k, cuda), to_dev(v, cuda), None, None
+        hk, hv, hks, hvs = k.view(np.uint16), v.view(np.uint16), None, None
+    else:
+        kc = torch.zeros((N, bs, Hkv, D), dtype=torch.uint8, device=cuda)
+        vc = torch.zeros_like(kc)
+        ks = torch.zeros((N, bs, Hkv), dtype=torch.float32, device=cuda)
+        vs = torch.zeros_like(ks)
+        slots = to_dev(np.arange(N * bs, dtype=np.int32), cuda)
+        vkv.reshape_and_cache(to_dev(k.reshape(-1, Hkv, D), cuda), to_dev(v.reshape(-1, Hkv, D), cuda), kc, vc,
+                              slots, ks, vs)
+        torch.cuda.synchronize()
+        hk, hv, hks, hvs = to_np(kc), to_np(vc), to_np(ks), to_np(vs)
+    out = torch.zeros((q.shape[0], H, D), dtype=torch.float16, device=cuda)
+    vkv.paged_prefill(out, tq, kc, vc, to_dev(lay.block_tables, cuda), to_dev(ctx, cuda), to_dev(qsl, cuda),
+                      int(q_lens.max()), scale, key_scales=ks, value_scales=vs)
+    torch.cuda.synchronize()
+    ref = oracle.paged_prefill(q.astype(np.float32), hk, hv, lay.block_tables, ctx, qsl, scale,
+                               key_scales=hks, value_scales=hvs)
+    got = to_np(out).astype(np.float32)
+    assert np.isfinite(got).all()
+    if kvt == "f16":
+        assert_close(got, ref, F16_ATOL, F16_RTOL, "prefill with growing logits")
+    else:
+        # The kernel stages dequantised keys as fp16 (2^-12 relative), which at
+        # logits near 50 moves single weights by about 1 %: held to the FP8
+        # contract (3e-2 relative) per output row instead of element-wise.
+        err = np.linalg.norm(got - ref, axis=-1) / np.maximum(np.linalg.norm(ref, axis=-1), 1e-6)
+        assert err.max() <= 3e-2, f"FP8 prefill with growing logits: row error {err.max():.3e}"

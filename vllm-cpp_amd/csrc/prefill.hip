@@ -81,19 +81,34 @@ struct Stage {
     static constexpr int UPT = UNITS / (64 * kMinWaves);  // units per staging thread
     static constexpr int STR = D * 2 + 16;            // bytes per K or V row in LDS
     static_assert(UNITS % (64 * kMinWaves) == 0, "a tile must split evenly over 256 threads");
+    // fp16: the 16 loaded bytes; FP8: 8 code bytes in .xy and the token's scale
+    // (bits) in .z, dequantised only when written to LDS so that the loads stay
+    // in flight while the current tile is computed.
     u32x4 k[UPT];
     u32x4 v[UPT];
 };
 
-// Eight fp16 values of one token: fp16 cache bytes as they are, FP8 codes
-// dequantised with the token's scale (code * scale in fp32, rounded to fp16).
+// Eight elements of one token as loaded: 16 fp16 bytes, or 8 FP8 code bytes
+// with the token's scale beside them.
 template <int KVT>
-__device__ __forceinline__ u32x4 load8(const char* p, float scale) {
+__device__ __forceinline__ u32x4 load8(const char* p, const float* scale) {
     if constexpr (KVT == kF16) {
         return load16_nt(p);
     } else {
         const u32x2 w = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
-        const float sc = scale * kFp8HalfScale;
+        return u32x4{w[0], w[1], __builtin_bit_cast(uint32_t, *scale), 0u};
+    }
+}
+
+// Eight fp16 values for LDS: fp16 bytes as they are, FP8 codes dequantised with
+// the token's scale (code * scale in fp32, rounded to fp16).
+template <int KVT>
+__device__ __forceinline__ u32x4 to_half8(u32x4 raw) {
+    if constexpr (KVT == kF16) {
+        return raw;
+    } else {
+        const u32x2 w = {raw[0], raw[1]};
+        const float sc = as_f32(raw[2]) * kFp8HalfScale;
         u32x4 r;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
@@ -111,6 +126,19 @@ __device__ __forceinline__ u32x4 load8(const char* p, float scale) {
     }
 }
 
+// Max over lanes l, l ^ 16, l ^ 32, l ^ 48 (the four key groups of one query
+// row): gfx950's permlane swaps exchange rows of 16 lanes (xor 16) and wave
+// halves (xor 32) on the VALU; swapping a value with itself leaves both
+// partners' values, one in each result.
+__device__ __forceinline__ float row_group_max(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(as_u32(x), as_u32(x), false, false);
+    x = fmaxf(as_f32(a[0]), as_f32(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(as_u32(x), as_u32(x), false, false);
+    return fmaxf(as_f32(b[0]), as_f32(b[1]));
+}
+
+constexpr float kLazy = 8.0f;  // rescale threshold of the running max, log2 units
+
 // ds_read_b64_tr_b16: 8 bytes per lane, transposed across 16-lane groups.
 __device__ __forceinline__ u32x2 tr_read(const char* lds) {
     typedef __fp16 fp16x4_t __attribute__((__vector_size__(4 * sizeof(__fp16))));
@@ -124,6 +152,7 @@ __device__ __forceinline__ void prefill_block(const PrefillArgs& a, const int s,
                                               char* klds, char* vlds, int* btc) {
     using St = Stage<D, KVT>;
     constexpr int EB = St::EB;
+    constexpr int kTileBytes = kBK * St::STR;  // one K (or V) tile buffer in LDS
     constexpr int DT = D / 16;  // output dim tiles
     constexpr int KS = D / 32;  // MFMA k-steps of Q K^T
 
@@ -201,41 +230,40 @@ __device__ __forceinline__ void prefill_block(const PrefillArgs& a, const int s,
         const int blk = btc[(k >> a.bs_log2) - win];
         return ((int64_t(blk) << a.bs_log2) + (k & bs_mask)) * row_bytes + int64_t(kvh) * D * EB;
     };
-    auto token_scale = [&](const float* scales, int k) __attribute__((always_inline)) {
-        if constexpr (KVT == kFp8) {
-            const int blk = btc[(k >> a.bs_log2) - win];
-            return scales[((int64_t(blk) << a.bs_log2) + (k & bs_mask)) * a.num_kv_heads + kvh];
-        } else {
-            return 1.0f;
-        }
-    };
+    // Keys past kend (the tail of the last tile) load the row of key kend - 1
+    // instead: every query row masks them, so no branch is needed around the
+    // loads and they all issue back to back.
     auto fetch = [&](St& st, int k0) __attribute__((always_inline)) {
+        int64_t off[St::UPT];
 #pragma unroll
         for (int i = 0; i < St::UPT; ++i) {
             const int u = tid + i * 64 * kMinWaves;
-            const int k = k0 + u / St::COLS;
-            const int c = u % St::COLS;
-            u32x4 wk = {0u, 0u, 0u, 0u}, wv = {0u, 0u, 0u, 0u};
-            if (k < kend) {
-                const int64_t off = token_off(k) + c * 8 * EB;
-                wk = load8<KVT>(a.kc + off, token_scale(a.ks, k));
-                wv = load8<KVT>(a.vc + off, token_scale(a.vs, k));
-            }
-            st.k[i] = wk;
-            st.v[i] = wv;
+            int k = k0 + u / St::COLS;
+            k = k < kend ? k : kend - 1;
+            const int blk = btc[(k >> a.bs_log2) - win];
+            off[i] = ((int64_t(blk) << a.bs_log2) + (k & bs_mask));  // slot
+        }
+#pragma unroll
+        for (int i = 0; i < St::UPT; ++i) {
+            const int c = (tid + i * 64 * kMinWaves) % St::COLS;
+            const int64_t bytes = off[i] * row_bytes + int64_t(kvh) * D * EB + c * 8 * EB;
+            const int64_t sidx = off[i] * a.num_kv_heads + kvh;
+            st.k[i] = load8<KVT>(a.kc + bytes, KVT == kFp8 ? a.ks + sidx : nullptr);
+            st.v[i] = load8<KVT>(a.vc + bytes, KVT == kFp8 ? a.vs + sidx : nullptr);
         }
     };
-    auto put = [&](const St& st) __attribute__((always_inline)) {
+    auto put = [&](const St& st, char* kbuf, char* vbuf) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < St::UPT; ++i) {
             const int u = tid + i * 64 * kMinWaves;
             const int off = (u / St::COLS) * St::STR + (u % St::COLS) * 16;
-            store16(klds + off, st.k[i]);
-            store16(vlds + off, st.v[i]);
+            store16(kbuf + off, to_half8<KVT>(st.k[i]));
+            store16(vbuf + off, to_half8<KVT>(st.v[i]));
         }
     };
 
     // ---------------- main loop
+    const float lazy = kLazy / sc;  // kLazy in raw (unscaled) logit units
     float m[kRT];
     float4_t lsum[kRT];  // row sums (every element the same), see below
     float4_t o[kRT][DT];
@@ -248,17 +276,28 @@ __device__ __forceinline__ void prefill_block(const PrefillArgs& a, const int s,
         for (int t = 0; t < DT; ++t) o[r][t] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
     }
 
-    // One staging set: tile kt's registers go to LDS, then are refilled with
-    // tile kt + 1 while tile kt is computed in two 32-key steps.
+    // Two LDS tile buffers and one staging register set: tile kt is computed
+    // from buffer kt & 1 while the registers (tile kt + 1, loaded during the
+    // previous tile) go to the other buffer and are refilled with tile kt + 2.
+    // One barrier per tile: it publishes buffer (kt + 1) & 1, and every wave
+    // has left tile kt - 1 (the previous user of that buffer) before it.
     St st;
     const bool stager = tid < 64 * kMinWaves;
     if (ntiles > 0) {
         ensure_window(0);
-        if (stager) fetch(st, 0);
+        if (stager) {
+            fetch(st, 0);
+            put(st, klds, vlds);
+        }
+        if (ntiles > 1) {
+            ensure_window(kBK >> a.bs_log2);
+            if (stager) fetch(st, kBK);
+        }
+        __syncthreads();
     }
     // One 32-key step in three parts, so that a tile's second S^T (matrix
     // pipe) is issued before the first step's softmax (VALU) and overlaps it.
-    auto qk = [&](const int sub, float4_t (&sv)[kRT][2]) __attribute__((always_inline)) {
+    auto qk = [&](const char* kb, const int sub, float4_t (&sv)[kRT][2]) __attribute__((always_inline)) {
         // S^T of both row tiles; each K operand (one LDS read) feeds both.
 #pragma unroll
         for (int r = 0; r < kRT; ++r) sv[r][0] = sv[r][1] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
@@ -267,7 +306,7 @@ __device__ __forceinline__ void prefill_block(const PrefillArgs& a, const int s,
 #pragma unroll
             for (int i = 0; i < KS; ++i) {
                 const half8_t kop = __builtin_bit_cast(
-                    half8_t, *reinterpret_cast<const u32x4*>(klds + (32 * sub + 16 * hh + col) * St::STR + (32 * i + 8 * grp) * 2));
+                    half8_t, *reinterpret_cast<const u32x4*>(kb + (32 * sub + 16 * hh + col) * St::STR + (32 * i + 8 * grp) * 2));
 #pragma unroll
                 for (int r = 0; r < kRT; ++r)
                     sv[r][hh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qop[r][i], sv[r][hh], 0, 0, 0);
@@ -291,10 +330,12 @@ __device__ __forceinline__ void prefill_block(const PrefillArgs& a, const int s,
                         if (kbase + 16 * hh + 4 * grp + e >= rctx[r]) x[4 * hh + e] = -INFINITY;
             }
             float mx = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
-            mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-            // rescale only when some row's max grows (each lane owns its row)
-            if (__builtin_amdgcn_ballot_w64(mx > m[r])) {
+            mx = row_group_max(mx);
+            // Rescale only when some row's max exceeds the one in use by more
+            // than kLazy (log2 units): below that the weights exp2((x - m) sc)
+            // stay under 2^kLazy, well inside fp16 for P and fp32 for the sums,
+            // and the result is the same softmax.  The first key always sets m.
+            if (__builtin_amdgcn_ballot_w64(mx > m[r] + lazy)) {
                 const float mn = fmaxf(m[r], mx);
                 const float alpha = mn > m[r] ? __builtin_amdgcn_exp2f((m[r] - mn) * sc) : 1.0f;
                 m[r] = mn;
@@ -311,7 +352,7 @@ __device__ __forceinline__ void prefill_block(const PrefillArgs& a, const int s,
             lsum[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kOnes, pop[r], lsum[r], 0, 0, 0);
         }
     };
-    auto pv = [&](const int sub, const half8_t (&pop)[kRT]) __attribute__((always_inline)) {
+    auto pv = [&](const char* vb, const int sub, const half8_t (&pop)[kRT]) __attribute__((always_inline)) {
         // O^T += V^T P^T; each V^T operand (two transpose reads of row-major V:
         // within each 16-lane group, lane i receives element i % 4 of the 8-byte
         // chunks addressed by lanes i / 4 + 4 e, e = 0..3, so lane m of group
@@ -321,8 +362,8 @@ __device__ __forceinline__ void prefill_block(const PrefillArgs& a, const int s,
 #pragma unroll
         for (int t = 0; t < DT; ++t) {
             const int dcol = (16 * t + 4 * (col & 3)) * 2;
-            const u32x2 lo = tr_read(vlds + vrow * St::STR + dcol);
-            const u32x2 hi = tr_read(vlds + (16 + vrow) * St::STR + dcol);
+            const u32x2 lo = tr_read(vb + vrow * St::STR + dcol);
+            const u32x2 hi = tr_read(vb + (16 + vrow) * St::STR + dcol);
             const half8_t vop = __builtin_bit_cast(half8_t, u32x4{lo[0], lo[1], hi[0], hi[1]});
 #pragma unroll
             for (int r = 0; r < kRT; ++r) o[r][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, pop[r], o[r][t], 0, 0, 0);
@@ -330,27 +371,31 @@ __device__ __forceinline__ void prefill_block(const PrefillArgs& a, const int s,
     };
     static_assert(kBK == 64, "the tile loop below computes two 32-key steps");
     for (int kt = 0; kt < ntiles; ++kt) {
-        if (stager) put(st);
-        __syncthreads();
-        if (kt + 1 < ntiles) {
-            ensure_window(((kt + 1) * kBK) >> a.bs_log2);
-            if (stager) fetch(st, (kt + 1) * kBK);
-        }
+        const char* kcur = klds + (kt & 1) * kTileBytes;
+        const char* vcur = vlds + (kt & 1) * kTileBytes;
         if (computes) {
             const bool second = kt * kBK + 32 < kend;
             float4_t sa[kRT][2], sb[kRT][2];
             half8_t pa[kRT], pb[kRT];
-            qk(0, sa);
-            if (second) qk(1, sb);
+            qk(kcur, 0, sa);
+            if (second) qk(kcur, 1, sb);
             softmax(kt * kBK, sa, pa);
-            pv(0, pa);
+            pv(vcur, 0, pa);
             if (second) {
                 softmax(kt * kBK + 32, sb, pb);
-                pv(1, pb);
+                pv(vcur, 1, pb);
             }
         }
-        __syncthreads();
+        if (kt + 1 < ntiles) {
+            if (stager) put(st, klds + ((kt + 1) & 1) * kTileBytes, vlds + ((kt + 1) & 1) * kTileBytes);
+            __syncthreads();
+            if (kt + 2 < ntiles) {
+                ensure_window(((kt + 2) * kBK) >> a.bs_log2);
+                if (stager) fetch(st, (kt + 2) * kBK);
+            }
+        }
     }
+    __syncthreads();  // LDS is free for the next item
 
     // ---------------- output: lane (row col) holds dims 16 t + 4 grp + e
     if (!computes) return;  // (after the loop's last barrier)
@@ -379,8 +424,8 @@ __device__ __forceinline__ void prefill_block(const PrefillArgs& a, const int s,
 template <int D, int KVT>
 __global__ __launch_bounds__(64 * kMaxWaves) void prefill_mfma_kernel(PrefillArgs a) {
     using St = Stage<D, KVT>;
-    __shared__ __attribute__((aligned(16))) char klds[kBK * St::STR];
-    __shared__ __attribute__((aligned(16))) char vlds[kBK * St::STR];
+    __shared__ __attribute__((aligned(16))) char klds[2 * kBK * St::STR];  // two tile buffers each
+    __shared__ __attribute__((aligned(16))) char vlds[2 * kBK * St::STR];
     __shared__ int btc[kBtCache];
     __shared__ int claimed;
     const int count = a.item_count[0];
