@@ -170,3 +170,73 @@ def test_append_fp8_rounding_boundaries(vkv, oracle, cuda):
     assert np.array_equal(to_np(ks).view(np.uint32), ks_ref.view(np.uint32))
     assert np.array_equal(to_np(kc), kc_ref)
     assert np.array_equal(to_np(vc), vc_ref)
+
+
+def test_append_fp8_every_fp16_value_at_scale_one(vkv, oracle, cuda):
+    """Every fp16 value in [-448, 448] (normal, subnormal, signed zeros, exact e4m3
+    ties) quantised with scale 1 (each row holds 448, so amax/448 == 1 and x/scale
+    == x): the encoder's codes equal the oracle's brute-force nearest-even codes."""
+    import torch
+    bits = np.arange(0, 0x5F01, dtype=np.uint16)            # +0 .. 448
+    vals = np.concatenate([bits.view(np.float16), (bits | 0x8000).view(np.float16)])
+    Hkv, D = 8, 128
+    per_row = D - 1
+    nrows = (len(vals) + per_row - 1) // per_row
+    rows = np.zeros((nrows, D), np.float16)
+    rows[:, 0] = 448.0
+    flat = np.zeros(nrows * per_row, np.float16)
+    flat[:len(vals)] = vals
+    rows[:, 1:] = flat.reshape(nrows, per_row)
+    T = (nrows + Hkv - 1) // Hkv
+    k = np.zeros((T * Hkv, D), np.float16)
+    k[:nrows] = rows
+    k = k.reshape(T, Hkv, D)
+    v = k[::-1].copy()
+    bs = 16
+    N = (T + bs - 1) // bs
+    slots = np.arange(T, dtype=np.int32)
+    kc_ref = np.zeros((N, bs, Hkv, D), np.uint8)
+    vc_ref = np.zeros_like(kc_ref)
+    ks_ref = np.zeros((N, bs, Hkv), np.float32)
+    vs_ref = np.zeros_like(ks_ref)
+    oracle.reshape_and_cache(k.view(np.uint16), v.view(np.uint16), kc_ref, vc_ref, slots, ks_ref, vs_ref)
+    assert (ks_ref.reshape(-1)[:nrows] == 1.0).all()
+    kc = torch.zeros((N, bs, Hkv, D), dtype=torch.uint8, device=cuda)
+    vc = torch.zeros_like(kc)
+    ks = torch.zeros((N, bs, Hkv), dtype=torch.float32, device=cuda)
+    vs = torch.zeros_like(ks)
+    vkv.reshape_and_cache(to_dev(k, cuda), to_dev(v, cuda), kc, vc, to_dev(slots, cuda), ks, vs)
+    torch.cuda.synchronize()
+    got = to_np(kc)
+    bad = np.argwhere(got != kc_ref)
+    assert len(bad) == 0, f"{len(bad)} codes differ, first at {bad[:3].tolist()}"
+    assert np.array_equal(to_np(vc), vc_ref)
+    assert np.array_equal(to_np(ks).view(np.uint32), ks_ref.view(np.uint32))
+
+
+def test_append_fp8_non_finite_inputs(vkv, oracle, cuda):
+    """inf / NaN in a head vector take the software encoder: codes and scales as the oracle's."""
+    import torch
+    rng = np.random.default_rng(3)
+    Hkv, D, N, bs, T = 2, 64, 4, 16, 8
+    k = rng.standard_normal((T, Hkv, D)).astype(np.float32)
+    v = rng.standard_normal((T, Hkv, D)).astype(np.float32)
+    k[1, 0, 5] = np.inf
+    k[2, 1, 7] = np.nan
+    v[3, 0, 0] = -np.inf
+    slots = np.arange(T, dtype=np.int32) * 5
+    kc_ref = np.zeros((N, bs, Hkv, D), np.uint8)
+    vc_ref = np.zeros_like(kc_ref)
+    ks_ref = np.zeros((N, bs, Hkv), np.float32)
+    vs_ref = np.zeros_like(ks_ref)
+    oracle.reshape_and_cache(k, v, kc_ref, vc_ref, slots, ks_ref, vs_ref)
+    kc = torch.zeros((N, bs, Hkv, D), dtype=torch.uint8, device=cuda)
+    vc = torch.zeros_like(kc)
+    ks = torch.zeros((N, bs, Hkv), dtype=torch.float32, device=cuda)
+    vs = torch.zeros_like(ks)
+    vkv.reshape_and_cache(to_dev(k, cuda), to_dev(v, cuda), kc, vc, to_dev(slots, cuda), ks, vs)
+    torch.cuda.synchronize()
+    assert np.array_equal(to_np(kc), kc_ref)
+    assert np.array_equal(to_np(vc), vc_ref)
+    assert np.array_equal(to_np(ks).view(np.uint32), ks_ref.view(np.uint32))
+    assert np.array_equal(to_np(vs).view(np.uint32), vs_ref.view(np.uint32))

@@ -103,9 +103,13 @@ __device__ __forceinline__ float quotient(float x, float s, float rinv) {
 }
 
 // Quantise-on-append to e4m3fn.  A group of LPT = head_dim/16 consecutive
-// lanes holds one (token, kv head) vector, 16 elements per lane; the group's
-// amax comes from a DPP max reduction, then every lane divides its elements by
-// the common scale (IEEE division) and stores 16 codes.
+// lanes holds one (token, kv head) vector, 16 elements per lane, for K and V
+// at once (both loaded before either is used); each group's amax comes from a
+// DPP max reduction, every lane forms its 16 quotients x / scale (exact, see
+// quotient()) and encodes them with gfx950's v_cvt_pk_fp8_f32 (OCP e4m3fn,
+// round to nearest even).  Quotients are finite and within 448 (1 + 2^-22)
+// unless the input holds inf or NaN; a wave that meets one encodes with the
+// software rule (f32_to_fp8_sat: NaN -> 0x7F, saturation) instead.
 template <typename SRC, int LPT>
 __global__ __launch_bounds__(256) void append_fp8_kernel(AppendArgs a) {
     constexpr int SRC_BYTES = 16 * int(sizeof(SRC));
@@ -118,44 +122,72 @@ __global__ __launch_bounds__(256) void append_fp8_kernel(AppendArgs a) {
         // Whole groups share t, so the skip below is uniform within a group.
         if (slot < 0 || slot >= a.num_slots) continue;
         const int64_t head = r / LPT;
+        const char* src[2] = {a.key + t * a.key_stride_bytes + r * SRC_BYTES,
+                              a.value + t * a.value_stride_bytes + r * SRC_BYTES};
+        u32x4 w[2][SRC_BYTES / 16];
+#pragma unroll
+        for (int kv = 0; kv < 2; ++kv)
+#pragma unroll
+            for (int j = 0; j < SRC_BYTES / 16; ++j) w[kv][j] = load16_nt(src[kv] + 16 * j);
+        float x[2][16];
+        float amax[2] = {0.0f, 0.0f};
 #pragma unroll
         for (int kv = 0; kv < 2; ++kv) {
-            const char* src = (kv ? a.value + t * a.value_stride_bytes : a.key + t * a.key_stride_bytes) +
-                              r * SRC_BYTES;
-            float x[16];
 #pragma unroll
-            for (int j = 0; j < SRC_BYTES / 16; ++j) {
-                const u32x4 w = load16(src + 16 * j);
+            for (int j = 0; j < SRC_BYTES / 16; ++j)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     if constexpr (sizeof(SRC) == 4) {
-                        x[4 * j + e] = as_f32(w[e]);
+                        x[kv][4 * j + e] = as_f32(w[kv][j][e]);
                     } else {
-                        x[8 * j + 2 * e] = f16_bits_to_f32(uint16_t(w[e] & 0xFFFFu));
-                        x[8 * j + 2 * e + 1] = f16_bits_to_f32(uint16_t(w[e] >> 16));
+                        x[kv][8 * j + 2 * e] = f16_bits_to_f32(uint16_t(w[kv][j][e] & 0xFFFFu));
+                        x[kv][8 * j + 2 * e + 1] = f16_bits_to_f32(uint16_t(w[kv][j][e] >> 16));
                     }
                 }
-            }
-            float amax = 0.0f;
 #pragma unroll
-            for (int e = 0; e < 16; ++e) amax = fmaxf(amax, fabsf(x[e]));
-            amax = group_max<LPT>(amax);
-            const float scale = fp8_scale_from_amax(amax);
-            const float rinv = 1.0f / scale;  // correctly rounded
-            u32x4 q;
+            for (int e = 0; e < 16; ++e) amax[kv] = fmaxf(amax[kv], fabsf(x[kv][e]));
+        }
+        amax[0] = group_max<LPT>(amax[0]);
+        amax[1] = group_max<LPT>(amax[1]);
+        bool finite = true;
+        float scale[2];
 #pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                uint32_t packed = 0;
+        for (int kv = 0; kv < 2; ++kv) {
+            scale[kv] = fp8_scale_from_amax(amax[kv]);
+            const float rinv = 1.0f / scale[kv];  // correctly rounded
 #pragma unroll
-                for (int b = 0; b < 4; ++b) packed |= f32_to_fp8_sat(quotient(x[4 * w + b], scale, rinv)) << (8 * b);
-                q[w] = packed;
+            for (int e = 0; e < 16; ++e) {
+                x[kv][e] = quotient(x[kv][e], scale[kv], rinv);
+                finite &= (as_u32(x[kv][e]) & 0x7F800000u) != 0x7F800000u;
             }
-            char* cache = kv ? a.value_cache : a.key_cache;
-            store16(cache + slot * a.row_bytes + r * 16, q);
-            if ((r % LPT) == 0) {
-                float* scales = kv ? a.value_scales : a.key_scales;
-                scales[slot * a.num_kv_heads + head] = scale;
-            }
+        }
+        u32x4 q[2];
+        if (__builtin_amdgcn_ballot_w64(!finite) == 0) {
+#pragma unroll
+            for (int kv = 0; kv < 2; ++kv)
+#pragma unroll
+                for (int wd = 0; wd < 4; ++wd) {
+                    int v = __builtin_amdgcn_cvt_pk_fp8_f32(x[kv][4 * wd], x[kv][4 * wd + 1], 0, false);
+                    v = __builtin_amdgcn_cvt_pk_fp8_f32(x[kv][4 * wd + 2], x[kv][4 * wd + 3], v, true);
+                    q[kv][wd] = uint32_t(v);
+                }
+        } else {
+#pragma unroll
+            for (int kv = 0; kv < 2; ++kv)
+#pragma unroll
+                for (int wd = 0; wd < 4; ++wd) {
+                    uint32_t packed = 0;
+#pragma unroll
+                    for (int b = 0; b < 4; ++b) packed |= f32_to_fp8_sat(x[kv][4 * wd + b]) << (8 * b);
+                    q[kv][wd] = packed;
+                }
+        }
+        const int64_t dst = slot * a.row_bytes + r * 16;
+        store16_nt(a.key_cache + dst, q[0]);
+        store16_nt(a.value_cache + dst, q[1]);
+        if ((r % LPT) == 0) {
+            a.key_scales[slot * a.num_kv_heads + head] = scale[0];
+            a.value_scales[slot * a.num_kv_heads + head] = scale[1];
         }
     }
 }
