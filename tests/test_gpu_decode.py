@@ -189,6 +189,36 @@ def test_decode_fp8(vkv, oracle, cuda, H, Hkv, D, bs, ctx):
     assert (num <= 0.15 * den + 1e-6).all(), f"fp8 vs fp16 relative error {float((num / den).max()):.4f}"
 
 
+@pytest.mark.parametrize("D", [128, 64])
+def test_decode_fp8_single_key_is_exact(vkv, oracle, cuda, D):
+    """ctx 1 with value scale 1: every output element is its e4m3 code's value
+    exactly (the weight is 1), so the value path's code-to-fp16 conversion is
+    checked for all 254 finite codes (matrix-core variant at D=128, VALU at 64)."""
+    import torch
+    H, Hkv, bs, S = 32, 8, 16, 3
+    G = H // Hkv
+    rng = np.random.default_rng(77)
+    finite = np.array([c for c in range(256) if c not in (0x7F, 0xFF)], np.uint8)
+    N = S + 1
+    kc = rng.integers(0, 0x70, (N, bs, Hkv, D), dtype=np.uint8)      # any finite keys
+    vc = np.zeros((N, bs, Hkv, D), np.uint8)
+    for s in range(S):
+        vc[s + 1, 0] = np.resize(rng.permutation(finite), Hkv * D).reshape(Hkv, D)
+    ks = np.full((N, bs, Hkv), 0.5, np.float32)
+    vs = np.ones((N, bs, Hkv), np.float32)
+    bt = np.arange(1, S + 1, dtype=np.int32)[:, None]
+    cl = np.ones(S, np.int32)
+    q = rng.standard_normal((S, H, D)).astype(np.float16)
+    out = torch.zeros((S, H, D), dtype=torch.float16, device=cuda)
+    vkv.paged_decode(out, to_dev(q, cuda), to_dev(kc, cuda), to_dev(vc, cuda), to_dev(bt, cuda), to_dev(cl, cuda),
+                     float(1.0 / np.sqrt(D)), key_scales=to_dev(ks, cuda), value_scales=to_dev(vs, cuda))
+    torch.cuda.synchronize()
+    table = np.array([oracle.fp8_decode(int(c)) for c in range(256)], np.float32)
+    want = table[vc[1:S + 1, 0]]                                   # [S, Hkv, D]
+    want = np.repeat(want, G, axis=1)                               # head h reads kv head h // G
+    assert np.array_equal(to_np(out).astype(np.float32), want)
+
+
 def test_decode_config2_sampled(vkv, oracle, cuda):
     """Full C2 (Llama-3-8B shape, B=64, ctx U[512,4096]): append + decode on the GPU;
     six sequences are recomputed by the oracle from their own blocks; a second

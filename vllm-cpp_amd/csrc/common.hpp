@@ -142,6 +142,14 @@ __device__ __forceinline__ void fp8x4_to_half2x2_scaled(uint32_t w, uint32_t& lo
 
 constexpr float kFp8HalfScale = 256.0f;  // undoes the 2^-8 of the re-expression above
 
+// Two e4m3fn codes (bits 0-15 of w, or bits 16-31 with HI) as their exact fp16
+// values, element 0 from the lower byte: gfx950's v_cvt_scalef32_pk_f16_fp8
+// with scale 1 (every finite e4m3fn value is an fp16 value).
+template <bool HI>
+__device__ __forceinline__ uint32_t fp8x2_to_half2(uint32_t w) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, HI));
+}
+
 // fp32 -> e4m3fn, round to nearest even, saturating: |x| beyond 448 (and inf)
 // encode as 448, NaN as 0x7F with the sign of x.
 __device__ __forceinline__ uint32_t f32_to_fp8_sat(float x) {

@@ -503,8 +503,8 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, const int s, co
 //   The accumulator gives lane l the logits of head l%16 for tokens
 //   4(l/16)..+3.  fp16 K: lane l loads dims 32i + 8(l/16) for MFMA i.  FP8 K:
 //   lane l loads 16 codes, dims 32(l/16) + 16j (two loads), feeding MFMAs 2j
-//   and 2j+1; codes are widened exactly to fp16 (times 2^-8) and the token's
-//   scale multiplies the logit.
+//   and 2j+1; codes are converted exactly to fp16 (v_cvt_scalef32_pk_f16_fp8,
+//   scale 1) and the token's scale multiplies the logit.
 //   Softmax on that layout (running max per head, lanes sharing l%16 agree),
 //   probabilities through a 16 x G slice of LDS to the V layout, and p * V as
 //   packed fp16 dot products over token pairs (lane l: token 4u + l/16, dims
@@ -555,11 +555,6 @@ __device__ __forceinline__ void decode_item_mfma(const DecodeArgs& a, const int 
         const int d0 = FP8 ? 32 * quad + 16 * (i >> 1) + 8 * (i & 1) : 32 * i + 8 * quad;
         u32x4 w = load16(qrow + d0 * 2);
         w = (w ^ u32x4{qflip, qflip, qflip, qflip}) & u32x4{qkeep, qkeep, qkeep, qkeep};
-        if constexpr (FP8) {
-            // widened FP8 codes come as (b0, b2), (b1, b3) per 4 bytes: same order for Q
-            w = u32x4{__builtin_amdgcn_perm(w[1], w[0], 0x05040100u), __builtin_amdgcn_perm(w[1], w[0], 0x07060302u),
-                      __builtin_amdgcn_perm(w[3], w[2], 0x05040100u), __builtin_amdgcn_perm(w[3], w[2], 0x07060302u)};
-        }
         qb[i] = __builtin_bit_cast(half8_t, w);
     }
     const float sc = neg_scale ? -a.scale_log2 : a.scale_log2;
@@ -621,17 +616,16 @@ __device__ __forceinline__ void decode_item_mfma(const DecodeArgs& a, const int 
         if constexpr (FP8) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                uint32_t w[4];
-                fp8x4_to_half2x2_scaled(ch.k[i >> 1][2 * (i & 1)], w[0], w[1]);
-                fp8x4_to_half2x2_scaled(ch.k[i >> 1][2 * (i & 1) + 1], w[2], w[3]);
-                cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                    __builtin_bit_cast(half8_t, u32x4{w[0], w[1], w[2], w[3]}), qb[i], cc, 0, 0, 0);
+                const uint32_t c0 = ch.k[i >> 1][2 * (i & 1)], c1 = ch.k[i >> 1][2 * (i & 1) + 1];
+                const u32x4 w = {fp8x2_to_half2<false>(c0), fp8x2_to_half2<true>(c0), fp8x2_to_half2<false>(c1),
+                                 fp8x2_to_half2<true>(c1)};
+                cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, w), qb[i], cc, 0, 0, 0);
             }
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 ch.ks[k] = __shfl(ch.sc1, 4 * quad + k, kWave);
                 ch.vs[k] = __shfl(ch.sc1, 16 + 4 * k + quad, kWave);
-                cc[k] *= ch.ks[k] * kFp8HalfScale;
+                cc[k] *= ch.ks[k];
             }
         } else {
 #pragma unroll
@@ -694,8 +688,8 @@ __device__ __forceinline__ void decode_item_mfma(const DecodeArgs& a, const int 
 #pragma unroll
         for (int u = 0; u < 4; u += 2) {
             half2_t pp[G];
-            const float v0 = FP8 ? ch.vs[u] * kFp8HalfScale : 1.0f;
-            const float v1 = FP8 ? ch.vs[u + 1] * kFp8HalfScale : 1.0f;
+            const float v0 = FP8 ? ch.vs[u] : 1.0f;
+            const float v1 = FP8 ? ch.vs[u + 1] : 1.0f;
 #pragma unroll
             for (int h = 0; h < G; ++h)
                 pp[h] = half2_t{static_cast<_Float16>(plds[(4 * u + quad) * G + h] * v0),
@@ -705,16 +699,13 @@ __device__ __forceinline__ void decode_item_mfma(const DecodeArgs& a, const int 
                 va = vr[u];
                 vb = vr[u + 1];
             } else {
-                // widen the two tokens' codes to fp16 in dim order: (b0, b1), (b2, b3)
+                // the two tokens' codes as fp16 in dim order: (b0, b1), (b2, b3)
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
-                    uint32_t lo, hi;
-                    fp8x4_to_half2x2_scaled(ch.v8[u][h], lo, hi);
-                    va[2 * h] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
-                    va[2 * h + 1] = __builtin_amdgcn_perm(hi, lo, 0x07060302u);
-                    fp8x4_to_half2x2_scaled(ch.v8[u + 1][h], lo, hi);
-                    vb[2 * h] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
-                    vb[2 * h + 1] = __builtin_amdgcn_perm(hi, lo, 0x07060302u);
+                    va[2 * h] = fp8x2_to_half2<false>(ch.v8[u][h]);
+                    va[2 * h + 1] = fp8x2_to_half2<true>(ch.v8[u][h]);
+                    vb[2 * h] = fp8x2_to_half2<false>(ch.v8[u + 1][h]);
+                    vb[2 * h + 1] = fp8x2_to_half2<true>(ch.v8[u + 1][h]);
                 }
             }
 #pragma unroll
