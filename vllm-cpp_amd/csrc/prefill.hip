@@ -442,59 +442,83 @@ __global__ __launch_bounds__(64 * kMaxWaves) void prefill_mfma_kernel(PrefillArg
 }
 
 // Work list of the matrix-core kernel, in one workgroup: items (s, qb * Hkv +
-// kvh) of every sequence with >= 2 query tokens, ordered by distance from the
-// sequence's last query block (last blocks, which see the most keys, first),
-// so that short blocks fill in at the end.  Level L holds block qb = nqb - 1 - L
-// of every sequence with nqb > L blocks.
+// kvh) of every sequence with >= 2 query tokens, ordered by level, where level
+// L holds block qb = nqb - 1 - L of every sequence with nqb > L blocks: last
+// blocks (which see the most keys) first, so that short blocks fill in at the
+// end.  Each sequence's q_len is read once; a histogram of block counts gives
+// every level's size and offset, and the sequences of a level take their slots
+// through LDS atomics (the order within a level does not matter to the
+// results).  At most kMaxLevels levels (max_query_len <= 32 * kMaxLevels).
+constexpr int kMaxLevels = 4096;
+
+// Exclusive prefix sum of arr[0, n) in LDS by 256 threads (each a contiguous
+// tile, tiles combined with wave shuffles and one LDS step); returns the total.
+__device__ int block_exclusive_scan(int* arr, int n, int* wave_tot) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int per = (n + 255) / 256;
+    const int b = tid * per;
+    int local = 0;
+    for (int i = 0; i < per; ++i)
+        if (b + i < n) local += arr[b + i];
+    int incl = local;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += y;
+    }
+    if (lane == 63) wave_tot[wave] = incl;
+    __syncthreads();
+    int before = 0;
+    for (int w = 0; w < wave; ++w) before += wave_tot[w];
+    const int total = wave_tot[0] + wave_tot[1] + wave_tot[2] + wave_tot[3];
+    int run = before + incl - local;
+    for (int i = 0; i < per; ++i) {
+        if (b + i < n) {
+            const int v = arr[b + i];
+            arr[b + i] = run;
+            run += v;
+        }
+    }
+    __syncthreads();  // (wave_tot may be reused by the next scan)
+    return total;
+}
+
 __global__ __launch_bounds__(256) void prefill_items_kernel(const int32_t* qsl, int32_t num_seqs, int32_t hkv,
                                                             int32_t max_qblocks, int2* items, int32_t* count) {
-    __shared__ int wave_sum[4];
-    __shared__ int level_total;
+    __shared__ int hist[kMaxLevels + 1];  // sequences with exactly n blocks, then its prefix sums
+    __shared__ int off[kMaxLevels];       // items per level, then level offsets
+    __shared__ int fill[kMaxLevels];      // slots taken per level
+    __shared__ int wave_tot[4];
     const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int per = (num_seqs + 255) / 256;
-    const int s0 = tid * per;
+    const int levels = max_qblocks < kMaxLevels ? max_qblocks : kMaxLevels;
+    for (int i = tid; i <= levels; i += 256) hist[i] = 0;
+    for (int i = tid; i < levels; i += 256) fill[i] = 0;
+    __syncthreads();
     auto nqb = [&](int s) {
         const int q = qsl[s + 1] - qsl[s];
         const int n = q >= 2 ? (q + kBQ - 1) / kBQ : 0;
-        return n < max_qblocks ? n : max_qblocks;  // max_query_len bounds q_len (caller contract)
+        return n < levels ? n : levels;  // max_query_len bounds q_len (caller contract)
     };
-    int total = 0;
-    for (int L = 0;; ++L) {
-        int local = 0;
-        for (int i = 0; i < per; ++i)
-            if (s0 + i < num_seqs && nqb(s0 + i) > L) local += hkv;
-        int incl = local;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int y = __shfl_up(incl, o, 64);
-            if (lane >= o) incl += y;
-        }
-        if (lane == 63) wave_sum[wave] = incl;
-        __syncthreads();
-        int before = 0;
-        for (int w = 0; w < wave; ++w) before += wave_sum[w];
-        if (tid == 255) level_total = before + incl;
-        int pos = total + before + incl - local;
-        for (int i = 0; i < per; ++i) {
-            const int s = s0 + i;
-            if (s >= num_seqs) break;
-            const int n = nqb(s);
-            if (n > L) {
-                for (int k = 0; k < hkv; ++k) items[pos + k] = int2{s, (n - 1 - L) * hkv + k};
-                pos += hkv;
-            }
-        }
-        __syncthreads();
-        const int lt = level_total;
-        __syncthreads();
-        if (lt == 0) break;
-        total += lt;
+    for (int s = tid; s < num_seqs; s += 256) {
+        const int n = nqb(s);
+        if (n > 0) atomicAdd(&hist[n], 1);
     }
+    __syncthreads();
+    // level L holds the sequences with n > L: total - (those with n <= L)
+    const int seqs = block_exclusive_scan(hist, levels + 1, wave_tot);
+    for (int L = tid; L < levels; L += 256) off[L] = (seqs - hist[L + 1]) * hkv;
+    __syncthreads();
+    const int total = block_exclusive_scan(off, levels, wave_tot);
     if (tid == 0) {
         count[0] = total;
         count[1] = 0;  // claim counter of the prefill kernel
+    }
+    for (int s = tid; s < num_seqs; s += 256) {
+        const int n = nqb(s);
+        for (int L = 0; L < n; ++L) {
+            const int pos = off[L] + atomicAdd(&fill[L], hkv);
+            for (int k = 0; k < hkv; ++k) items[pos + k] = int2{s, (n - 1 - L) * hkv + k};
+        }
     }
 }
 
@@ -508,7 +532,8 @@ int ilog2i(int x) {
 
 bool prefill_mfma_supported(const vkv_prefill_params* p) {
     return p->io_dtype == VKV_DTYPE_F16 && (p->kv_dtype == VKV_DTYPE_F16 || p->kv_dtype == VKV_DTYPE_FP8_E4M3) &&
-           (p->head_dim == 64 || p->head_dim == 128) && p->max_query_len >= 2;
+           (p->head_dim == 64 || p->head_dim == 128) && p->max_query_len >= 2 &&
+           (int64_t(p->max_query_len) + kBQ - 1) / kBQ <= kMaxLevels;
 }
 
 size_t prefill_items_bytes(const vkv_prefill_params* p) {
