@@ -612,6 +612,21 @@ def suite_rope(dev, steps, warmup):
                              "(D fp32) and slot + position per token"}
 
 
+def suite_step(dev, steps, warmup):
+    """Batched attention step (AttentionMetadata + PagedAttentionLayer, 32 layers of
+    Llama-3-8B attention, C2's 64 sequences) beside the reference's per-sequence,
+    per-token call pattern on the same kernels: vllm-cpp_amd/_build/bench_attention_step."""
+    import subprocess
+    exe = os.path.join(ROOT, "vllm-cpp_amd", "_build", "bench_attention_step")
+    if not os.path.exists(exe):
+        raise RuntimeError(f"{exe} not built: run __graft_entry__.build()")
+    r = subprocess.run([exe, "32", str(max(5, steps // 5)), "2"], stdout=subprocess.PIPE, stderr=subprocess.PIPE,
+                       text=True, timeout=600)
+    if r.returncode != 0:
+        raise RuntimeError(f"bench_attention_step failed ({r.returncode}): {r.stdout[-2000:]} {r.stderr[-2000:]}")
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
 def suite_stream(dev, steps, warmup):
     """Device-to-device copy of 1 GiB (read + write): the practical HBM ceiling."""
     import torch
@@ -693,7 +708,8 @@ def suite_c4(dev, steps, warmup):
                              "sample": f"oracle copy_blocks of {Ps} pairs x {Ls} layers x K,V, {reps} calls"}}
 
 
-SUITES = {"stream": suite_stream, "c1": suite_c1, "append": suite_append, "rope": suite_rope, "c3": suite_c3,
+SUITES = {"stream": suite_stream, "c1": suite_c1, "append": suite_append, "rope": suite_rope, "step": suite_step,
+          "c3": suite_c3,
           "c3p": suite_c3_prefill_only, "c5": suite_c5, "c4": suite_c4}
 
 
