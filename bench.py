@@ -404,7 +404,7 @@ def suite_c1(dev, steps, warmup):
     return {"row": "C1 append + decode", "workload": "Qwen2.5-0.5B shape H14/Hkv2/D64 fp16 bs16, B=4, ctx U[1,512]",
             "kv_bytes": kvb, "step_us_median": round(t[0] * 1e3, 2),
             "step_us_p10_p90": [round(t[1] * 1e3, 2), round(t[2] * 1e3, 2)],
-            "note": "launch-bound: two kernels for 0.5 MB of KV",
+            "note": "launch-bound: three kernels (append, partition, merge) for 0.6 MB of KV",
             "cpu_baseline": {"us_per_step": round(sec * 1e6, 1), "cores": 1, "kind": "port",
                              "sample": f"oracle append + decode of the whole step, {reps} steps"}}
 

@@ -68,6 +68,8 @@ constexpr int kMinWavesPerSimd = VKV_DECODE_MIN_WAVES;
 constexpr int kOneChunkAboveG = VKV_DECODE_ONE_CHUNK_ABOVE_G;
 constexpr int kOneChunkAboveGFp8 = VKV_DECODE_ONE_CHUNK_ABOVE_G_FP8;
 constexpr float kLog2e = 1.4426950408889634f;
+// Default partition sizing aims at this many (row, partition, kv head) items.
+constexpr int64_t kMinItems = 2048;
 // Launch cap in workgroups per CU.  A grid holding every item group lets the
 // hardware dispatcher balance the CUs; claims through the counters only serve
 // batches with more groups than this.
@@ -1055,18 +1057,26 @@ int ilog2(int x) {
 DecodePlan plan_decode(const vkv_decode_params* p) {
     DecodePlan plan;
     const int bs = p->block_size;
+    int64_t max_ctx = p->max_context_len;
+    const int64_t table_tokens = int64_t(p->max_blocks_per_seq) * bs;
+    if (max_ctx > table_tokens) max_ctx = table_tokens;
+    if (max_ctx < 0) max_ctx = 0;
     // Default 768 tokens: the best of a 384..1024 sweep for both the C2
     // (B=64, ctx U[512,4096]) and C5 (B=256, lognormal ctx) decode batches.
+    // Small batches split finer (halving, not below 32 tokens) until the
+    // longest possible contexts would give kMinItems work items: a wave walks
+    // its partition serially, so 8 items of 512 tokens (C1) leave the GPU
+    // idle while 88 items of 48 tokens finish together.
     int P = p->partition_size > 0 ? p->partition_size : 768;
+    if (p->partition_size <= 0) {
+        const int64_t per_part = int64_t(p->num_seqs) * p->num_kv_heads;
+        while (P / 2 >= 32 && per_part * ((max_ctx + P - 1) / P) < kMinItems) P /= 2;
+    }
     // A partition starts on a block boundary and holds at most 64 blocks
     // (one block id per lane).
     if (P < bs) P = bs;
     P = (P / bs) * bs;
     if (P > 64 * bs) P = 64 * bs;
-    int64_t max_ctx = p->max_context_len;
-    const int64_t table_tokens = int64_t(p->max_blocks_per_seq) * bs;
-    if (max_ctx > table_tokens) max_ctx = table_tokens;
-    if (max_ctx < 0) max_ctx = 0;
     plan.partition_size = P;
     plan.max_parts = int((max_ctx + P - 1) / P);
     if (plan.max_parts < 1) plan.max_parts = 1;
