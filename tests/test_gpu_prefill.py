@@ -31,7 +31,7 @@ def _case(H, Hkv, D, bs, q_lens, prior, seed):
     (32, 8, 128, 16, [5, 1, 17], [0, 30, 40]),
     (28, 4, 128, 32, [64, 1, 1, 33], [100, 500, 0, 7]),
     (14, 2, 64, 16, [40], [0]),
-    (16, 2, 128, 16, [40, 3, 1], [10, 0, 77]),      # group 8: eight waves per workgroup
+    (16, 2, 128, 16, [40, 3, 1], [10, 0, 77]),      # group 8: two head groups (grid.z), one claim counter each
     (8, 8, 64, 8, [70, 2], [9000, 5]),              # MHA; 1131 blocks: block-id window reloads
     (16, 4, 128, 64, [33, 1, 100], [64, 0, 129]),   # blocks larger than a key tile
     (12, 4, 128, 16, [2, 31, 32, 65], [0, 1, 15, 300]),
@@ -49,10 +49,10 @@ def test_prefill_vs_oracle(vkv, oracle, cuda, H, Hkv, D, bs, q_lens, prior):
     assert_close(to_np(out).astype(np.float32), ref, F16_ATOL, F16_RTOL, "prefill")
 
 
-def test_prefill_fp8_vs_oracle(vkv, oracle, cuda):
+@pytest.mark.parametrize("H,Hkv,D,bs", [(28, 4, 128, 32), (16, 2, 64, 16)])  # groups 7 and 8
+def test_prefill_fp8_vs_oracle(vkv, oracle, cuda, H, Hkv, D, bs):
     """FP8 cache (quantised by the GPU append): against the oracle on the same codes and scales."""
     import torch
-    H, Hkv, D, bs = 28, 4, 128, 32
     lay, ctx, qsl, q, k, v, scale = _case(H, Hkv, D, bs, [48, 1, 130], [20, 300, 64], 9)
     N = lay.num_blocks
     kc = torch.zeros((N, bs, Hkv, D), dtype=torch.uint8, device=cuda)

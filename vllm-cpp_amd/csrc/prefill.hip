@@ -22,12 +22,14 @@
 //                 never leaves the wave.
 // The output tile is O^T, again one row per lane, normalised at the end.
 //
-// Staging.  Each of the first 256 threads loads its share of the next tile's K
-// and V rows (16 bytes = 8 dims of one token per load) into registers while
-// the current tile is computed, then writes both row-major into LDS (rows
-// padded by 16 bytes to spread the banks).
-// FP8 caches are dequantised (code x per-token scale, fp32 -> fp16) on the way
-// into LDS.  Block ids of the sequence are cached in LDS, 1024 at a time.
+// Staging.  fp16 caches (prefill_dma_kernel): one extra producer wave loads
+// the tiles straight from global memory into LDS (global_load_lds, three tile
+// buffers, two tiles ahead), so the compute waves run no staging code.  FP8
+// caches (prefill_mfma_kernel): each of the first 256 threads loads its share
+// of the next tile's K and V rows into registers while the current tile is
+// computed, then writes them row-major into LDS (rows padded by 16 bytes to
+// spread the banks), dequantised on the way (code x per-token scale, fp32 ->
+// fp16).  Block ids of the sequence are cached in LDS, 1024 at a time.
 #include <type_traits>
 
 #include "common.hpp"
@@ -69,7 +71,7 @@ struct PrefillArgs {
     int32_t qblocks;  // query blocks per sequence in the grid
     int32_t num_seqs;
     const int2* items;       // work list (s, qb * Hkv + kvh)
-    int32_t* item_count;     // [0] items, [1] claim counter (zeroed by the list kernel)
+    int32_t* item_count;     // [0] items, [1 + z] claim counter of head group z (zeroed by the list kernel)
     float scale_log2;
 };
 
@@ -224,11 +226,6 @@ __device__ __forceinline__ void prefill_block(const PrefillArgs& a, const int s,
             }
             __syncthreads();
         }
-    };
-    // address of token k's row in the K or V cache (block id from the LDS cache)
-    auto token_off = [&](int k) __attribute__((always_inline)) {
-        const int blk = btc[(k >> a.bs_log2) - win];
-        return ((int64_t(blk) << a.bs_log2) + (k & bs_mask)) * row_bytes + int64_t(kvh) * D * EB;
     };
     // Keys past kend (the tail of the last tile) load the row of key kend - 1
     // instead: every query row masks them, so no branch is needed around the
@@ -430,7 +427,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void prefill_mfma_kernel(PrefillArg
     __shared__ int claimed;
     const int count = a.item_count[0];
     for (;;) {
-        if (threadIdx.x == 0) claimed = atomicAdd(a.item_count + 1, 1);
+        if (threadIdx.x == 0) claimed = atomicAdd(a.item_count + 1 + blockIdx.z, 1);
         __syncthreads();
         const int it = claimed;
         __syncthreads();  // every thread has read `claimed` before thread 0 may overwrite it
@@ -438,6 +435,306 @@ __global__ __launch_bounds__(64 * kMaxWaves) void prefill_mfma_kernel(PrefillArg
         const int2 item = a.items[it];
         prefill_block<D, KVT>(a, item.x, item.y / a.num_kv_heads, item.y % a.num_kv_heads, klds, vlds, btc);
         __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------------------
+// fp16 caches: one producer wave stages the tiles by direct global->LDS loads.
+//
+// The workgroup is heads_per_wg compute waves plus one producer wave, which
+// keeps kStages tile buffers in flight: it loads tile t + 2 while the compute
+// waves work on tile t, and publishes tile t + 1 with the barrier that ends
+// tile t (its own loads counted out with s_waitcnt vmcnt before it).  So the
+// compute waves run no staging code and hold no staging registers, and a
+// load has two tiles of compute to land.  A direct load writes 1 KiB of LDS
+// per wave instruction (lane L -> bytes 16 L), so tile rows are unpadded:
+// 16-byte chunk c of key row r sits at slot c ^ (r % CH) (CH chunks per row),
+// which spreads the compute waves' reads of one chunk column over the banks.
+constexpr int kStages = 3;
+constexpr int kMaxComputeWaves = 7;  // + the producer: 8 waves, 2 per SIMD
+
+template <int D>
+struct DmaTile {
+    static constexpr int ROW = D * 2;        // bytes per key row
+    static constexpr int CH = ROW / 16;      // 16-byte chunks per row
+    static constexpr int RPI = 1024 / ROW;   // rows per wave instruction
+    static constexpr int INST = kBK / RPI;   // wave instructions per K (or V) tile
+    static constexpr int BYTES = kBK * ROW;  // one K (or V) tile
+    // LDS byte of (row, chunk)
+    __device__ static __forceinline__ int off(int row, int chunk) { return row * ROW + ((chunk ^ (row % CH)) << 4); }
+};
+
+// s_waitcnt with only the vector-memory count limited (GFX9 encoding: vmcnt
+// bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Workgroup barrier that orders LDS only: the producer's direct loads are
+// counted out by wait_vmcnt before it, and every compute wave has consumed its
+// LDS reads (they feed the tile's MFMAs) before it arrives.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+__device__ __forceinline__ float vmax3(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
+// One work item on an fp16 cache: query block qb (kBQ tokens) of sequence s
+// against kv head kvh; wave heads_per_wg is the producer.
+template <int D>
+__device__ __forceinline__ void prefill_block_dma(const PrefillArgs& a, const int s, const int qb, const int kvh,
+                                                  char* tiles, int* btc) {
+    using T = DmaTile<D>;
+    constexpr int DT = D / 16;  // output dim tiles
+    constexpr int KS = D / 32;  // MFMA k-steps of Q K^T
+    constexpr int STAGE = 2 * T::BYTES;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int col = lane & 15;
+    const int grp = lane >> 4;
+    const bool producer = wave == a.heads_per_wg;
+    const int g = blockIdx.z * a.heads_per_wg + wave;
+    const bool computes = !producer && g < a.group;
+
+    const int q0 = a.qsl[s];
+    const int qlen = a.qsl[s + 1] - q0;
+    if (qlen < 2 || qb * kBQ >= qlen) return;  // (the item list holds none of these)
+    const int prior = a.cl[s] - qlen;
+    const int jmax = min(qlen, qb * kBQ + kBQ);
+    int kend = prior + jmax;
+    kend = kend < a.table_tokens ? kend : a.table_tokens;
+    const int ntiles = kend > 0 ? (kend + kBK - 1) / kBK : 0;
+
+    if (producer) {
+        // ---------------- producer: tiles 0 and 1 ahead, then one per barrier
+        const int bs_mask = (1 << a.bs_log2) - 1;
+        const int64_t row_bytes = int64_t(a.num_kv_heads) * D * 2;
+        const int64_t head_off = int64_t(kvh) * D * 2;
+        const int32_t* table = a.bt + int64_t(s) * a.max_blocks_per_seq;
+        int win = -1;
+        auto produce = [&](const int t) __attribute__((always_inline)) {
+            const int k0 = t * kBK;
+            const int first = k0 >> a.bs_log2;
+            if (win < 0 || first + (kBK >> a.bs_log2) + 1 > win + kBtCache) {
+                // block ids cached in LDS (read by this wave only)
+                win = first;
+                for (int i = lane; i < kBtCache; i += 64) {
+                    const int b = win + i;
+                    int id = 0;
+                    if (b < a.max_blocks_per_seq) {
+                        id = table[b];
+                        if (a.num_blocks > 0 && unsigned(id) >= unsigned(a.num_blocks)) id = 0;
+                    }
+                    btc[i] = id;
+                }
+            }
+            char* kdst = tiles + (t % kStages) * STAGE;
+            char* vdst = kdst + T::BYTES;
+            int64_t slot[T::INST];  // cache slot of each instruction's key (block ids read first, together)
+#pragma unroll
+            for (int j = 0; j < T::INST; ++j) {
+                int k = k0 + j * T::RPI + lane / T::CH;
+                k = k < kend ? k : kend - 1;  // past the end: key kend - 1 again (masked)
+                slot[j] = (int64_t(btc[(k >> a.bs_log2) - win]) << a.bs_log2) + (k & bs_mask);
+            }
+#pragma unroll
+            for (int j = 0; j < T::INST; ++j) {
+                const int row = j * T::RPI + lane / T::CH;
+                const int chunk = (lane % T::CH) ^ (row % T::CH);
+                const int64_t off = slot[j] * row_bytes + head_off + chunk * 16;
+                __builtin_amdgcn_global_load_lds(a.kc + off, (__attribute__((address_space(3))) void*)(kdst + j * 1024),
+                                                 16, 0, 0);
+                __builtin_amdgcn_global_load_lds(a.vc + off, (__attribute__((address_space(3))) void*)(vdst + j * 1024),
+                                                 16, 0, 0);
+            }
+        };
+        if (ntiles > 0) produce(0);
+        if (ntiles > 1) produce(1);
+        for (int t = 0; t < ntiles; ++t) {
+            if (t + 1 < ntiles) wait_vmcnt<2 * T::INST>();  // tile t landed, t + 1 may be in flight
+            else wait_vmcnt<0>();
+            lds_barrier();  // publishes tile t; every wave has left tile t - 1
+            if (t + 2 < ntiles) produce(t + 2);  // into the buffer of tile t - 1
+        }
+        return;
+    }
+
+    // ---------------- compute waves: Q (B operand of S^T = K Q^T) and per-row context
+    const int h = kvh * a.group + g;
+    const bool neg_scale = a.scale_log2 < 0.0f;
+    const float sc = neg_scale ? -a.scale_log2 : a.scale_log2;
+    half8_t qop[kRT][KS];
+    int rctx[kRT];
+#pragma unroll
+    for (int r = 0; r < kRT; ++r) {
+        const int j = qb * kBQ + 16 * r + col;
+        int c = prior + j + 1;
+        c = c < 0 ? 0 : (c > a.table_tokens ? a.table_tokens : c);
+        rctx[r] = (j < qlen) ? c : 0;
+#pragma unroll
+        for (int i = 0; i < KS; ++i) {
+            const bool ok = computes && j < qlen;
+            const int64_t qrow = ok ? int64_t(q0) + j : int64_t(q0);
+            const int64_t qcol = ok ? int64_t(h) * D : 0;
+            u32x4 w = load16(a.q + (qrow * a.q_stride + qcol + 32 * i + 8 * grp) * 2);
+            const uint32_t keep = ok ? 0xFFFFFFFFu : 0u;
+            const uint32_t flip = neg_scale ? 0x80008000u : 0u;
+            w = (w ^ u32x4{flip, flip, flip, flip}) & u32x4{keep, keep, keep, keep};
+            qop[r][i] = __builtin_bit_cast(half8_t, w);
+        }
+    }
+
+    const float lazy = kLazy / sc;  // kLazy in raw (unscaled) logit units
+    float m[kRT], mlim[kRT], msc[kRT];
+    float4_t lsum[kRT];  // row sums (every element the same)
+    float4_t o[kRT][DT];
+    const half8_t kOnes = {1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16};
+#pragma unroll
+    for (int r = 0; r < kRT; ++r) {
+        m[r] = -INFINITY;
+        mlim[r] = -INFINITY;  // m + lazy
+        msc[r] = 0.0f;        // m * sc, 0 while the row has no key
+        lsum[r] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int t = 0; t < DT; ++t) o[r][t] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+
+    auto qk = [&](const char* kb, const int sub, float4_t (&sv)[kRT][2]) __attribute__((always_inline)) {
+        half8_t kop[2][KS];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+            for (int i = 0; i < KS; ++i)
+                kop[hh][i] = __builtin_bit_cast(
+                    half8_t, *reinterpret_cast<const u32x4*>(kb + T::off(32 * sub + 16 * hh + col, 4 * i + grp)));
+#pragma unroll
+        for (int r = 0; r < kRT; ++r) sv[r][0] = sv[r][1] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int i = 0; i < KS; ++i)
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                for (int r = 0; r < kRT; ++r)
+                    sv[r][hh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop[hh][i], qop[r][i], sv[r][hh], 0, 0, 0);
+    };
+    auto softmax = [&](const int kbase, const float4_t (&sv)[kRT][2], half8_t (&pop)[kRT]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int r = 0; r < kRT; ++r) {
+            float x[8];
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) x[4 * hh + e] = sv[r][hh][e];
+            if (__builtin_amdgcn_ballot_w64(kbase + 32 > rctx[r])) {
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (kbase + 16 * hh + 4 * grp + e >= rctx[r]) x[4 * hh + e] = -INFINITY;
+            }
+            // This lane's max decides whether the row max is needed at all: it
+            // is only when some lane exceeds the lazy limit m + kLazy (then the
+            // max over the row's four key groups resets m and rescales).  Below
+            // the limit the weights exp2((x - m) sc) stay under 2^kLazy, well
+            // inside fp16 for P and fp32 for the sums: the same softmax.
+            const float lmx = vmax3(vmax3(x[0], x[1], x[2]), vmax3(x[3], x[4], x[5]), fmaxf(x[6], x[7]));
+            if (__builtin_amdgcn_ballot_w64(lmx > mlim[r])) {
+                const float mx = row_group_max(lmx);
+                const float mn = fmaxf(m[r], mx);
+                const float alpha = mn > m[r] ? __builtin_amdgcn_exp2f((m[r] - mn) * sc) : 1.0f;
+                m[r] = mn;
+                mlim[r] = mn + lazy;
+                msc[r] = (mn == -INFINITY ? 0.0f : mn) * sc;
+                lsum[r] *= alpha;
+#pragma unroll
+                for (int t = 0; t < DT; ++t) o[r][t] *= alpha;
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) pop[r][e] = static_cast<_Float16>(__builtin_amdgcn_exp2f(fmaf(x[e], sc, -msc[r])));
+            lsum[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kOnes, pop[r], lsum[r], 0, 0, 0);
+        }
+    };
+    auto pv = [&](const char* vb, const int sub, const half8_t (&pop)[kRT]) __attribute__((always_inline)) {
+        // V^T operands by transposed reads of row-major V (lane m of group grp:
+        // key row 4 grp + m / 4 (+16), dims 16 t + 4 (m % 4) .. +3)
+        const int vrow = 32 * sub + 4 * grp + (col >> 2);
+        half8_t vop[DT];
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+            const int dcol = (16 * t + 4 * (col & 3)) * 2;
+            const u32x2 lo = tr_read(vb + T::off(vrow, dcol >> 4) + (dcol & 15));
+            const u32x2 hi = tr_read(vb + T::off(16 + vrow, dcol >> 4) + (dcol & 15));
+            vop[t] = __builtin_bit_cast(half8_t, u32x4{lo[0], lo[1], hi[0], hi[1]});
+        }
+#pragma unroll
+        for (int t = 0; t < DT; ++t)
+#pragma unroll
+            for (int r = 0; r < kRT; ++r) o[r][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop[t], pop[r], o[r][t], 0, 0, 0);
+    };
+
+    for (int t = 0; t < ntiles; ++t) {
+        lds_barrier();  // tile t published by the producer
+        if (computes) {
+            const char* kcur = tiles + (t % kStages) * STAGE;
+            const char* vcur = kcur + T::BYTES;
+            float4_t sa[kRT][2];
+            half8_t pa[kRT];
+            qk(kcur, 0, sa);
+            softmax(t * kBK, sa, pa);
+            pv(vcur, 0, pa);
+            if (t * kBK + 32 < kend) {
+                qk(kcur, 1, sa);
+                softmax(t * kBK + 32, sa, pa);
+                pv(vcur, 1, pa);
+            }
+        }
+    }
+
+    // ---------------- output: lane (row col) holds dims 16 t + 4 grp + e
+    if (!computes) return;
+#pragma unroll
+    for (int r = 0; r < kRT; ++r) {
+        const float lt = lsum[r][0];
+        const int j = qb * kBQ + 16 * r + col;
+        if (j >= qlen) continue;
+        const float inv = (rctx[r] > 0 && lt > 0.0f) ? 1.0f / lt : 0.0f;
+        _Float16* orow = a.out + ((int64_t(q0) + j) * a.num_heads + h) * D;
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+            const half2_t lo = {static_cast<_Float16>(o[r][t][0] * inv), static_cast<_Float16>(o[r][t][1] * inv)};
+            const half2_t hi = {static_cast<_Float16>(o[r][t][2] * inv), static_cast<_Float16>(o[r][t][3] * inv)};
+            *reinterpret_cast<u32x2*>(orow + 16 * t + 4 * grp) =
+                u32x2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
+        }
+    }
+}
+
+// Persistent workgroups over the item list, as prefill_mfma_kernel; the
+// barriers of the claim also end every wave's use of the tile buffers.
+template <int D>
+__global__ __launch_bounds__(64 * (kMaxComputeWaves + 1)) void prefill_dma_kernel(PrefillArgs a) {
+    __shared__ __attribute__((aligned(1024))) char tiles[kStages * 2 * DmaTile<D>::BYTES];
+    __shared__ int btc[kBtCache];
+    __shared__ int claimed;
+    const int count = a.item_count[0];
+    for (;;) {
+        if (threadIdx.x == 0) claimed = atomicAdd(a.item_count + 1 + blockIdx.z, 1);
+        __syncthreads();
+        const int it = claimed;
+        __syncthreads();
+        if (it >= count) break;
+        const int2 item = a.items[it];
+        prefill_block_dma<D>(a, item.x, item.y / a.num_kv_heads, item.y % a.num_kv_heads, tiles, btc);
     }
 }
 
@@ -450,6 +747,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void prefill_mfma_kernel(PrefillArg
 // through LDS atomics (the order within a level does not matter to the
 // results).  At most kMaxLevels levels (max_query_len <= 32 * kMaxLevels).
 constexpr int kMaxLevels = 4096;
+constexpr int kMaxHeadGroups = 63;  // claim counters after the item count (256-byte header)
 
 // Exclusive prefix sum of arr[0, n) in LDS by 256 threads (each a contiguous
 // tile, tiles combined with wave shuffles and one LDS step); returns the total.
@@ -509,10 +807,8 @@ __global__ __launch_bounds__(256) void prefill_items_kernel(const int32_t* qsl, 
     for (int L = tid; L < levels; L += 256) off[L] = (seqs - hist[L + 1]) * hkv;
     __syncthreads();
     const int total = block_exclusive_scan(off, levels, wave_tot);
-    if (tid == 0) {
-        count[0] = total;
-        count[1] = 0;  // claim counter of the prefill kernel
-    }
+    if (tid == 0) count[0] = total;
+    if (tid < kMaxHeadGroups) count[1 + tid] = 0;  // claim counters of the prefill kernel
     for (int s = tid; s < num_seqs; s += 256) {
         const int n = nqb(s);
         for (int L = 0; L < n; ++L) {
@@ -533,7 +829,8 @@ int ilog2i(int x) {
 bool prefill_mfma_supported(const vkv_prefill_params* p) {
     return p->io_dtype == VKV_DTYPE_F16 && (p->kv_dtype == VKV_DTYPE_F16 || p->kv_dtype == VKV_DTYPE_FP8_E4M3) &&
            (p->head_dim == 64 || p->head_dim == 128) && p->max_query_len >= 2 &&
-           (int64_t(p->max_query_len) + kBQ - 1) / kBQ <= kMaxLevels;
+           (int64_t(p->max_query_len) + kBQ - 1) / kBQ <= kMaxLevels &&
+           p->num_heads / p->num_kv_heads <= kMaxHeadGroups * kMaxComputeWaves;
 }
 
 size_t prefill_items_bytes(const vkv_prefill_params* p) {
@@ -556,7 +853,11 @@ int launch_prefill_mfma(const vkv_prefill_params* p, void* item_space, hipStream
     a.num_heads = p->num_heads;
     a.num_kv_heads = p->num_kv_heads;
     a.group = p->num_heads / p->num_kv_heads;
-    const int head_groups = (a.group + kMaxWaves - 1) / kMaxWaves;
+    // fp16 caches: up to kMaxComputeWaves heads + the producer wave per
+    // workgroup; FP8: up to kMaxWaves heads, the first 256 threads staging
+    const bool dma = p->kv_dtype == VKV_DTYPE_F16;
+    const int max_heads = dma ? kMaxComputeWaves : kMaxWaves;
+    const int head_groups = (a.group + max_heads - 1) / max_heads;
     a.heads_per_wg = (a.group + head_groups - 1) / head_groups;
     a.bs_log2 = ilog2i(p->block_size);
     a.max_blocks_per_seq = p->max_blocks_per_seq;
@@ -578,14 +879,14 @@ int launch_prefill_mfma(const vkv_prefill_params* p, void* item_space, hipStream
     if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     const int64_t upper = int64_t(p->num_seqs) * a.qblocks * p->num_kv_heads;
     const int64_t wgs = int64_t(cus) * 2 < upper ? int64_t(cus) * 2 : upper;
-    const int waves = a.heads_per_wg < kMinWaves ? kMinWaves : a.heads_per_wg;
+    const int waves = dma ? a.heads_per_wg + 1 : (a.heads_per_wg < kMinWaves ? kMinWaves : a.heads_per_wg);
     const dim3 grid(unsigned(wgs > 0 ? wgs : 1), 1u, unsigned(head_groups));
     const dim3 block(unsigned(64 * waves));
     if (p->head_dim == 128) {
-        if (p->kv_dtype == VKV_DTYPE_F16) hipLaunchKernelGGL((prefill_mfma_kernel<128, kF16>), grid, block, 0, st, a);
+        if (dma) hipLaunchKernelGGL((prefill_dma_kernel<128>), grid, block, 0, st, a);
         else hipLaunchKernelGGL((prefill_mfma_kernel<128, kFp8>), grid, block, 0, st, a);
     } else {
-        if (p->kv_dtype == VKV_DTYPE_F16) hipLaunchKernelGGL((prefill_mfma_kernel<64, kF16>), grid, block, 0, st, a);
+        if (dma) hipLaunchKernelGGL((prefill_dma_kernel<64>), grid, block, 0, st, a);
         else hipLaunchKernelGGL((prefill_mfma_kernel<64, kFp8>), grid, block, 0, st, a);
     }
     return 0;
