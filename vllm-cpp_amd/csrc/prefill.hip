@@ -22,14 +22,16 @@
 //                 never leaves the wave.
 // The output tile is O^T, again one row per lane, normalised at the end.
 //
-// Staging.  fp16 caches (prefill_dma_kernel): one extra producer wave loads
-// the tiles straight from global memory into LDS (global_load_lds, three tile
-// buffers, two tiles ahead), so the compute waves run no staging code.  FP8
-// caches (prefill_mfma_kernel): each of the first 256 threads loads its share
-// of the next tile's K and V rows into registers while the current tile is
-// computed, then writes them row-major into LDS (rows padded by 16 bytes to
-// spread the banks), dequantised on the way (code x per-token scale, fp32 ->
-// fp16).  Block ids of the sequence are cached in LDS, 1024 at a time.
+// fp16 caches (prefill_wide_kernel) use work items of (token, head) rows
+// instead, and stage tiles by direct global->LDS loads (global_load_lds,
+// three tile buffers, two tiles ahead) that every wave shares.
+//
+// Staging of FP8 caches (prefill_mfma_kernel): each of the first 256 threads
+// loads its share of the next tile's K and V rows into registers while the
+// current tile is computed, then writes them row-major into LDS (rows padded
+// by 16 bytes to spread the banks), dequantised on the way (code x per-token
+// scale, fp32 -> fp16).  Block ids of the sequence are cached in LDS, 1024 at
+// a time.
 #include <type_traits>
 
 #include "common.hpp"
@@ -439,20 +441,12 @@ __global__ __launch_bounds__(64 * kMaxWaves) void prefill_mfma_kernel(PrefillArg
 }
 
 // ---------------------------------------------------------------------------
-// fp16 caches: one producer wave stages the tiles by direct global->LDS loads.
+// fp16 caches: tiles staged by direct global->LDS loads.
 //
-// The workgroup is heads_per_wg compute waves plus one producer wave, which
-// keeps kStages tile buffers in flight: it loads tile t + 2 while the compute
-// waves work on tile t, and publishes tile t + 1 with the barrier that ends
-// tile t (its own loads counted out with s_waitcnt vmcnt before it).  So the
-// compute waves run no staging code and hold no staging registers, and a
-// load has two tiles of compute to land.  A direct load writes 1 KiB of LDS
-// per wave instruction (lane L -> bytes 16 L), so tile rows are unpadded:
-// 16-byte chunk c of key row r sits at slot c ^ (r % CH) (CH chunks per row),
-// which spreads the compute waves' reads of one chunk column over the banks.
-constexpr int kStages = 3;
-constexpr int kMaxComputeWaves = 7;  // + the producer: 8 waves, 2 per SIMD
-
+// A direct load writes 1 KiB of LDS per wave instruction (lane L -> bytes
+// 16 L), so tile rows are unpadded: 16-byte chunk c of key row r sits at slot
+// c ^ (r % CH) (CH chunks per row), which spreads the reads of one chunk
+// column by 16 lanes over the banks.
 template <int D>
 struct DmaTile {
     static constexpr int ROW = D * 2;        // bytes per key row
@@ -472,121 +466,123 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// Workgroup barrier that orders LDS only: the producer's direct loads are
-// counted out by wait_vmcnt before it, and every compute wave has consumed its
-// LDS reads (they feed the tile's MFMAs) before it arrives.
+// Workgroup barrier that orders LDS only: every wave counts its own direct
+// loads out with wait_vmcnt before it, and has consumed its LDS reads (they
+// feed the tile's MFMAs) before it arrives.
 __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// max(a, b, c) as v_maximum3_f32 (NaN-propagating, so no canonicalising
+// v_max_f32 x, x, x is inserted for operands that come from the matrix cores)
 __device__ __forceinline__ float vmax3(float a, float b, float c) {
-    float r;
-    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-    return r;
+    return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
 }
 
-// One work item on an fp16 cache: query block qb (kBQ tokens) of sequence s
-// against kv head kvh; wave heads_per_wg is the producer.
+// ---------------------------------------------------------------------------
+// fp16 caches: work items of (token, head) rows.
+//
+// A workgroup of kWideWaves waves owns (sequence, kv head, block of
+// Wide<D>::ROWS rows), where the rows of a (sequence, kv head) are its
+// (query token, head) pairs in the order j * G + g: each wave computes RT
+// 16-row MFMA tiles of any mix of heads and tokens, since every row keeps its
+// own context length and softmax state in its lane.  So every wave computes
+// whatever the group size (G = 1 included), and the G heads of a token still
+// share each K/V tile staged in LDS.  Each wave issues 1 / kWideWaves of the
+// direct global->LDS loads of every tile (tile t + 2 while tile t is
+// computed; the block ids one tile earlier still) and counts its own loads of
+// tile t + 1 out with s_waitcnt vmcnt before the barrier that publishes it.
+constexpr int kWideWaves = 8;  // two per SIMD
+constexpr int kWideStages = 3;
+// 16-row tiles per wave (what fits 256 registers) and (token, head) rows per item
 template <int D>
-__device__ __forceinline__ void prefill_block_dma(const PrefillArgs& a, const int s, const int qb, const int kvh,
-                                                  char* tiles, int* btc) {
+struct Wide {
+    static constexpr int RT = D == 128 ? 2 : 4;
+    static constexpr int ROWS = kWideWaves * RT * 16;
+};
+
+template <int D>
+__device__ __forceinline__ void prefill_block_wide(const PrefillArgs& a, const int s, const int b, const int kvh,
+                                                   char* tiles) {
     using T = DmaTile<D>;
     constexpr int DT = D / 16;  // output dim tiles
     constexpr int KS = D / 32;  // MFMA k-steps of Q K^T
-    constexpr int STAGE = 2 * T::BYTES;
+    constexpr int RT = Wide<D>::RT;
+    constexpr int kWideRows = Wide<D>::ROWS;
+    constexpr int JW = T::INST / kWideWaves;  // direct loads per K (or V) tile and wave
+    static_assert(T::INST % kWideWaves == 0, "the loads of a tile must split evenly over the waves");
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int col = lane & 15;
     const int grp = lane >> 4;
-    const bool producer = wave == a.heads_per_wg;
-    const int g = blockIdx.z * a.heads_per_wg + wave;
-    const bool computes = !producer && g < a.group;
+    const int G = a.group;
 
     const int q0 = a.qsl[s];
     const int qlen = a.qsl[s + 1] - q0;
-    if (qlen < 2 || qb * kBQ >= qlen) return;  // (the item list holds none of these)
+    const int nrows = qlen * G;
+    if (qlen < 2 || b * kWideRows >= nrows) return;  // (the item list holds none of these)
     const int prior = a.cl[s] - qlen;
-    const int jmax = min(qlen, qb * kBQ + kBQ);
-    int kend = prior + jmax;
+    const int last_row = min(nrows, (b + 1) * kWideRows) - 1;
+    int kend = prior + last_row / G + 1;  // keys any row of the block may see
     kend = kend < a.table_tokens ? kend : a.table_tokens;
     const int ntiles = kend > 0 ? (kend + kBK - 1) / kBK : 0;
 
-    if (producer) {
-        // ---------------- producer: tiles 0 and 1 ahead, then one per barrier
-        const int bs_mask = (1 << a.bs_log2) - 1;
-        const int64_t row_bytes = int64_t(a.num_kv_heads) * D * 2;
-        const int64_t head_off = int64_t(kvh) * D * 2;
-        const int32_t* table = a.bt + int64_t(s) * a.max_blocks_per_seq;
-        int win = -1;
-        auto produce = [&](const int t) __attribute__((always_inline)) {
-            const int k0 = t * kBK;
-            const int first = k0 >> a.bs_log2;
-            if (win < 0 || first + (kBK >> a.bs_log2) + 1 > win + kBtCache) {
-                // block ids cached in LDS (read by this wave only)
-                win = first;
-                for (int i = lane; i < kBtCache; i += 64) {
-                    const int b = win + i;
-                    int id = 0;
-                    if (b < a.max_blocks_per_seq) {
-                        id = table[b];
-                        if (a.num_blocks > 0 && unsigned(id) >= unsigned(a.num_blocks)) id = 0;
-                    }
-                    btc[i] = id;
-                }
-            }
-            char* kdst = tiles + (t % kStages) * STAGE;
-            char* vdst = kdst + T::BYTES;
-            int64_t slot[T::INST];  // cache slot of each instruction's key (block ids read first, together)
+    // ---------------- loads of tile t: block ids first (one tile ahead), then the rows
+    const int bs_mask = (1 << a.bs_log2) - 1;
+    const int64_t row_bytes = int64_t(a.num_kv_heads) * D * 2;
+    const int64_t head_off = int64_t(kvh) * D * 2;
+    const int32_t* table = a.bt + int64_t(s) * a.max_blocks_per_seq;
+    // key of this lane's row in load j of tile t (keys past the end: kend - 1 again, masked)
+    auto load_key = [&](const int t, const int j) __attribute__((always_inline)) {
+        const int k = t * kBK + (wave * JW + j) * T::RPI + lane / T::CH;
+        return k < kend ? k : kend - 1;
+    };
+    auto load_ids = [&](const int t, int (&ids)[JW]) __attribute__((always_inline)) {
 #pragma unroll
-            for (int j = 0; j < T::INST; ++j) {
-                int k = k0 + j * T::RPI + lane / T::CH;
-                k = k < kend ? k : kend - 1;  // past the end: key kend - 1 again (masked)
-                slot[j] = (int64_t(btc[(k >> a.bs_log2) - win]) << a.bs_log2) + (k & bs_mask);
-            }
+        for (int j = 0; j < JW; ++j) ids[j] = table[load_key(t, j) >> a.bs_log2];
+    };
+    auto load_tile = [&](const int t, const int (&ids)[JW]) __attribute__((always_inline)) {
+        char* kdst = tiles + (t % kWideStages) * T::BYTES;
+        char* vdst = tiles + (kWideStages + t % kWideStages) * T::BYTES;
 #pragma unroll
-            for (int j = 0; j < T::INST; ++j) {
-                const int row = j * T::RPI + lane / T::CH;
-                const int chunk = (lane % T::CH) ^ (row % T::CH);
-                const int64_t off = slot[j] * row_bytes + head_off + chunk * 16;
-                __builtin_amdgcn_global_load_lds(a.kc + off, (__attribute__((address_space(3))) void*)(kdst + j * 1024),
-                                                 16, 0, 0);
-                __builtin_amdgcn_global_load_lds(a.vc + off, (__attribute__((address_space(3))) void*)(vdst + j * 1024),
-                                                 16, 0, 0);
-            }
-        };
-        if (ntiles > 0) produce(0);
-        if (ntiles > 1) produce(1);
-        for (int t = 0; t < ntiles; ++t) {
-            if (t + 1 < ntiles) wait_vmcnt<2 * T::INST>();  // tile t landed, t + 1 may be in flight
-            else wait_vmcnt<0>();
-            lds_barrier();  // publishes tile t; every wave has left tile t - 1
-            if (t + 2 < ntiles) produce(t + 2);  // into the buffer of tile t - 1
+        for (int j = 0; j < JW; ++j) {
+            const int jj = wave * JW + j;
+            const int row = jj * T::RPI + lane / T::CH;
+            const int chunk = (lane % T::CH) ^ (row % T::CH);
+            int id = ids[j];
+            if (a.num_blocks > 0 && unsigned(id) >= unsigned(a.num_blocks)) id = 0;
+            const int64_t slot = (int64_t(id) << a.bs_log2) + (load_key(t, j) & bs_mask);
+            const int64_t off = slot * row_bytes + head_off + chunk * 16;
+            __builtin_amdgcn_global_load_lds(a.kc + off, (__attribute__((address_space(3))) void*)(kdst + jj * 1024),
+                                             16, 0, 0);
+            __builtin_amdgcn_global_load_lds(a.vc + off, (__attribute__((address_space(3))) void*)(vdst + jj * 1024),
+                                             16, 0, 0);
         }
-        return;
-    }
+    };
 
-    // ---------------- compute waves: Q (B operand of S^T = K Q^T) and per-row context
-    const int h = kvh * a.group + g;
+    // ---------------- Q (B operand of S^T = K Q^T) and per-row context; row
+    // rho = b * ROWS + 16 (RT wave + r) + col is (token rho / G, head rho % G)
     const bool neg_scale = a.scale_log2 < 0.0f;
     const float sc = neg_scale ? -a.scale_log2 : a.scale_log2;
-    half8_t qop[kRT][KS];
-    int rctx[kRT];
+    half8_t qop[RT][KS];
+    int rctx[RT];
 #pragma unroll
-    for (int r = 0; r < kRT; ++r) {
-        const int j = qb * kBQ + 16 * r + col;
+    for (int r = 0; r < RT; ++r) {
+        const int rho = b * kWideRows + 16 * RT * wave + 16 * r + col;
+        const bool ok = rho < nrows;
+        const int j = ok ? rho / G : 0;
+        const int h = kvh * G + (ok ? rho - j * G : 0);
         int c = prior + j + 1;
         c = c < 0 ? 0 : (c > a.table_tokens ? a.table_tokens : c);
-        rctx[r] = (j < qlen) ? c : 0;
+        rctx[r] = ok ? c : 0;
+        const int64_t qbase = (int64_t(q0) + j) * a.q_stride + int64_t(h) * D;
 #pragma unroll
         for (int i = 0; i < KS; ++i) {
-            const bool ok = computes && j < qlen;
-            const int64_t qrow = ok ? int64_t(q0) + j : int64_t(q0);
-            const int64_t qcol = ok ? int64_t(h) * D : 0;
-            u32x4 w = load16(a.q + (qrow * a.q_stride + qcol + 32 * i + 8 * grp) * 2);
+            u32x4 w = load16(a.q + (qbase + 32 * i + 8 * grp) * 2);
             const uint32_t keep = ok ? 0xFFFFFFFFu : 0u;
             const uint32_t flip = neg_scale ? 0x80008000u : 0u;
             w = (w ^ u32x4{flip, flip, flip, flip}) & u32x4{keep, keep, keep, keep};
@@ -594,13 +590,22 @@ __device__ __forceinline__ void prefill_block_dma(const PrefillArgs& a, const in
         }
     }
 
+    // Loads of tiles 0 and 1 and the block ids of tile 2 (every wave issues
+    // them, also for tiles past the end, so the vmcnt counts below are exact).
+    int ids_a[JW], ids_b[JW];
+    load_ids(0, ids_a);
+    load_ids(1, ids_b);
+    load_tile(0, ids_a);
+    load_tile(1, ids_b);
+    load_ids(2, ids_a);
+
     const float lazy = kLazy / sc;  // kLazy in raw (unscaled) logit units
-    float m[kRT], mlim[kRT], msc[kRT];
-    float4_t lsum[kRT];  // row sums (every element the same)
-    float4_t o[kRT][DT];
+    float m[RT], mlim[RT], msc[RT];
+    float4_t lsum[RT];  // row sums (every element the same)
+    float4_t o[RT][DT];
     const half8_t kOnes = {1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16};
 #pragma unroll
-    for (int r = 0; r < kRT; ++r) {
+    for (int r = 0; r < RT; ++r) {
         m[r] = -INFINITY;
         mlim[r] = -INFINITY;  // m + lazy
         msc[r] = 0.0f;        // m * sc, 0 while the row has no key
@@ -609,104 +614,135 @@ __device__ __forceinline__ void prefill_block_dma(const PrefillArgs& a, const in
         for (int t = 0; t < DT; ++t) o[r][t] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
     }
 
-    auto qk = [&](const char* kb, const int sub, float4_t (&sv)[kRT][2]) __attribute__((always_inline)) {
-        half8_t kop[2][KS];
+    // This lane's LDS byte offsets within a step's K (V) rows.  The swizzle of
+    // row r depends on r % CH only, and the rows this lane reads differ by
+    // multiples of 16 (CH divides 16), so the other row halves and steps are
+    // constant offsets.  K operand: row col (+16 hh), chunk 4 i + grp.  V^T
+    // operand (transposed reads; lane m of group grp: key row 4 grp + m / 4
+    // (+16), dims 16 t + 4 (m % 4) .. +3): chunk 2 t + (m % 4) / 2.
+    int koff[KS], voff[DT];
+    const int vrow = 4 * grp + (col >> 2);
 #pragma unroll
-        for (int hh = 0; hh < 2; ++hh)
+    for (int i = 0; i < KS; ++i) koff[i] = T::off(col, 4 * i + grp);
 #pragma unroll
-            for (int i = 0; i < KS; ++i)
-                kop[hh][i] = __builtin_bit_cast(
-                    half8_t, *reinterpret_cast<const u32x4*>(kb + T::off(32 * sub + 16 * hh + col, 4 * i + grp)));
+    for (int t = 0; t < DT; ++t) voff[t] = T::off(vrow, 2 * t + ((col & 3) >> 1)) + 8 * (col & 1);
+
+    auto qk = [&](const char* kb, float4_t (&sv)[RT][2]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int r = 0; r < kRT; ++r) sv[r][0] = sv[r][1] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int r = 0; r < RT; ++r) sv[r][0] = sv[r][1] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int i = 0; i < KS; ++i)
 #pragma unroll
-            for (int hh = 0; hh < 2; ++hh)
+            for (int hh = 0; hh < 2; ++hh) {
+                const half8_t kop =
+                    __builtin_bit_cast(half8_t, *reinterpret_cast<const u32x4*>(kb + koff[i] + 16 * hh * T::ROW));
 #pragma unroll
-                for (int r = 0; r < kRT; ++r)
-                    sv[r][hh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop[hh][i], qop[r][i], sv[r][hh], 0, 0, 0);
+                for (int r = 0; r < RT; ++r)
+                    sv[r][hh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qop[r][i], sv[r][hh], 0, 0, 0);
+            }
     };
-    auto softmax = [&](const int kbase, const float4_t (&sv)[kRT][2], half8_t (&pop)[kRT]) __attribute__((always_inline)) {
+    auto softmax = [&](const int kbase, float4_t (&sv)[RT][2], half8_t (&pop)[RT]) __attribute__((always_inline)) {
+        // causal / context mask, only on steps that reach past some row's
+        // context (wave-uniform test): key kbase + 16 hh + 4 grp + e < rctx
+        bool edge = false;
 #pragma unroll
-        for (int r = 0; r < kRT; ++r) {
-            float x[8];
+        for (int r = 0; r < RT; ++r) edge = edge || kbase + 32 > rctx[r];
+        if (__builtin_amdgcn_ballot_w64(edge)) {
 #pragma unroll
-            for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) x[4 * hh + e] = sv[r][hh][e];
-            if (__builtin_amdgcn_ballot_w64(kbase + 32 > rctx[r])) {
+            for (int r = 0; r < RT; ++r)
 #pragma unroll
                 for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
-                        if (kbase + 16 * hh + 4 * grp + e >= rctx[r]) x[4 * hh + e] = -INFINITY;
-            }
-            // This lane's max decides whether the row max is needed at all: it
-            // is only when some lane exceeds the lazy limit m + kLazy (then the
-            // max over the row's four key groups resets m and rescales).  Below
-            // the limit the weights exp2((x - m) sc) stay under 2^kLazy, well
-            // inside fp16 for P and fp32 for the sums: the same softmax.
-            const float lmx = vmax3(vmax3(x[0], x[1], x[2]), vmax3(x[3], x[4], x[5]), fmaxf(x[6], x[7]));
-            if (__builtin_amdgcn_ballot_w64(lmx > mlim[r])) {
-                const float mx = row_group_max(lmx);
-                const float mn = fmaxf(m[r], mx);
-                const float alpha = mn > m[r] ? __builtin_amdgcn_exp2f((m[r] - mn) * sc) : 1.0f;
-                m[r] = mn;
-                mlim[r] = mn + lazy;
-                msc[r] = (mn == -INFINITY ? 0.0f : mn) * sc;
-                lsum[r] *= alpha;
+                        if (kbase + 16 * hh + 4 * grp + e >= rctx[r]) sv[r][hh][e] = -INFINITY;
+        }
+        // This lane's max decides whether the row max is needed at all: it is
+        // only when some lane exceeds the lazy limit m + kLazy (then the max
+        // over the row's four key groups resets m and rescales).  Below the
+        // limit the weights exp2((x - m) sc) stay under 2^kLazy, well inside
+        // fp16 for P and fp32 for the sums: the same softmax.
+        float lmx[RT];
+        bool over = false;
 #pragma unroll
-                for (int t = 0; t < DT; ++t) o[r][t] *= alpha;
-            }
+        for (int r = 0; r < RT; ++r) {
+            lmx[r] = vmax3(vmax3(sv[r][0][0], sv[r][0][1], sv[r][0][2]), vmax3(sv[r][0][3], sv[r][1][0], sv[r][1][1]),
+                           vmax3(sv[r][1][2], sv[r][1][3], sv[r][1][3]));
+            over = over || lmx[r] > mlim[r];
+        }
+        if (__builtin_amdgcn_ballot_w64(over)) {
 #pragma unroll
-            for (int e = 0; e < 8; ++e) pop[r][e] = static_cast<_Float16>(__builtin_amdgcn_exp2f(fmaf(x[e], sc, -msc[r])));
+            for (int r = 0; r < RT; ++r) {
+                if (__builtin_amdgcn_ballot_w64(lmx[r] > mlim[r])) {
+                    const float mx = row_group_max(lmx[r]);
+                    const float mn = fmaxf(m[r], mx);
+                    const float alpha = mn > m[r] ? __builtin_amdgcn_exp2f((m[r] - mn) * sc) : 1.0f;
+                    m[r] = mn;
+                    mlim[r] = mn + lazy;
+                    msc[r] = (mn == -INFINITY ? 0.0f : mn) * sc;
+                    lsum[r] *= alpha;
+#pragma unroll
+                    for (int t = 0; t < DT; ++t) o[r][t] *= alpha;
+                }
+            }
+        }
+        // P^T operand: k slot (grp, e) = key 4 grp + e, slot (grp, 4 + e) = key 16 + 4 grp + e
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    pop[r][4 * hh + e] =
+                        static_cast<_Float16>(__builtin_amdgcn_exp2f(fmaf(sv[r][hh][e], sc, -msc[r])));
+            // row sums on the matrix pipe: a V^T tile of ones gives sum_k p in every lane
             lsum[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kOnes, pop[r], lsum[r], 0, 0, 0);
         }
     };
-    auto pv = [&](const char* vb, const int sub, const half8_t (&pop)[kRT]) __attribute__((always_inline)) {
-        // V^T operands by transposed reads of row-major V (lane m of group grp:
-        // key row 4 grp + m / 4 (+16), dims 16 t + 4 (m % 4) .. +3)
-        const int vrow = 32 * sub + 4 * grp + (col >> 2);
-        half8_t vop[DT];
+    auto pv = [&](const char* vb, const half8_t (&pop)[RT]) __attribute__((always_inline)) {
 #pragma unroll
         for (int t = 0; t < DT; ++t) {
-            const int dcol = (16 * t + 4 * (col & 3)) * 2;
-            const u32x2 lo = tr_read(vb + T::off(vrow, dcol >> 4) + (dcol & 15));
-            const u32x2 hi = tr_read(vb + T::off(16 + vrow, dcol >> 4) + (dcol & 15));
-            vop[t] = __builtin_bit_cast(half8_t, u32x4{lo[0], lo[1], hi[0], hi[1]});
+            const u32x2 lo = tr_read(vb + voff[t]);
+            const u32x2 hi = tr_read(vb + voff[t] + 16 * T::ROW);
+            const half8_t vop = __builtin_bit_cast(half8_t, u32x4{lo[0], lo[1], hi[0], hi[1]});
+#pragma unroll
+            for (int r = 0; r < RT; ++r) o[r][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, pop[r], o[r][t], 0, 0, 0);
         }
-#pragma unroll
-        for (int t = 0; t < DT; ++t)
-#pragma unroll
-            for (int r = 0; r < kRT; ++r) o[r][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop[t], pop[r], o[r][t], 0, 0, 0);
     };
 
+    wait_vmcnt<JW + 2 * JW>();  // tile 0 landed (tile 1's loads and tile 2's ids may be in flight)
     for (int t = 0; t < ntiles; ++t) {
-        lds_barrier();  // tile t published by the producer
-        if (computes) {
-            const char* kcur = tiles + (t % kStages) * STAGE;
-            const char* vcur = kcur + T::BYTES;
-            float4_t sa[kRT][2];
-            half8_t pa[kRT];
-            qk(kcur, 0, sa);
-            softmax(t * kBK, sa, pa);
-            pv(vcur, 0, pa);
-            if (t * kBK + 32 < kend) {
-                qk(kcur, 1, sa);
-                softmax(t * kBK + 32, sa, pa);
-                pv(vcur, 1, pa);
-            }
+        lds_barrier();  // tile t published; every wave has left tile t - 1
+        // ids of tile t + 3 into the registers freed by tile t + 2's loads
+        // (issued first, so that waiting for them never waits for tile t + 1)
+        int ids_n[JW];
+        load_ids(t + 3, ids_n);
+        load_tile(t + 2, ids_a);  // into the buffer of tile t - 1
+#pragma unroll
+        for (int j = 0; j < JW; ++j) ids_a[j] = ids_n[j];
+        const char* kcur = tiles + (t % kWideStages) * T::BYTES;
+        const char* vcur = tiles + (kWideStages + t % kWideStages) * T::BYTES;
+        float4_t sv[RT][2];
+        half8_t pop[RT];
+        qk(kcur, sv);
+        softmax(t * kBK, sv, pop);
+        pv(vcur, pop);
+        if (t * kBK + 32 < kend) {
+            qk(kcur + 32 * T::ROW, sv);
+            softmax(t * kBK + 32, sv, pop);
+            pv(vcur + 32 * T::ROW, pop);
         }
+        wait_vmcnt<JW + 2 * JW>();  // tile t + 1 landed (ids of t + 3, loads of t + 2 may be in flight)
     }
+    wait_vmcnt<0>();  // no load of this item may land in the next item's buffers
 
     // ---------------- output: lane (row col) holds dims 16 t + 4 grp + e
-    if (!computes) return;
 #pragma unroll
-    for (int r = 0; r < kRT; ++r) {
+    for (int r = 0; r < RT; ++r) {
+        const int rho = b * kWideRows + 16 * RT * wave + 16 * r + col;
+        if (rho >= nrows) continue;
+        const int j = rho / G;
+        const int h = kvh * G + rho - j * G;
         const float lt = lsum[r][0];
-        const int j = qb * kBQ + 16 * r + col;
-        if (j >= qlen) continue;
         const float inv = (rctx[r] > 0 && lt > 0.0f) ? 1.0f / lt : 0.0f;
         _Float16* orow = a.out + ((int64_t(q0) + j) * a.num_heads + h) * D;
 #pragma unroll
@@ -719,22 +755,19 @@ __device__ __forceinline__ void prefill_block_dma(const PrefillArgs& a, const in
     }
 }
 
-// Persistent workgroups over the item list, as prefill_mfma_kernel; the
-// barriers of the claim also end every wave's use of the tile buffers.
 template <int D>
-__global__ __launch_bounds__(64 * (kMaxComputeWaves + 1)) void prefill_dma_kernel(PrefillArgs a) {
-    __shared__ __attribute__((aligned(1024))) char tiles[kStages * 2 * DmaTile<D>::BYTES];
-    __shared__ int btc[kBtCache];
+__global__ __launch_bounds__(64 * kWideWaves) void prefill_wide_kernel(PrefillArgs a) {
+    __shared__ __attribute__((aligned(1024))) char tiles[kWideStages * 2 * DmaTile<D>::BYTES];
     __shared__ int claimed;
     const int count = a.item_count[0];
     for (;;) {
-        if (threadIdx.x == 0) claimed = atomicAdd(a.item_count + 1 + blockIdx.z, 1);
+        if (threadIdx.x == 0) claimed = atomicAdd(a.item_count + 1, 1);
         __syncthreads();
         const int it = claimed;
         __syncthreads();
         if (it >= count) break;
         const int2 item = a.items[it];
-        prefill_block_dma<D>(a, item.x, item.y / a.num_kv_heads, item.y % a.num_kv_heads, tiles, btc);
+        prefill_block_wide<D>(a, item.x, item.y / a.num_kv_heads, item.y % a.num_kv_heads, tiles);
     }
 }
 
@@ -782,6 +815,7 @@ __device__ int block_exclusive_scan(int* arr, int n, int* wave_tot) {
 }
 
 __global__ __launch_bounds__(256) void prefill_items_kernel(const int32_t* qsl, int32_t num_seqs, int32_t hkv,
+                                                            int32_t row_mult, int32_t rows_per_item,
                                                             int32_t max_qblocks, int2* items, int32_t* count) {
     __shared__ int hist[kMaxLevels + 1];  // sequences with exactly n blocks, then its prefix sums
     __shared__ int off[kMaxLevels];       // items per level, then level offsets
@@ -794,7 +828,7 @@ __global__ __launch_bounds__(256) void prefill_items_kernel(const int32_t* qsl, 
     __syncthreads();
     auto nqb = [&](int s) {
         const int q = qsl[s + 1] - qsl[s];
-        const int n = q >= 2 ? (q + kBQ - 1) / kBQ : 0;
+        const int n = q >= 2 ? int((int64_t(q) * row_mult + rows_per_item - 1) / rows_per_item) : 0;
         return n < levels ? n : levels;  // max_query_len bounds q_len (caller contract)
     };
     for (int s = tid; s < num_seqs; s += 256) {
@@ -830,7 +864,7 @@ bool prefill_mfma_supported(const vkv_prefill_params* p) {
     return p->io_dtype == VKV_DTYPE_F16 && (p->kv_dtype == VKV_DTYPE_F16 || p->kv_dtype == VKV_DTYPE_FP8_E4M3) &&
            (p->head_dim == 64 || p->head_dim == 128) && p->max_query_len >= 2 &&
            (int64_t(p->max_query_len) + kBQ - 1) / kBQ <= kMaxLevels &&
-           p->num_heads / p->num_kv_heads <= kMaxHeadGroups * kMaxComputeWaves;
+           p->num_heads / p->num_kv_heads <= kMaxHeadGroups * kMaxWaves;
 }
 
 size_t prefill_items_bytes(const vkv_prefill_params* p) {
@@ -853,18 +887,19 @@ int launch_prefill_mfma(const vkv_prefill_params* p, void* item_space, hipStream
     a.num_heads = p->num_heads;
     a.num_kv_heads = p->num_kv_heads;
     a.group = p->num_heads / p->num_kv_heads;
-    // fp16 caches: up to kMaxComputeWaves heads + the producer wave per
-    // workgroup; FP8: up to kMaxWaves heads, the first 256 threads staging
-    const bool dma = p->kv_dtype == VKV_DTYPE_F16;
-    const int max_heads = dma ? kMaxComputeWaves : kMaxWaves;
-    const int head_groups = (a.group + max_heads - 1) / max_heads;
+    // fp16 caches: prefill_wide_kernel, Wide<D>::ROWS (token, head) rows per item;
+    // FP8: prefill_mfma_kernel, up to kMaxWaves heads x kBQ tokens per item
+    const bool wide = p->kv_dtype == VKV_DTYPE_F16;
+    const int head_groups = wide ? 1 : (a.group + kMaxWaves - 1) / kMaxWaves;
     a.heads_per_wg = (a.group + head_groups - 1) / head_groups;
     a.bs_log2 = ilog2i(p->block_size);
     a.max_blocks_per_seq = p->max_blocks_per_seq;
     a.num_blocks = p->num_blocks;
     const int64_t tt = int64_t(p->max_blocks_per_seq) * p->block_size;
     a.table_tokens = int32_t(tt > 0x7FFFFFFF ? 0x7FFFFFFF : tt);
-    a.qblocks = (p->max_query_len + kBQ - 1) / kBQ;
+    const int row_mult = wide ? a.group : 1;
+    const int rows_per_item = wide ? (p->head_dim == 128 ? Wide<128>::ROWS : Wide<64>::ROWS) : kBQ;
+    a.qblocks = int((int64_t(p->max_query_len) * row_mult + rows_per_item - 1) / rows_per_item);
     a.num_seqs = p->num_seqs;
     a.scale_log2 = p->scale * 1.4426950408889634f;
     int32_t* count = static_cast<int32_t*>(item_space);
@@ -872,21 +907,24 @@ int launch_prefill_mfma(const vkv_prefill_params* p, void* item_space, hipStream
     a.items = items;
     a.item_count = count;
     hipLaunchKernelGGL(prefill_items_kernel, dim3(1), dim3(256), 0, st, p->query_start_loc, p->num_seqs,
-                       p->num_kv_heads, a.qblocks, items, count);
-    // Persistent grid: two workgroups per CU (at D = 128 one is resident, the
-    // other starts when a CU frees up), never more than there can be items.
+                       p->num_kv_heads, row_mult, rows_per_item, a.qblocks, items, count);
+    // Persistent grid, never more workgroups than there can be items: one per
+    // CU for the wide kernel (its LDS and registers fill a CU); two per CU for
+    // the FP8 kernel (at D = 128 one is resident, the other starts when a CU
+    // frees up).
     int dev = 0, cus = 256;
     if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     const int64_t upper = int64_t(p->num_seqs) * a.qblocks * p->num_kv_heads;
-    const int64_t wgs = int64_t(cus) * 2 < upper ? int64_t(cus) * 2 : upper;
-    const int waves = dma ? a.heads_per_wg + 1 : (a.heads_per_wg < kMinWaves ? kMinWaves : a.heads_per_wg);
+    const int64_t per_cu = wide ? 1 : 2;
+    const int64_t wgs = int64_t(cus) * per_cu < upper ? int64_t(cus) * per_cu : upper;
+    const int waves = wide ? kWideWaves : (a.heads_per_wg < kMinWaves ? kMinWaves : a.heads_per_wg);
     const dim3 grid(unsigned(wgs > 0 ? wgs : 1), 1u, unsigned(head_groups));
     const dim3 block(unsigned(64 * waves));
     if (p->head_dim == 128) {
-        if (dma) hipLaunchKernelGGL((prefill_dma_kernel<128>), grid, block, 0, st, a);
+        if (wide) hipLaunchKernelGGL((prefill_wide_kernel<128>), grid, block, 0, st, a);
         else hipLaunchKernelGGL((prefill_mfma_kernel<128, kFp8>), grid, block, 0, st, a);
     } else {
-        if (dma) hipLaunchKernelGGL((prefill_dma_kernel<64>), grid, block, 0, st, a);
+        if (wide) hipLaunchKernelGGL((prefill_wide_kernel<64>), grid, block, 0, st, a);
         else hipLaunchKernelGGL((prefill_mfma_kernel<64, kFp8>), grid, block, 0, st, a);
     }
     return 0;
