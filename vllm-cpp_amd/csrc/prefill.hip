@@ -533,8 +533,15 @@ __device__ __forceinline__ void prefill_block_wide(const PrefillArgs& a, const i
 
     // ---------------- loads of tile t: block ids first (one tile ahead), then the rows
     const int bs_mask = (1 << a.bs_log2) - 1;
-    const int64_t row_bytes = int64_t(a.num_kv_heads) * D * 2;
-    const int64_t head_off = int64_t(kvh) * D * 2;
+    const uint32_t row_bytes32 = uint32_t(a.num_kv_heads) * D * 2;
+    // this lane's bytes within the cache row of its load j: the kv head and
+    // the chunk that the swizzle puts at its LDS slot (the same in every tile)
+    uint32_t lane_off[JW];
+#pragma unroll
+    for (int j = 0; j < JW; ++j) {
+        const int row = (wave * JW + j) * T::RPI + lane / T::CH;
+        lane_off[j] = uint32_t(kvh) * D * 2 + uint32_t(((lane % T::CH) ^ (row % T::CH)) * 16);
+    }
     const int32_t* table = a.bt + int64_t(s) * a.max_blocks_per_seq;
     // key of this lane's row in load j of tile t (keys past the end: kend - 1 again, masked)
     auto load_key = [&](const int t, const int j) __attribute__((always_inline)) {
@@ -545,18 +552,18 @@ __device__ __forceinline__ void prefill_block_wide(const PrefillArgs& a, const i
 #pragma unroll
         for (int j = 0; j < JW; ++j) ids[j] = table[load_key(t, j) >> a.bs_log2];
     };
-    auto load_tile = [&](const int t, const int (&ids)[JW]) __attribute__((always_inline)) {
-        char* kdst = tiles + (t % kWideStages) * T::BYTES;
-        char* vdst = tiles + (kWideStages + t % kWideStages) * T::BYTES;
+    // (slots are int32 in the API: slot_mapping, num_blocks * block_size)
+    auto load_tile = [&](auto stage, const int t, const int (&ids)[JW]) __attribute__((always_inline)) {
+        constexpr int S = decltype(stage)::value;
+        char* kdst = tiles + S * T::BYTES;
+        char* vdst = tiles + (kWideStages + S) * T::BYTES;
 #pragma unroll
         for (int j = 0; j < JW; ++j) {
             const int jj = wave * JW + j;
-            const int row = jj * T::RPI + lane / T::CH;
-            const int chunk = (lane % T::CH) ^ (row % T::CH);
             int id = ids[j];
             if (a.num_blocks > 0 && unsigned(id) >= unsigned(a.num_blocks)) id = 0;
-            const int64_t slot = (int64_t(id) << a.bs_log2) + (load_key(t, j) & bs_mask);
-            const int64_t off = slot * row_bytes + head_off + chunk * 16;
+            const uint32_t slot = (uint32_t(id) << a.bs_log2) + uint32_t(load_key(t, j) & bs_mask);
+            const uint64_t off = uint64_t(slot) * row_bytes32 + lane_off[j];
             __builtin_amdgcn_global_load_lds(a.kc + off, (__attribute__((address_space(3))) void*)(kdst + jj * 1024),
                                              16, 0, 0);
             __builtin_amdgcn_global_load_lds(a.vc + off, (__attribute__((address_space(3))) void*)(vdst + jj * 1024),
@@ -595,8 +602,8 @@ __device__ __forceinline__ void prefill_block_wide(const PrefillArgs& a, const i
     int ids_a[JW], ids_b[JW];
     load_ids(0, ids_a);
     load_ids(1, ids_b);
-    load_tile(0, ids_a);
-    load_tile(1, ids_b);
+    load_tile(std::integral_constant<int, 0>(), 0, ids_a);
+    load_tile(std::integral_constant<int, 1>(), 1, ids_b);
     load_ids(2, ids_a);
 
     const float lazy = kLazy / sc;  // kLazy in raw (unscaled) logit units
@@ -641,13 +648,15 @@ __device__ __forceinline__ void prefill_block_wide(const PrefillArgs& a, const i
                     sv[r][hh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qop[r][i], sv[r][hh], 0, 0, 0);
             }
     };
-    auto softmax = [&](const int kbase, float4_t (&sv)[RT][2], half8_t (&pop)[RT]) __attribute__((always_inline)) {
-        // causal / context mask, only on steps that reach past some row's
-        // context (wave-uniform test): key kbase + 16 hh + 4 grp + e < rctx
+    auto softmax = [&](auto masked, const int kbase, float4_t (&sv)[RT][2], half8_t (&pop)[RT])
+                       __attribute__((always_inline)) {
+        // causal / context mask, on the tiles of the masked tail only, and
+        // there on steps that reach past some row's context (wave-uniform
+        // test): key kbase + 16 hh + 4 grp + e < rctx
         bool edge = false;
 #pragma unroll
         for (int r = 0; r < RT; ++r) edge = edge || kbase + 32 > rctx[r];
-        if (__builtin_amdgcn_ballot_w64(edge)) {
+        if (decltype(masked)::value && __builtin_amdgcn_ballot_w64(edge)) {
 #pragma unroll
             for (int r = 0; r < RT; ++r)
 #pragma unroll
@@ -709,29 +718,53 @@ __device__ __forceinline__ void prefill_block_wide(const PrefillArgs& a, const i
         }
     };
 
-    wait_vmcnt<JW + 2 * JW>();  // tile 0 landed (tile 1's loads and tile 2's ids may be in flight)
-    for (int t = 0; t < ntiles; ++t) {
+    // One tile t in buffer S = t % kWideStages (a compile-time constant, so
+    // that every LDS address is a per-lane register plus an immediate);
+    // masked: the causal / context mask may cut into the tile.
+    auto tile = [&](auto stage, auto masked, const int t) __attribute__((always_inline)) {
+        constexpr int S = decltype(stage)::value;
         lds_barrier();  // tile t published; every wave has left tile t - 1
         // ids of tile t + 3 into the registers freed by tile t + 2's loads
         // (issued first, so that waiting for them never waits for tile t + 1)
         int ids_n[JW];
         load_ids(t + 3, ids_n);
-        load_tile(t + 2, ids_a);  // into the buffer of tile t - 1
+        load_tile(std::integral_constant<int, (S + 2) % kWideStages>(), t + 2, ids_a);  // buffer of tile t - 1
 #pragma unroll
         for (int j = 0; j < JW; ++j) ids_a[j] = ids_n[j];
-        const char* kcur = tiles + (t % kWideStages) * T::BYTES;
-        const char* vcur = tiles + (kWideStages + t % kWideStages) * T::BYTES;
+        const char* kcur = tiles + S * T::BYTES;
+        const char* vcur = tiles + (kWideStages + S) * T::BYTES;
         float4_t sv[RT][2];
         half8_t pop[RT];
         qk(kcur, sv);
-        softmax(t * kBK, sv, pop);
+        softmax(masked, t * kBK, sv, pop);
         pv(vcur, pop);
-        if (t * kBK + 32 < kend) {
+        if (!decltype(masked)::value || t * kBK + 32 < kend) {
             qk(kcur + 32 * T::ROW, sv);
-            softmax(t * kBK + 32, sv, pop);
+            softmax(masked, t * kBK + 32, sv, pop);
             pv(vcur + 32 * T::ROW, pop);
         }
         wait_vmcnt<JW + 2 * JW>();  // tile t + 1 landed (ids of t + 3, loads of t + 2 may be in flight)
+    };
+    using C0 = std::integral_constant<int, 0>;
+    using C1 = std::integral_constant<int, 1>;
+    using C2 = std::integral_constant<int, 2>;
+    static_assert(kWideStages == 3, "the main loop below is unrolled over three buffers");
+    // Tiles below every row's context need no mask: the first row of the item
+    // has the shortest context.
+    const int ctx_min = min(prior + (b * kWideRows) / G + 1, kend);
+    const int tfull = ctx_min / kBK;
+    wait_vmcnt<JW + 2 * JW>();  // tile 0 landed (tile 1's loads and tile 2's ids may be in flight)
+    int t = 0;
+    for (; t + 3 <= tfull; t += 3) {
+        tile(C0(), std::false_type(), t);
+        tile(C1(), std::false_type(), t + 1);
+        tile(C2(), std::false_type(), t + 2);
+    }
+    for (; t < ntiles; ++t) {
+        const int sidx = t % kWideStages;
+        if (sidx == 0) tile(C0(), std::true_type(), t);
+        else if (sidx == 1) tile(C1(), std::true_type(), t);
+        else tile(C2(), std::true_type(), t);
     }
     wait_vmcnt<0>();  // no load of this item may land in the next item's buffers
 
