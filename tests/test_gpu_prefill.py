@@ -35,6 +35,9 @@ def _case(H, Hkv, D, bs, q_lens, prior, seed):
     (8, 8, 64, 8, [70, 2], [9000, 5]),              # MHA; 1131 blocks: block-id window reloads
     (16, 4, 128, 64, [33, 1, 100], [64, 0, 129]),   # blocks larger than a key tile
     (12, 4, 128, 16, [2, 31, 32, 65], [0, 1, 15, 300]),
+    # groups 5 and 6: 256-row work items end inside a token's heads
+    (10, 2, 128, 16, [77, 1, 300, 52], [3, 40, 129, 0]),
+    (24, 4, 64, 32, [129, 7, 1, 250], [600, 0, 33, 64]),
 ])
 def test_prefill_vs_oracle(vkv, oracle, cuda, H, Hkv, D, bs, q_lens, prior):
     import torch
@@ -69,6 +72,24 @@ def test_prefill_fp8_vs_oracle(vkv, oracle, cuda, H, Hkv, D, bs):
     ref = oracle.paged_prefill(q.astype(np.float32), to_np(kc), to_np(vc), lay.block_tables, ctx, qsl, scale,
                                key_scales=to_np(ks), value_scales=to_np(vs))
     assert_close(to_np(out).astype(np.float32), ref, F16_ATOL, F16_RTOL, "fp8 prefill")
+
+
+def test_prefill_many_items(vkv, oracle, cuda):
+    """More work items than persistent workgroups (items claimed in turn), ragged lengths."""
+    import torch
+    rng = np.random.default_rng(11)
+    S = 24  # ~290 items of 256 (token, head) rows
+    q_lens = rng.integers(2, 200, S).tolist()
+    prior = rng.integers(0, 300, S).tolist()
+    H, Hkv, D, bs = 28, 4, 128, 16
+    lay, ctx, qsl, q, k, v, scale = _case(H, Hkv, D, bs, q_lens, prior, 5)
+    ref = oracle.paged_prefill(q.astype(np.float32), k.view(np.uint16), v.view(np.uint16), lay.block_tables,
+                               ctx, qsl, scale, nthreads=8)
+    out = torch.zeros((q.shape[0], H, D), dtype=torch.float16, device=cuda)
+    vkv.paged_prefill(out, to_dev(q, cuda), to_dev(k, cuda), to_dev(v, cuda), to_dev(lay.block_tables, cuda),
+                      to_dev(ctx, cuda), to_dev(qsl, cuda), int(max(q_lens)), scale)
+    torch.cuda.synchronize()
+    assert_close(to_np(out).astype(np.float32), ref, F16_ATOL, F16_RTOL, "prefill")
 
 
 def test_prefill_f32_rows(vkv, oracle, cuda):
