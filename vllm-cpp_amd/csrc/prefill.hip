@@ -804,14 +804,16 @@ __global__ __launch_bounds__(64 * kWideWaves) void prefill_wide_kernel(PrefillAr
     }
 }
 
-// Work list of the matrix-core kernel, in one workgroup: items (s, qb * Hkv +
-// kvh) of every sequence with >= 2 query tokens, ordered by level, where level
-// L holds block qb = nqb - 1 - L of every sequence with nqb > L blocks: last
-// blocks (which see the most keys) first, so that short blocks fill in at the
-// end.  Each sequence's q_len is read once; a histogram of block counts gives
-// every level's size and offset, and the sequences of a level take their slots
-// through LDS atomics (the order within a level does not matter to the
-// results).  At most kMaxLevels levels (max_query_len <= 32 * kMaxLevels).
+// Work list of the matrix-core kernels, in one workgroup: items (s, b * Hkv +
+// kvh), row block b of every sequence with >= 2 query tokens, ordered by the
+// number of key tiles they stage, most first, so that persistent workgroups
+// claiming them in turn form a longest-processing-time schedule (short items
+// fill in at the end).  A row block of rows_per_item rows (query tokens
+// times row_mult heads) sees keys 0 .. kend - 1 with kend = prior + its last
+// token + 1; a histogram over the tile counts (bins above kMaxLevels - 1
+// share the top bin) gives every count's offset, and the blocks take their
+// slots through LDS atomics (the order within a bin does not matter to the
+// results).
 constexpr int kMaxLevels = 4096;
 constexpr int kMaxHeadGroups = 63;  // claim counters after the item count (256-byte header)
 
@@ -847,40 +849,47 @@ __device__ int block_exclusive_scan(int* arr, int n, int* wave_tot) {
     return total;
 }
 
-__global__ __launch_bounds__(256) void prefill_items_kernel(const int32_t* qsl, int32_t num_seqs, int32_t hkv,
-                                                            int32_t row_mult, int32_t rows_per_item,
-                                                            int32_t max_qblocks, int2* items, int32_t* count) {
-    __shared__ int hist[kMaxLevels + 1];  // sequences with exactly n blocks, then its prefix sums
-    __shared__ int off[kMaxLevels];       // items per level, then level offsets
-    __shared__ int fill[kMaxLevels];      // slots taken per level
+__global__ __launch_bounds__(256) void prefill_items_kernel(const int32_t* qsl, const int32_t* cl, int32_t num_seqs,
+                                                            int32_t hkv, int32_t row_mult, int32_t rows_per_item,
+                                                            int32_t max_qblocks, int32_t table_tokens, int2* items,
+                                                            int32_t* count) {
+    __shared__ int off[kMaxLevels];   // items per bin, then bin offsets
+    __shared__ int fill[kMaxLevels];  // slots taken per bin
     __shared__ int wave_tot[4];
     const int tid = threadIdx.x;
-    const int levels = max_qblocks < kMaxLevels ? max_qblocks : kMaxLevels;
-    for (int i = tid; i <= levels; i += 256) hist[i] = 0;
-    for (int i = tid; i < levels; i += 256) fill[i] = 0;
+    for (int i = tid; i < kMaxLevels; i += 256) off[i] = fill[i] = 0;
     __syncthreads();
-    auto nqb = [&](int s) {
-        const int q = qsl[s + 1] - qsl[s];
+    // row blocks of sequence s (max_query_len bounds q_len: caller contract)
+    auto blocks = [&](int q) {
         const int n = q >= 2 ? int((int64_t(q) * row_mult + rows_per_item - 1) / rows_per_item) : 0;
-        return n < levels ? n : levels;  // max_query_len bounds q_len (caller contract)
+        return n < max_qblocks ? n : max_qblocks;
+    };
+    // bin of row block b: kMaxLevels - 1 - (its key tiles), most tiles first
+    auto bin = [&](int prior, int q, int b) {
+        const int64_t last = (int64_t(b + 1) * rows_per_item - 1) / row_mult + 1;
+        int64_t kend = prior + (last < q ? last : q);
+        kend = kend < table_tokens ? kend : table_tokens;
+        const int64_t tiles = kend > 0 ? (kend + kBK - 1) / kBK : 0;
+        return kMaxLevels - 1 - int(tiles < kMaxLevels - 1 ? tiles : kMaxLevels - 1);
     };
     for (int s = tid; s < num_seqs; s += 256) {
-        const int n = nqb(s);
-        if (n > 0) atomicAdd(&hist[n], 1);
+        const int q = qsl[s + 1] - qsl[s];
+        const int prior = cl[s] - q;
+        const int n = blocks(q);
+        for (int b = 0; b < n; ++b) atomicAdd(&off[bin(prior, q, b)], hkv);
     }
     __syncthreads();
-    // level L holds the sequences with n > L: total - (those with n <= L)
-    const int seqs = block_exclusive_scan(hist, levels + 1, wave_tot);
-    for (int L = tid; L < levels; L += 256) off[L] = (seqs - hist[L + 1]) * hkv;
-    __syncthreads();
-    const int total = block_exclusive_scan(off, levels, wave_tot);
+    const int total = block_exclusive_scan(off, kMaxLevels, wave_tot);
     if (tid == 0) count[0] = total;
     if (tid < kMaxHeadGroups) count[1 + tid] = 0;  // claim counters of the prefill kernel
     for (int s = tid; s < num_seqs; s += 256) {
-        const int n = nqb(s);
-        for (int L = 0; L < n; ++L) {
-            const int pos = off[L] + atomicAdd(&fill[L], hkv);
-            for (int k = 0; k < hkv; ++k) items[pos + k] = int2{s, (n - 1 - L) * hkv + k};
+        const int q = qsl[s + 1] - qsl[s];
+        const int prior = cl[s] - q;
+        const int n = blocks(q);
+        for (int b = 0; b < n; ++b) {
+            const int k0 = bin(prior, q, b);
+            const int pos = off[k0] + atomicAdd(&fill[k0], hkv);
+            for (int k = 0; k < hkv; ++k) items[pos + k] = int2{s, b * hkv + k};
         }
     }
 }
@@ -896,7 +905,6 @@ int ilog2i(int x) {
 bool prefill_mfma_supported(const vkv_prefill_params* p) {
     return p->io_dtype == VKV_DTYPE_F16 && (p->kv_dtype == VKV_DTYPE_F16 || p->kv_dtype == VKV_DTYPE_FP8_E4M3) &&
            (p->head_dim == 64 || p->head_dim == 128) && p->max_query_len >= 2 &&
-           (int64_t(p->max_query_len) + kBQ - 1) / kBQ <= kMaxLevels &&
            p->num_heads / p->num_kv_heads <= kMaxHeadGroups * kMaxWaves;
 }
 
@@ -939,8 +947,9 @@ int launch_prefill_mfma(const vkv_prefill_params* p, void* item_space, hipStream
     int2* items = reinterpret_cast<int2*>(static_cast<char*>(item_space) + 256);
     a.items = items;
     a.item_count = count;
-    hipLaunchKernelGGL(prefill_items_kernel, dim3(1), dim3(256), 0, st, p->query_start_loc, p->num_seqs,
-                       p->num_kv_heads, row_mult, rows_per_item, a.qblocks, items, count);
+    hipLaunchKernelGGL(prefill_items_kernel, dim3(1), dim3(256), 0, st, p->query_start_loc, p->context_lens,
+                       p->num_seqs, p->num_kv_heads, row_mult, rows_per_item, a.qblocks, a.table_tokens, items,
+                       count);
     // Persistent grid, never more workgroups than there can be items: one per
     // CU for the wide kernel (its LDS and registers fill a CU); two per CU for
     // the FP8 kernel (at D = 128 one is resident, the other starts when a CU
