@@ -7,11 +7,14 @@
 // sequence's paged cache, i.e. causal attention over the prior context plus
 // the chunk.  Keys are gathered through the block table like decode.
 //
-// Work decomposition.  A workgroup owns (sequence, kv head, block of kBQ = 32
-// query tokens); wave w computes query head kvh * G + w for those 32 tokens as
-// two 16-row MFMA tiles, so the G heads that share a kv head share every K/V
-// tile staged in LDS.  Keys are staged kBK = 64 at a time and computed in
-// 32-key steps:
+// Two kernels share the matrix-core layout below: prefill_wide_kernel for fp16
+// caches (work items of (token, head) rows, tiles staged by direct
+// global->LDS loads) and prefill_mfma_kernel for FP8 caches.  In the latter a
+// workgroup owns (sequence, kv head, block of kBQ = 32 query tokens); wave w
+// computes query head kvh * G + w for those 32 tokens as two 16-row MFMA
+// tiles, so the G heads that share a kv head share every K/V tile staged in
+// LDS.  In both, keys are staged kBK = 64 at a time and computed in 32-key
+// steps:
 //   S^T = K Q^T   v_mfma_f32_16x16x32_f16, A = K rows (LDS), B = Q (registers);
 //                 lane l holds row (query token) l % 16 for keys 4 (l / 16) + e
 //                 of each 16-key half: softmax state (max, sum) is lane-local
@@ -21,10 +24,6 @@
 //                 runs over keys in the order the S^T layout holds them), so P
 //                 never leaves the wave.
 // The output tile is O^T, again one row per lane, normalised at the end.
-//
-// fp16 caches (prefill_wide_kernel) use work items of (token, head) rows
-// instead, and stage tiles by direct global->LDS loads (global_load_lds,
-// three tile buffers, two tiles ahead) that every wave shares.
 //
 // Staging of FP8 caches (prefill_mfma_kernel): each of the first 256 threads
 // loads its share of the next tile's K and V rows into registers while the
@@ -70,9 +69,9 @@ struct PrefillArgs {
     int32_t max_blocks_per_seq;
     int32_t num_blocks;
     int32_t table_tokens;
-    int32_t qblocks;  // query blocks per sequence in the grid
+    int32_t qblocks;  // row blocks per sequence, at most (bounds the number of items)
     int32_t num_seqs;
-    const int2* items;       // work list (s, qb * Hkv + kvh)
+    const int2* items;       // work list (s, b * Hkv + kvh), b the sequence's row block
     int32_t* item_count;     // [0] items, [1 + z] claim counter of head group z (zeroed by the list kernel)
     float scale_log2;
 };
