@@ -92,6 +92,31 @@ def test_prefill_many_items(vkv, oracle, cuda):
     assert_close(to_np(out).astype(np.float32), ref, F16_ATOL, F16_RTOL, "prefill")
 
 
+def test_prefill_context_shorter_than_chunk(vkv, oracle, cuda):
+    """context_lens below q_len (invalid input): rows whose position sees no key
+    are zeros, the others attend the keys there are, and nothing is read out of
+    range (the second sequence's items have no keys at all)."""
+    import torch
+    from vllm_kv_amd import workloads
+    rng = np.random.default_rng(17)
+    H, Hkv, D, bs = 28, 4, 128, 16
+    q_lens = np.array([40, 33, 5], np.int32)
+    ctx = np.array([10, 0, 60], np.int32)  # prior -30, -33, 55
+    lay = workloads.make_layout(np.maximum(ctx, 1), bs, rng, slack=0.2)
+    k, v = workloads.fill_pool_numpy(rng, lay.num_blocks, bs, Hkv, D, 0.5)
+    qsl = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    q = (rng.standard_normal((int(qsl[-1]), H, D), dtype=np.float32) * 0.5).astype(np.float16)
+    scale = float(1.0 / np.sqrt(np.float32(D)))
+    ref = oracle.paged_prefill(q.astype(np.float32), k.view(np.uint16), v.view(np.uint16), lay.block_tables,
+                               ctx, qsl, scale)
+    assert not ref[:29].any() and not ref[40:73].any()  # no key before position 0
+    out = torch.full((q.shape[0], H, D), 7.0, dtype=torch.float16, device=cuda)
+    vkv.paged_prefill(out, to_dev(q, cuda), to_dev(k, cuda), to_dev(v, cuda), to_dev(lay.block_tables, cuda),
+                      to_dev(ctx, cuda), to_dev(qsl, cuda), int(q_lens.max()), scale)
+    torch.cuda.synchronize()
+    assert_close(to_np(out).astype(np.float32), ref, F16_ATOL, F16_RTOL, "prefill")
+
+
 def test_prefill_f32_rows(vkv, oracle, cuda):
     """fp32 queries take the per-row decode path (reference precision)."""
     import torch

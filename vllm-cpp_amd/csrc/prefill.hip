@@ -542,10 +542,13 @@ __device__ __forceinline__ void prefill_block_wide(const PrefillArgs& a, const i
         lane_off[j] = uint32_t(kvh) * D * 2 + uint32_t(((lane % T::CH) ^ (row % T::CH)) * 16);
     }
     const int32_t* table = a.bt + int64_t(s) * a.max_blocks_per_seq;
-    // key of this lane's row in load j of tile t (keys past the end: kend - 1 again, masked)
+    // key of this lane's row in load j of tile t (keys past the end: kend - 1
+    // again, masked; key 0 for an item with no keys at all, whose loads are
+    // still issued so that the vmcnt counts below stay exact)
     auto load_key = [&](const int t, const int j) __attribute__((always_inline)) {
-        const int k = t * kBK + (wave * JW + j) * T::RPI + lane / T::CH;
-        return k < kend ? k : kend - 1;
+        int k = t * kBK + (wave * JW + j) * T::RPI + lane / T::CH;
+        k = k < kend ? k : kend - 1;
+        return k > 0 ? k : 0;
     };
     auto load_ids = [&](const int t, int (&ids)[JW]) __attribute__((always_inline)) {
 #pragma unroll
