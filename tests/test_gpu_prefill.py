@@ -32,7 +32,9 @@ def _case(H, Hkv, D, bs, q_lens, prior, seed):
     (28, 4, 128, 32, [64, 1, 1, 33], [100, 500, 0, 7]),
     (14, 2, 64, 16, [40], [0]),
     (16, 2, 128, 16, [40, 3, 1], [10, 0, 77]),      # group 8: two head groups (grid.z), one claim counter each
-    (8, 8, 64, 8, [70, 2], [9000, 5]),              # MHA; 1131 blocks: block-id window reloads
+    (8, 8, 64, 8, [70, 2], [9000, 5]),              # MHA; 1131 blocks: block-id window reloads (FP8 kernel)
+    (8, 8, 64, 8, [40, 3], [17000, 9]),             # 2130 blocks: the fp16 kernel's 2048-id window refills
+    (8, 2, 128, 8, [20, 1], [16500, 40]),           # the same at D 128
     (16, 4, 128, 64, [33, 1, 100], [64, 0, 129]),   # blocks larger than a key tile
     (12, 4, 128, 16, [2, 31, 32, 65], [0, 1, 15, 300]),
     # groups 5 and 6: 256-row work items end inside a token's heads

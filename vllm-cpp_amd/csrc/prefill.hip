@@ -465,13 +465,16 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// Workgroup barrier that orders LDS only: every wave counts its own direct
-// loads out with wait_vmcnt before it, and has consumed its LDS reads (they
-// feed the tile's MFMAs) before it arrives.
-__device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+// Workgroup barrier that publishes a tile: each wave first waits until at
+// most N of its vector-memory operations are outstanding (its direct loads of
+// the tile landed in LDS, the next tile's may still be in flight) and for all
+// of its LDS operations, then meets the others.  Written as one asm block:
+// with a release fence the compiler waits for every direct load in flight
+// instead.  The memory clobber keeps LDS accesses on their side of it.
+template <int N>
+__device__ __forceinline__ void tile_barrier() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(N) : "memory");
 }
 
 // max(a, b, c) as v_maximum3_f32 (NaN-propagating, so no canonicalising
@@ -495,6 +498,7 @@ __device__ __forceinline__ float vmax3(float a, float b, float c) {
 // tile t + 1 out with s_waitcnt vmcnt before the barrier that publishes it.
 constexpr int kWideWaves = 8;  // two per SIMD
 constexpr int kWideStages = 3;
+constexpr int kWideBtc = 2048;  // block ids held in LDS at a time
 // 16-row tiles per wave (what fits 256 registers) and (token, head) rows per item
 template <int D>
 struct Wide {
@@ -502,9 +506,19 @@ struct Wide {
     static constexpr int ROWS = kWideWaves * RT * 16;
 };
 
+// K and V tile buffers of the three stages: six LDS objects, so that the
+// compiler can tell the direct loads into one stage from the reads of
+// another (with one shared array it waits for every load in flight before
+// each LDS read, which would undo the loads' lead).
+struct WideBuffers {
+    char* k[3];
+    char* v[3];
+    int* btc;  // block ids of the item (kWideBtc)
+};
+
 template <int D>
 __device__ __forceinline__ void prefill_block_wide(const PrefillArgs& a, const int s, const int b, const int kvh,
-                                                   char* tiles) {
+                                                   const WideBuffers& buf) {
     using T = DmaTile<D>;
     constexpr int DT = D / 16;  // output dim tiles
     constexpr int KS = D / 32;  // MFMA k-steps of Q K^T
@@ -519,6 +533,7 @@ __device__ __forceinline__ void prefill_block_wide(const PrefillArgs& a, const i
     const int col = lane & 15;
     const int grp = lane >> 4;
     const int G = a.group;
+    int* btc = buf.btc;
 
     const int q0 = a.qsl[s];
     const int qlen = a.qsl[s + 1] - q0;
@@ -530,7 +545,7 @@ __device__ __forceinline__ void prefill_block_wide(const PrefillArgs& a, const i
     kend = kend < a.table_tokens ? kend : a.table_tokens;
     const int ntiles = kend > 0 ? (kend + kBK - 1) / kBK : 0;
 
-    // ---------------- loads of tile t: block ids first (one tile ahead), then the rows
+    // ---------------- loads of tile t, through block ids held in LDS
     const int bs_mask = (1 << a.bs_log2) - 1;
     const uint32_t row_bytes32 = uint32_t(a.num_kv_heads) * D * 2;
     // this lane's bytes within the cache row of its load j: the kv head and
@@ -550,21 +565,33 @@ __device__ __forceinline__ void prefill_block_wide(const PrefillArgs& a, const i
         k = k < kend ? k : kend - 1;
         return k > 0 ? k : 0;
     };
-    auto load_ids = [&](const int t, int (&ids)[JW]) __attribute__((always_inline)) {
-#pragma unroll
-        for (int j = 0; j < JW; ++j) ids[j] = table[load_key(t, j) >> a.bs_log2];
+    // The item's block ids (range-checked) sit in LDS, kWideBtc from block
+    // `win` on.  Block ids read from global memory inside the tile loop would
+    // be vector-memory results among the direct loads, and the compiler,
+    // unable to count those apart, would wait for every load in flight
+    // before using one.  Callers synchronise the workgroup after a fill.
+    const int nblk = kend > 0 ? ((kend - 1) >> a.bs_log2) + 1 : 1;
+    int win = 0;
+    auto fill_window = [&](const int first) __attribute__((always_inline)) {
+        win = first;
+        const int n = nblk - first < kWideBtc ? nblk - first : kWideBtc;
+        for (int i = tid; i < n; i += 64 * kWideWaves) {
+            int id = table[first + i];
+            if (a.num_blocks > 0 && unsigned(id) >= unsigned(a.num_blocks)) id = 0;
+            btc[i] = id;
+        }
     };
     // (slots are int32 in the API: slot_mapping, num_blocks * block_size)
-    auto load_tile = [&](auto stage, const int t, const int (&ids)[JW]) __attribute__((always_inline)) {
+    auto load_tile = [&](auto stage, const int t) __attribute__((always_inline)) {
         constexpr int S = decltype(stage)::value;
-        char* kdst = tiles + S * T::BYTES;
-        char* vdst = tiles + (kWideStages + S) * T::BYTES;
+        char* kdst = buf.k[S];
+        char* vdst = buf.v[S];
 #pragma unroll
         for (int j = 0; j < JW; ++j) {
             const int jj = wave * JW + j;
-            int id = ids[j];
-            if (a.num_blocks > 0 && unsigned(id) >= unsigned(a.num_blocks)) id = 0;
-            const uint32_t slot = (uint32_t(id) << a.bs_log2) + uint32_t(load_key(t, j) & bs_mask);
+            const int k = load_key(t, j);
+            const int id = btc[(k >> a.bs_log2) - win];
+            const uint32_t slot = (uint32_t(id) << a.bs_log2) + uint32_t(k & bs_mask);
             const uint64_t off = uint64_t(slot) * row_bytes32 + lane_off[j];
             __builtin_amdgcn_global_load_lds(a.kc + off, (__attribute__((address_space(3))) void*)(kdst + jj * 1024),
                                              16, 0, 0);
@@ -572,6 +599,9 @@ __device__ __forceinline__ void prefill_block_wide(const PrefillArgs& a, const i
                                              16, 0, 0);
         }
     };
+
+    fill_window(0);
+    __syncthreads();
 
     // ---------------- Q (B operand of S^T = K Q^T) and per-row context; row
     // rho = b * ROWS + 16 (RT wave + r) + col is (token rho / G, head rho % G)
@@ -599,14 +629,10 @@ __device__ __forceinline__ void prefill_block_wide(const PrefillArgs& a, const i
         }
     }
 
-    // Loads of tiles 0 and 1 and the block ids of tile 2 (every wave issues
-    // them, also for tiles past the end, so the vmcnt counts below are exact).
-    int ids_a[JW], ids_b[JW];
-    load_ids(0, ids_a);
-    load_ids(1, ids_b);
-    load_tile(std::integral_constant<int, 0>(), 0, ids_a);
-    load_tile(std::integral_constant<int, 1>(), 1, ids_b);
-    load_ids(2, ids_a);
+    // Loads of tiles 0 and 1 (every wave issues its share, also for tiles past
+    // the end, so that the vmcnt counts below are exact).
+    load_tile(std::integral_constant<int, 0>(), 0);
+    load_tile(std::integral_constant<int, 1>(), 1);
 
     const float lazy = kLazy / sc;  // kLazy in raw (unscaled) logit units
     float m[RT], mlim[RT], msc[RT];
@@ -725,16 +751,19 @@ __device__ __forceinline__ void prefill_block_wide(const PrefillArgs& a, const i
     // masked: the causal / context mask may cut into the tile.
     auto tile = [&](auto stage, auto masked, const int t) __attribute__((always_inline)) {
         constexpr int S = decltype(stage)::value;
-        lds_barrier();  // tile t published; every wave has left tile t - 1
-        // ids of tile t + 3 into the registers freed by tile t + 2's loads
-        // (issued first, so that waiting for them never waits for tile t + 1)
-        int ids_n[JW];
-        load_ids(t + 3, ids_n);
-        load_tile(std::integral_constant<int, (S + 2) % kWideStages>(), t + 2, ids_a);  // buffer of tile t - 1
-#pragma unroll
-        for (int j = 0; j < JW; ++j) ids_a[j] = ids_n[j];
-        const char* kcur = tiles + S * T::BYTES;
-        const char* vcur = tiles + (kWideStages + S) * T::BYTES;
+        tile_barrier<2 * JW>();  // tile t published (t + 1 in flight); every wave has left tile t - 1
+        {
+            // the block ids of tile t + 2 must be in the window (every wave has
+            // issued tile t + 1's loads, the last reads of the old window)
+            const int last = (t + 3) * kBK - 1 < kend - 1 ? (t + 3) * kBK - 1 : kend - 1;
+            if (last > 0 && (last >> a.bs_log2) - win >= kWideBtc) {
+                fill_window(((t + 2) * kBK) >> a.bs_log2);
+                __syncthreads();
+            }
+        }
+        load_tile(std::integral_constant<int, (S + 2) % kWideStages>(), t + 2);  // buffer of tile t - 1
+        const char* kcur = buf.k[S];
+        const char* vcur = buf.v[S];
         float4_t sv[RT][2];
         half8_t pop[RT];
         qk(kcur, sv);
@@ -745,7 +774,6 @@ __device__ __forceinline__ void prefill_block_wide(const PrefillArgs& a, const i
             softmax(masked, t * kBK + 32, sv, pop);
             pv(vcur + 32 * T::ROW, pop);
         }
-        wait_vmcnt<JW + 2 * JW>();  // tile t + 1 landed (ids of t + 3, loads of t + 2 may be in flight)
     };
     using C0 = std::integral_constant<int, 0>;
     using C1 = std::integral_constant<int, 1>;
@@ -755,7 +783,6 @@ __device__ __forceinline__ void prefill_block_wide(const PrefillArgs& a, const i
     // has the shortest context.
     const int ctx_min = min(prior + (b * kWideRows) / G + 1, kend);
     const int tfull = ctx_min / kBK;
-    wait_vmcnt<JW + 2 * JW>();  // tile 0 landed (tile 1's loads and tile 2's ids may be in flight)
     int t = 0;
     for (; t + 3 <= tfull; t += 3) {
         tile(C0(), std::false_type(), t);
@@ -792,7 +819,15 @@ __device__ __forceinline__ void prefill_block_wide(const PrefillArgs& a, const i
 
 template <int D>
 __global__ __launch_bounds__(64 * kWideWaves) void prefill_wide_kernel(PrefillArgs a) {
-    __shared__ __attribute__((aligned(1024))) char tiles[kWideStages * 2 * DmaTile<D>::BYTES];
+    __shared__ __attribute__((aligned(1024))) char k0[DmaTile<D>::BYTES];
+    __shared__ __attribute__((aligned(1024))) char k1[DmaTile<D>::BYTES];
+    __shared__ __attribute__((aligned(1024))) char k2[DmaTile<D>::BYTES];
+    __shared__ __attribute__((aligned(1024))) char v0[DmaTile<D>::BYTES];
+    __shared__ __attribute__((aligned(1024))) char v1[DmaTile<D>::BYTES];
+    __shared__ __attribute__((aligned(1024))) char v2[DmaTile<D>::BYTES];
+    __shared__ int btc[kWideBtc];
+    static_assert(kWideStages == 3, "three K and three V buffers");
+    const WideBuffers buf = {{k0, k1, k2}, {v0, v1, v2}, btc};
     __shared__ int claimed;
     const int count = a.item_count[0];
     for (;;) {
@@ -802,7 +837,7 @@ __global__ __launch_bounds__(64 * kWideWaves) void prefill_wide_kernel(PrefillAr
         __syncthreads();
         if (it >= count) break;
         const int2 item = a.items[it];
-        prefill_block_wide<D>(a, item.x, item.y / a.num_kv_heads, item.y % a.num_kv_heads, tiles);
+        prefill_block_wide<D>(a, item.x, item.y / a.num_kv_heads, item.y % a.num_kv_heads, buf);
     }
 }
 
