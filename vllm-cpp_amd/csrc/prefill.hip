@@ -847,8 +847,9 @@ __global__ __launch_bounds__(64 * kWideWaves) void prefill_wide_kernel(PrefillAr
 // claiming them in turn form a longest-processing-time schedule (short items
 // fill in at the end).  A row block of rows_per_item rows (query tokens
 // times row_mult heads) sees keys 0 .. kend - 1 with kend = prior + its last
-// token + 1; a histogram over the tile counts (bins above kMaxLevels - 1
-// share the top bin) gives every count's offset, and the blocks take their
+// token + 1; a histogram over the tile counts (one bin per possible count,
+// at most kMaxLevels: counts past that share the top bin) gives every count's
+// offset, and the blocks take their
 // slots through LDS atomics (the order within a bin does not matter to the
 // results).
 constexpr int kMaxLevels = 4096;
@@ -888,26 +889,26 @@ __device__ int block_exclusive_scan(int* arr, int n, int* wave_tot) {
 
 __global__ __launch_bounds__(256) void prefill_items_kernel(const int32_t* qsl, const int32_t* cl, int32_t num_seqs,
                                                             int32_t hkv, int32_t row_mult, int32_t rows_per_item,
-                                                            int32_t max_qblocks, int32_t table_tokens, int2* items,
-                                                            int32_t* count) {
-    __shared__ int off[kMaxLevels];   // items per bin, then bin offsets
+                                                            int32_t max_qblocks, int32_t table_tokens, int32_t nbins,
+                                                            int2* items, int32_t* count) {
+    __shared__ int off[kMaxLevels];   // items per bin, then bin offsets (nbins used)
     __shared__ int fill[kMaxLevels];  // slots taken per bin
     __shared__ int wave_tot[4];
     const int tid = threadIdx.x;
-    for (int i = tid; i < kMaxLevels; i += 256) off[i] = fill[i] = 0;
+    for (int i = tid; i < nbins; i += 256) off[i] = fill[i] = 0;
     __syncthreads();
     // row blocks of sequence s (max_query_len bounds q_len: caller contract)
     auto blocks = [&](int q) {
         const int n = q >= 2 ? int((int64_t(q) * row_mult + rows_per_item - 1) / rows_per_item) : 0;
         return n < max_qblocks ? n : max_qblocks;
     };
-    // bin of row block b: kMaxLevels - 1 - (its key tiles), most tiles first
+    // bin of row block b: nbins - 1 - (its key tiles), most tiles first
     auto bin = [&](int prior, int q, int b) {
         const int64_t last = (int64_t(b + 1) * rows_per_item - 1) / row_mult + 1;
         int64_t kend = prior + (last < q ? last : q);
         kend = kend < table_tokens ? kend : table_tokens;
         const int64_t tiles = kend > 0 ? (kend + kBK - 1) / kBK : 0;
-        return kMaxLevels - 1 - int(tiles < kMaxLevels - 1 ? tiles : kMaxLevels - 1);
+        return nbins - 1 - int(tiles < nbins - 1 ? tiles : nbins - 1);
     };
     for (int s = tid; s < num_seqs; s += 256) {
         const int q = qsl[s + 1] - qsl[s];
@@ -916,7 +917,7 @@ __global__ __launch_bounds__(256) void prefill_items_kernel(const int32_t* qsl, 
         for (int b = 0; b < n; ++b) atomicAdd(&off[bin(prior, q, b)], hkv);
     }
     __syncthreads();
-    const int total = block_exclusive_scan(off, kMaxLevels, wave_tot);
+    const int total = block_exclusive_scan(off, nbins, wave_tot);
     if (tid == 0) count[0] = total;
     if (tid < kMaxHeadGroups) count[1 + tid] = 0;  // claim counters of the prefill kernel
     for (int s = tid; s < num_seqs; s += 256) {
@@ -984,9 +985,12 @@ int launch_prefill_mfma(const vkv_prefill_params* p, void* item_space, hipStream
     int2* items = reinterpret_cast<int2*>(static_cast<char*>(item_space) + 256);
     a.items = items;
     a.item_count = count;
+    // bins: every possible tile count (items past kMaxLevels - 1 tiles share the last)
+    const int64_t max_tiles = (int64_t(a.table_tokens) + kBK - 1) / kBK;
+    const int nbins = int(max_tiles + 1 < kMaxLevels ? max_tiles + 1 : kMaxLevels);
     hipLaunchKernelGGL(prefill_items_kernel, dim3(1), dim3(256), 0, st, p->query_start_loc, p->context_lens,
-                       p->num_seqs, p->num_kv_heads, row_mult, rows_per_item, a.qblocks, a.table_tokens, items,
-                       count);
+                       p->num_seqs, p->num_kv_heads, row_mult, rows_per_item, a.qblocks, a.table_tokens, nbins,
+                       items, count);
     // Persistent grid, never more workgroups than there can be items: one per
     // CU for the wide kernel (its LDS and registers fill a CU); two per CU for
     // the FP8 kernel (at D = 128 one is resident, the other starts when a CU
