@@ -269,10 +269,11 @@ def test_decode_config2_sampled(vkv, oracle, cuda):
 
 @pytest.mark.parametrize("H,Hkv,D", [(8, 8, 64), (32, 8, 128)])
 def test_decode_more_groups_than_grid(vkv, oracle, cuda, H, Hkv, D):
-    """A batch with more work groups (4 kv-head items each) than the launch cap
-    of 16 per CU: the groups past the grid are claimed through the workspace
-    counters.  Sampled sequences against the oracle; a second call must agree
-    bit for bit (the counters return to zero)."""
+    """A batch with many more work groups (4 kv-head items each) than the grid,
+    which holds one workgroup per resident slot (at most 8 per CU): the groups
+    past the grid are claimed through the workspace counters.  Sampled
+    sequences against the oracle; a second call must agree bit for bit (the
+    counters return to zero)."""
     import torch
     S, bs, P = 2048, 16, 64
     rng = np.random.default_rng(D + H)
@@ -330,3 +331,50 @@ def test_decode_caller_workspace_and_errors(vkv, cuda):
     with pytest.raises(vkv.VkvError) as e:
         vkv.paged_decode(out_b, *args, workspace=small)
     assert e.value.code == -4
+
+
+def test_decode_default_partition_choice(vkv, oracle, cuda):
+    """Partition size left to the library on a batch whose default-size items
+    fill between one and two rounds of resident waves (C3's 120 decode rows:
+    G = 7, contexts U[1024, 8192]): the kernels pick the size on the device
+    and record it in the workspace header (int 1).  The result must equal an
+    explicit call at the recorded size bit for bit (same partitions, so the
+    merge kernel read the size right), and sampled rows match the oracle."""
+    import torch
+    from vllm_kv_amd import workloads
+    cfg = workloads.config3()
+    npf = int((cfg.q_lens > 1).sum())
+    lay = cfg.layout
+    H, Hkv, D, bs = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim, cfg.block_size
+    bt = to_dev(np.ascontiguousarray(lay.block_tables[npf:]), cuda)
+    cl = to_dev(np.ascontiguousarray(lay.context_lens[npf:]), cuda)
+    S = bt.shape[0]
+    g = torch.Generator(device=cuda).manual_seed(21)
+    shape = (lay.num_blocks, bs, Hkv, D)
+    kc = (torch.randn(shape, generator=g, device=cuda) * 0.5).half()
+    vc = (torch.randn(shape, generator=g, device=cuda) * 0.5).half()
+    q = (torch.randn((S, H, D), generator=g, device=cuda) * 0.5).half()
+    scale = cfg.scale
+    out = torch.zeros((S, H, D), dtype=torch.float16, device=cuda)
+    need = vkv.decode_workspace_size(out, q, kc, vc, bt, cl, scale)
+    ws = torch.zeros(need // 4 + 4, dtype=torch.int32, device=cuda)
+    vkv.paged_decode(out, q, kc, vc, bt, cl, scale, workspace=ws)
+    torch.cuda.synchronize()
+    chosen = int(ws[1].item())
+    # candidates: 5/6, 1, 5/4, 3/2, 5/3 and 2 x 768 tokens, in 32-token blocks
+    assert chosen in (640, 768, 960, 1152, 1280, 1536), chosen
+    out2 = torch.zeros_like(out)
+    vkv.paged_decode(out2, q, kc, vc, bt, cl, scale, partition_size=chosen)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), out2.view(torch.int16)), chosen
+    got = to_np(out).astype(np.float32)
+    qn = to_np(q).astype(np.float32)
+    for s in [0, 1, 57, 118, 119]:
+        n = int(lay.context_lens[npf + s])
+        nblk = (n + bs - 1) // bs
+        ids = torch.from_numpy(lay.block_tables[npf + s, :nblk]).long().to(cuda)
+        kk = to_np(kc[ids]).view(np.uint16)
+        vv = to_np(vc[ids]).view(np.uint16)
+        ref = oracle.paged_decode(qn[s:s + 1], kk, vv, np.arange(nblk, dtype=np.int32)[None, :],
+                                  np.array([n], np.int32), scale)
+        assert_close(got[s:s + 1], ref, F16_ATOL, F16_RTOL, f"row {s} (partition {chosen})")

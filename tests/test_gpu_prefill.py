@@ -94,6 +94,44 @@ def test_prefill_many_items(vkv, oracle, cuda):
     assert_close(to_np(out).astype(np.float32), ref, F16_ATOL, F16_RTOL, "prefill")
 
 
+def test_prefill_mixed_config3_sampled(vkv, oracle, cuda):
+    """C3's mixed call at its full size: 8 chunks of 512 query tokens (prior
+    U[0, 2048]) on the matrix-core kernel and 120 single-token sequences
+    (contexts U[1024, 8192]) through split-K decode with the partition size
+    picked on the device.  Sampled query rows of both kinds against the oracle
+    (row j of a chunk is decode over prior + j + 1 keys)."""
+    import torch
+    from vllm_kv_amd import workloads
+    cfg = workloads.config3()
+    lay = cfg.layout
+    H, Hkv, D, bs = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim, cfg.block_size
+    qsl = cfg.query_start_loc
+    Tq = int(qsl[-1])
+    g = torch.Generator(device=cuda).manual_seed(23)
+    shape = (lay.num_blocks, bs, Hkv, D)
+    kc = (torch.randn(shape, generator=g, device=cuda) * 0.5).half()
+    vc = (torch.randn(shape, generator=g, device=cuda) * 0.5).half()
+    q = (torch.randn((Tq, H, D), generator=g, device=cuda) * 0.5).half()
+    out = torch.zeros((Tq, H, D), dtype=torch.float16, device=cuda)
+    vkv.paged_prefill(out, q, kc, vc, to_dev(lay.block_tables, cuda), to_dev(lay.context_lens, cuda),
+                      to_dev(qsl, cuda), int(cfg.q_lens.max()), cfg.scale)
+    torch.cuda.synchronize()
+    got = to_np(out).astype(np.float32)
+    qn = to_np(q).astype(np.float32)
+    npf = int((cfg.q_lens > 1).sum())
+    rows = [(0, 0), (0, 511), (3, 200), (7, 511), (npf, 0), (npf + 60, 0), (len(cfg.q_lens) - 1, 0)]
+    for s, j in rows:
+        n = int(cfg.prior_lens[s]) + j + 1
+        nblk = (n + bs - 1) // bs
+        ids = torch.from_numpy(lay.block_tables[s, :nblk]).long().to(cuda)
+        kk = to_np(kc[ids]).view(np.uint16)
+        vv = to_np(vc[ids]).view(np.uint16)
+        r = int(qsl[s]) + j
+        ref = oracle.paged_decode(qn[r:r + 1], kk, vv, np.arange(nblk, dtype=np.int32)[None, :],
+                                  np.array([n], np.int32), cfg.scale)
+        assert_close(got[r:r + 1], ref, F16_ATOL, F16_RTOL, f"sequence {s} row {j}")
+
+
 def test_prefill_context_shorter_than_chunk(vkv, oracle, cuda):
     """context_lens below q_len (invalid input): rows whose position sees no key
     are zeros, the others attend the keys there are, and nothing is read out of

@@ -29,6 +29,8 @@
 //
 // FP8 lanes load 8 bytes (8 codes) so that fp8 and fp16 share one lane layout
 // (D=128: 16 lanes per token) and one register footprint.
+#include <atomic>
+#include <cstdint>
 #include <cstdlib>
 #include <type_traits>
 
@@ -70,10 +72,20 @@ constexpr int kOneChunkAboveGFp8 = VKV_DECODE_ONE_CHUNK_ABOVE_G_FP8;
 constexpr float kLog2e = 1.4426950408889634f;
 // Default partition sizing aims at this many (row, partition, kv head) items.
 constexpr int64_t kMinItems = 2048;
-// Launch cap in workgroups per CU.  A grid holding every item group lets the
-// hardware dispatcher balance the CUs; claims through the counters only serve
-// batches with more groups than this.
-constexpr int kGridBlocksPerCu = 16;
+// Per-call partition choice (library default only).  Candidates relative to
+// the default size P0 (block multiples, at most 64 blocks): 5/6, 1, 5/4, 3/2,
+// 5/3, 2 x P0.  Calls over more rows than kAdaptMaxRows keep P0.
+constexpr int kCandNum[kMaxPartitionCandidates] = {5, 1, 5, 3, 5, 2};
+constexpr int kCandDen[kMaxPartitionCandidates] = {6, 1, 4, 2, 3, 1};
+constexpr int kAdaptMaxRows = 4096;
+// Fixed cost of one item (partial write, merge input, chain start-up) in
+// token-equivalents, for the span estimate of the partition choice.
+constexpr int kItemOverheadTokens = 128;
+// Workspace header int holding the partition size the partition kernel
+// chose, read by the merge kernel (the claim counters use ints 0, 32, ...).
+constexpr int kChosenPartitionSlot = 1;
+// LDS per CU on gfx950, for the resident-wave estimate.
+constexpr int kLdsPerCu = 160 * 1024;
 
 struct DecodeArgs {
     void* out;
@@ -108,6 +120,11 @@ struct DecodeArgs {
     int32_t num_rows;         // sequences (decode) or query rows (prefill)
     int* counters;            // claim counters in the workspace header (zero between calls)
     int32_t mfma_enabled;     // use the matrix-core QK^T variant where it applies
+    // num_cands > 1: P is the default size, the kernel picks the partition
+    // size among cands (ascending) and records it in the workspace header.
+    int32_t num_cands;
+    int32_t cands[kMaxPartitionCandidates];
+    int32_t wave_slots;       // waves of this launch resident at once (estimate)
 };
 
 // Keys row r attends (clamped to the table) and the query/output row it uses.
@@ -177,8 +194,8 @@ __device__ __forceinline__ void unpack_lane(const uint32_t* w, float* v) {
 // row) for kv head kvh, computed by the calling wave alone.  Writes the
 // item's partial (o, max, sum) to the workspace.
 template <typename IO, int KVT, int D, int G>
-__device__ __forceinline__ void decode_item(const DecodeArgs& a, const int s, const int kvh, const int part,
-                                            const int lane) {
+__device__ __forceinline__ void decode_item(const DecodeArgs& a, const int P, const int s, const int kvh,
+                                            const int part, const int lane) {
     constexpr int EB = KvTraits<KVT>::bytes;
     constexpr int LW = LaneLoad<KVT>::words;
     constexpr int EPL = LaneLoad<KVT>::elems;  // elements per lane per load
@@ -192,9 +209,9 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, const int s, co
 
     const int seq = a.row_seq ? a.row_seq[s] : s;
     const int ctx = row_context(a, s);
-    const int t0 = part * a.P;
+    const int t0 = part * P;
     if (t0 >= ctx) return;
-    const int n = (ctx - t0) < a.P ? (ctx - t0) : a.P;
+    const int n = (ctx - t0) < P ? (ctx - t0) : P;
 
     const int sub = lane % LPT;  // which slice of the head vector
     const int grp = lane / LPT;  // which token of a wave-wide load
@@ -514,8 +531,8 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, const int s, co
 // This moves the 128 VALU instructions of the per-token dot products and their
 // cross-lane sums per chunk onto the matrix pipe.
 template <int G, int KVT>
-__device__ __forceinline__ void decode_item_mfma(const DecodeArgs& a, const int s, const int kvh, const int part,
-                                                 const int lane, float* plds) {
+__device__ __forceinline__ void decode_item_mfma(const DecodeArgs& a, const int P, const int s, const int kvh,
+                                                 const int part, const int lane, float* plds) {
     constexpr int D = 128;
     constexpr int CH = 16;
     constexpr bool FP8 = KVT == kFp8;
@@ -527,9 +544,9 @@ __device__ __forceinline__ void decode_item_mfma(const DecodeArgs& a, const int 
 
     const int seq = a.row_seq ? a.row_seq[s] : s;
     const int ctx = row_context(a, s);
-    const int t0 = part * a.P;
+    const int t0 = part * P;
     if (t0 >= ctx) return;
-    const int n = (ctx - t0) < a.P ? (ctx - t0) : a.P;
+    const int n = (ctx - t0) < P ? (ctx - t0) : P;
     const int bs_mask = (1 << a.bs_log2) - 1;
     const int col = lane & 15;  // MFMA column (query head) / V dim slice
     const int quad = lane >> 4; // MFMA k-slice / accumulator row group / V token in a load
@@ -804,9 +821,58 @@ constexpr int min_waves_per_simd() {
     return (MFMA && ((KVT == kF16 && G > kOneChunkAboveG) || (KVT == kFp8 && G > 6))) ? 2 : kMinWavesPerSimd;
 }
 
+// Partition size of a call that left it to the library.  Every workgroup
+// evaluates the same candidates over the rows' context lengths (each thread
+// brings its row tile's partition count per candidate), so all reach the same
+// size.  Items run in rounds of wave_slots resident waves.  A call whose
+// default-size items fit in one round keeps the default: it is
+// bandwidth-bound, and longer partitions only lengthen each wave's chain
+// (C2's batch: 105 us at 768 tokens, 116 us at 1 024).  Between one and two
+// rounds a second round that is only partly filled costs nearly a whole one,
+// so the candidate with the least rounds x (P + kItemOverheadTokens) wins
+// (ties: the smaller size): C3's decode rows fill 1.6 rounds at 768 tokens
+// (227 us) and one at 1 280 (the choice, 207 us).  Beyond two rounds the
+// default stays: waves that claim items as they finish fill the last round
+// with the short final partitions of the rows, and C5's batch (3.3 rounds at
+// 768) measured 361 us at 768 against 365 us at 640, the size this estimate
+// would take.
+__device__ int choose_partition(const DecodeArgs& a, const int (&cnt)[kMaxPartitionCandidates]) {
+    __shared__ int sums[kWavesPerBlock][kMaxPartitionCandidates];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+#pragma unroll
+    for (int c = 0; c < kMaxPartitionCandidates; ++c) {
+        int v = cnt[c];
+#pragma unroll
+        for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+        if (lane == 0) sums[wave][c] = v;
+    }
+    __syncthreads();
+    const unsigned W = a.wave_slots > 0 ? unsigned(a.wave_slots) : 1u;
+    const unsigned cap = 0x7FFFFFFFu / unsigned(a.num_kv_heads);
+    unsigned items0 = 0;
+    uint64_t best_cost = ~uint64_t(0);
+    int best = a.P;
+#pragma unroll
+    for (int c = 0; c < kMaxPartitionCandidates; ++c) {
+        if (c >= a.num_cands) break;
+        unsigned pairs = 0;
+#pragma unroll
+        for (int w = 0; w < kWavesPerBlock; ++w) pairs += unsigned(sums[w][c]);
+        const unsigned items = (pairs < cap ? pairs : cap) * unsigned(a.num_kv_heads);
+        if (a.cands[c] == a.P) items0 = items;
+        const uint64_t cost = uint64_t((items + W - 1) / W) * unsigned(a.cands[c] + kItemOverheadTokens);
+        if (cost < best_cost) {
+            best_cost = cost;
+            best = a.cands[c];
+        }
+    }
+    return (items0 <= W || items0 > 2 * W) ? a.P : best;
+}
+
 template <typename IO, int KVT, int D, int G, bool MFMA>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(min_waves_per_simd<KVT, G, MFMA>())))
-void decode_partition_kernel(DecodeArgs a) {
+void decode_partition_kernel(const DecodeArgs a) {
     extern __shared__ int prefix[];  // [num_rows + 1] exclusive prefix of partitions per row
     const int lane = threadIdx.x & (kWave - 1);
     const int nrows = a.num_rows;
@@ -814,17 +880,44 @@ void decode_partition_kernel(DecodeArgs a) {
     // Partitions per row and their exclusive prefix, scanned by the whole
     // workgroup: each thread sums a contiguous tile of rows, the 256 tile sums
     // are scanned with wave shuffles plus one LDS step, then each thread writes
-    // its tile's prefix entries.
+    // its tile's prefix entries.  A call that leaves the partition size to the
+    // library counts its tile for every candidate size in the same pass and
+    // picks the size first.
     __shared__ int wave_total[kWavesPerBlock];
+    int P = a.P;
     auto parts_of = [&](int r) {
         const int ctx = row_context(a, r);
-        return ctx > 0 ? (ctx + a.P - 1) / a.P : 0;
+        return ctx > 0 ? (ctx + P - 1) / P : 0;
     };
     const int per = (nrows + int(blockDim.x) - 1) / int(blockDim.x);
     const int r0 = int(threadIdx.x) * per;
     int local = 0;
-    for (int i = 0; i < per; ++i)
-        if (r0 + i < nrows) local += parts_of(r0 + i);
+    if (a.num_cands > 1) {
+        int cnt[kMaxPartitionCandidates];
+#pragma unroll
+        for (int c = 0; c < kMaxPartitionCandidates; ++c) cnt[c] = 0;
+        for (int i = 0; i < per; ++i) {
+            const int ctx = r0 + i < nrows ? row_context(a, r0 + i) : 0;
+            if (ctx > 0) {
+                // candidates are block multiples m * bs: ceil(ctx / (m * bs)) = ceil(nb / m)
+                const int nb = ((ctx - 1) >> a.bs_log2) + 1;
+#pragma unroll
+                for (int c = 0; c < kMaxPartitionCandidates; ++c) {
+                    const int m = a.cands[c] >> a.bs_log2;  // >= 1 (the host pads unused entries)
+                    cnt[c] += (nb + m - 1) / m;
+                }
+            }
+        }
+        P = __builtin_amdgcn_readfirstlane(choose_partition(a, cnt));  // wave-uniform: keep it scalar
+#pragma unroll
+        for (int c = 0; c < kMaxPartitionCandidates; ++c)
+            if (a.cands[c] == P) local = cnt[c];
+        // for the merge kernel (same stream, after this grid)
+        if (blockIdx.x == 0 && threadIdx.x == 0) a.counters[kChosenPartitionSlot] = P;
+    } else {
+        for (int i = 0; i < per; ++i)
+            if (r0 + i < nrows) local += parts_of(r0 + i);
+    }
     int incl = local;
 #pragma unroll
     for (int o = 1; o < kWave; o <<= 1) {
@@ -874,8 +967,8 @@ void decode_partition_kernel(DecodeArgs a) {
                 if (prefix[mid] <= pair) lo = mid;
                 else hi = mid - 1;
             }
-            if constexpr (MFMA) decode_item_mfma<G, KVT>(a, lo, kvh, pair - prefix[lo], lane, plds[wave]);
-            else decode_item<IO, KVT, D, G>(a, lo, kvh, pair - prefix[lo], lane);
+            if constexpr (MFMA) decode_item_mfma<G, KVT>(a, P, lo, kvh, pair - prefix[lo], lane, plds[wave]);
+            else decode_item<IO, KVT, D, G>(a, P, lo, kvh, pair - prefix[lo], lane);
         }
         if (g0 >= num_groups) break;  // the grid covers every group: nothing to claim
         __syncthreads();
@@ -931,7 +1024,8 @@ __global__ __launch_bounds__(D) void decode_reduce_kernel(DecodeArgs a) {
     load_batch(0);
     if (a.qsl && a.qsl[s + 1] - a.qsl[s] != 1) return;  // a prefill sequence: not decoded here
     const int ctx = row_context(a, s);
-    const int np = ctx > 0 ? (ctx + a.P - 1) / a.P : 0;
+    const int P = a.num_cands > 1 ? __builtin_amdgcn_readfirstlane(a.counters[kChosenPartitionSlot]) : a.P;
+    const int np = ctx > 0 ? (ctx + P - 1) / P : 0;
     float m = -INFINITY, l = 0.0f, acc = 0.0f;
     for (int i0 = 0; i0 < np; i0 += kMergeBatch) {
         if (i0 > 0) load_batch(i0);
@@ -960,7 +1054,7 @@ __global__ __launch_bounds__(D) void decode_reduce_kernel(DecodeArgs a) {
 }
 
 // VKV_DECODE_BLOCKS_PER_CU=<n> overrides the grid's workgroups per CU
-// (tuning; default kGridBlocksPerCu).
+// (tuning; default: as many as are resident at once).
 int blocks_per_cu(int fits) {
     static const int v = [] {
         const char* e = std::getenv("VKV_DECODE_BLOCKS_PER_CU");
@@ -992,26 +1086,50 @@ int device_cu_count() {
 }
 
 template <typename IO, int KVT, int D, int G>
-void launch_g(const DecodeArgs& args, int grid_x, int grid_y, int grid_z, size_t lds, hipStream_t st) {
+void launch_g(DecodeArgs& args, int grid_x, int grid_y, int grid_z, size_t lds, hipStream_t st) {
     // Matrix-core QK^T for fp16 query and keys at D = 128 with blocks of a
     // multiple of 16 tokens; the VALU variant covers everything else.
     constexpr bool kMfmaShape = std::is_same<IO, _Float16>::value && KVT != kF32 && D == 128;
-    // grid_x arrives as the number of item groups (an upper bound).  Up to
-    // kGridBlocksPerCu workgroups per CU are launched, one group each, and the
-    // hardware dispatcher starts them as slots free up; groups beyond the grid
-    // are claimed by workgroups that finish early.
-    auto run = [&](auto kernel) {
-        const int64_t wgs = int64_t(device_cu_count()) * blocks_per_cu(kGridBlocksPerCu);
+    // grid_x arrives as the number of item groups (an upper bound).  One workgroup per resident slot: the variant's workgroups per CU by
+    // registers (queried once per variant), bounded by the LDS the rows'
+    // prefix takes, and never more than there are item groups.  Groups
+    // beyond the grid are claimed through the counters as workgroups finish
+    // (each workgroup scans the rows once, where a grid of every group pays
+    // that scan per group: C5's batch measured 361 us against 382 us).  The
+    // resident wave count also feeds the partition choice.
+    static std::atomic<int> reg_blocks[2];
+    auto run = [&](auto kernel, int variant) {
+        const int cus = device_cu_count();
+        int per_cu = reg_blocks[variant].load(std::memory_order_relaxed);
+        if (per_cu <= 0) {
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kWave * kWavesPerBlock, 0) !=
+                    hipSuccess || per_cu <= 0)
+                per_cu = 1;
+            reg_blocks[variant].store(per_cu, std::memory_order_relaxed);
+        }
+        const int by_lds = kLdsPerCu / int(lds + 4096);  // + an allowance for the static LDS
+        if (by_lds < per_cu) per_cu = by_lds > 0 ? by_lds : 1;
+        per_cu = blocks_per_cu(per_cu);
+        const int64_t wgs = int64_t(cus) * per_cu;
         const int gx = int(wgs < grid_x ? wgs : grid_x);
+        args.wave_slots = (gx > 0 ? gx : 1) * kWavesPerBlock;
+        // When even the longest possible contexts give at most one round of
+        // default-size items, the default stands and the kernels (this one
+        // and the merge, which reads these args) skip the choice.
+        if (args.num_cands > 1) {
+            const int64_t worst = int64_t(args.num_rows) * ((int64_t(args.max_ctx) + args.P - 1) / args.P) *
+                                  args.num_kv_heads;
+            if (worst <= args.wave_slots) args.num_cands = 1;
+        }
         hipLaunchKernelGGL(kernel, dim3(gx > 0 ? gx : 1, grid_y, grid_z), dim3(kWave * kWavesPerBlock), lds, st, args);
     };
-    if (kMfmaShape && args.bs_log2 >= 4 && args.mfma_enabled) run(decode_partition_kernel<IO, KVT, D, G, kMfmaShape>);
-    else run(decode_partition_kernel<IO, KVT, D, G, false>);
+    if (kMfmaShape && args.bs_log2 >= 4 && args.mfma_enabled) run(decode_partition_kernel<IO, KVT, D, G, kMfmaShape>, 1);
+    else run(decode_partition_kernel<IO, KVT, D, G, false>, 0);
 }
 
 
 template <typename IO, int KVT, int D>
-int dispatch_g(int G, const DecodeArgs& args, int grid_x, int Hkv, int S, size_t lds, hipStream_t st) {
+int dispatch_g(int G, DecodeArgs& args, int grid_x, int Hkv, int S, size_t lds, hipStream_t st) {
     switch (G) {
         case 1: launch_g<IO, KVT, D, 1>(args, grid_x, Hkv, S, lds, st); return 0;
         case 2: launch_g<IO, KVT, D, 2>(args, grid_x, Hkv, S, lds, st); return 0;
@@ -1026,7 +1144,7 @@ int dispatch_g(int G, const DecodeArgs& args, int grid_x, int Hkv, int S, size_t
 }
 
 template <typename IO, int KVT>
-int dispatch_d(int D, int G, const DecodeArgs& args, int grid_x, int Hkv, int S, size_t lds,
+int dispatch_d(int D, int G, DecodeArgs& args, int grid_x, int Hkv, int S, size_t lds,
                hipStream_t st) {
     switch (D) {
         case 64: return dispatch_g<IO, KVT, 64>(G, args, grid_x, Hkv, S, lds, st);
@@ -1078,7 +1196,22 @@ DecodePlan plan_decode(const vkv_decode_params* p) {
     P = (P / bs) * bs;
     if (P > 64 * bs) P = 64 * bs;
     plan.partition_size = P;
-    plan.max_parts = int((max_ctx + P - 1) / P);
+    plan.num_candidates = 1;
+    for (int i = 0; i < kMaxPartitionCandidates; ++i) plan.candidates[i] = P;
+    int smallest = P;
+    if (p->partition_size <= 0 && p->num_seqs <= kAdaptMaxRows) {
+        // the kernels pick the size per call among these (ascending)
+        int n = 0;
+        for (int i = 0; i < kMaxPartitionCandidates; ++i) {
+            int c = (P * kCandNum[i] / kCandDen[i]) / bs * bs;
+            c = c < bs ? bs : (c > 64 * bs ? 64 * bs : c);
+            if (n == 0 || c != plan.candidates[n - 1]) plan.candidates[n++] = c;
+        }
+        for (int i = n; i < kMaxPartitionCandidates; ++i) plan.candidates[i] = plan.candidates[n - 1];
+        plan.num_candidates = n;
+        smallest = plan.candidates[0];
+    }
+    plan.max_parts = int((max_ctx + smallest - 1) / smallest);
     if (plan.max_parts < 1) plan.max_parts = 1;
     plan.workspace_bytes = kWorkspaceHeader +
                            size_t(p->num_seqs) * p->num_heads * plan.max_parts * (p->head_dim + 2) * sizeof(float);
@@ -1136,6 +1269,9 @@ int launch_rows(const vkv_decode_params* p, const DecodePlan& plan, void* worksp
     a.num_blocks = p->num_blocks;
     a.P = plan.partition_size;
     a.max_parts = plan.max_parts;
+    a.num_cands = plan.num_candidates;
+    for (int i = 0; i < kMaxPartitionCandidates; ++i) a.cands[i] = plan.candidates[i];
+    a.wave_slots = 0;  // set per variant at launch
     a.scale_log2 = p->scale * kLog2e;
     a.accumulate = p->accumulate;
 

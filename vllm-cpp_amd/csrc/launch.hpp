@@ -14,10 +14,17 @@ int launch_rope_append(const vkv_rope_append_params* p, hipStream_t st);
 
 // Split-K decode: partition kernel + reduce kernel.  part_o / part_ml point into
 // a workspace of decode_workspace_bytes(); partition_size already normalised.
+// When the caller leaves the partition size to the library, num_candidates > 1
+// sizes (ascending, partition_size among them) go to the kernels, which pick
+// one per call from the device-side context lengths; max_parts then covers the
+// smallest.
+constexpr int kMaxPartitionCandidates = 6;
 struct DecodePlan {
     int partition_size;
     int max_parts;
     size_t workspace_bytes;
+    int num_candidates;
+    int candidates[kMaxPartitionCandidates];
 };
 DecodePlan plan_decode(const vkv_decode_params* p);
 int launch_decode(const vkv_decode_params* p, const DecodePlan& plan, void* workspace, hipStream_t st);
