@@ -132,6 +132,64 @@ def test_prefill_mixed_config3_sampled(vkv, oracle, cuda):
         assert_close(got[r:r + 1], ref, F16_ATOL, F16_RTOL, f"sequence {s} row {j}")
 
 
+def _mixed_inputs(cuda):
+    import torch
+    rng = np.random.default_rng(31)
+    H, Hkv, D, bs = 28, 4, 128, 32
+    q_lens = [300, 1, 1, 77, 1, 1, 1, 200] + [1] * 40
+    prior = rng.integers(0, 3000, len(q_lens)).tolist()
+    lay, ctx, qsl, q, k, v, scale = _case(H, Hkv, D, bs, q_lens, prior, 9)
+    args = [to_dev(x, cuda) for x in (q, k, v, lay.block_tables, ctx, qsl)]
+    out = torch.zeros((q.shape[0], H, D), dtype=torch.float16, device=cuda)
+    return out, args, int(max(q_lens)), scale
+
+
+def test_prefill_mixed_on_caller_stream(vkv, cuda):
+    """A mixed call (matrix-core rows and single-token decode rows) issued on a
+    non-default stream: after synchronising only that stream the output is
+    complete and equals a call on the default stream bit for bit."""
+    import torch
+    out, args, mql, scale = _mixed_inputs(cuda)
+    vkv.paged_prefill(out, *args, mql, scale)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    for _ in range(3):
+        out2 = torch.full_like(out, float("nan"))
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            vkv.paged_prefill(out2, *args, mql, scale, stream=s)
+            out2.record_stream(s)
+        s.synchronize()
+        assert torch.equal(out.view(torch.int16), out2.view(torch.int16))
+
+
+def test_prefill_mixed_graph_replays(vkv, cuda):
+    """A mixed call captured in a graph (work-list, prefill, decode and merge
+    kernels; the claim counters are reset by kernels, not memsets) replays to
+    the eager result, with eager calls on the same library workspace and
+    synchronisations between the replays."""
+    import torch
+    out, args, mql, scale = _mixed_inputs(cuda)
+    vkv.paged_prefill(out, *args, mql, scale)
+    torch.cuda.synchronize()
+    ref = out.clone()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        out.zero_()
+        with torch.cuda.graph(g, stream=s):
+            vkv.paged_prefill(out, *args, mql, scale, stream=s)
+    torch.cuda.synchronize()
+    for i in range(3):
+        out.fill_(float("nan"))
+        vkv.paged_prefill(torch.empty_like(out), *args, mql, scale)  # eager work between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(ref.view(torch.int16), out.view(torch.int16)), i
+
+
 def test_prefill_context_shorter_than_chunk(vkv, oracle, cuda):
     """context_lens below q_len (invalid input): rows whose position sees no key
     are zeros, the others attend the keys there are, and nothing is read out of

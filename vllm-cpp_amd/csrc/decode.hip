@@ -1357,9 +1357,12 @@ int launch_prefill(const vkv_prefill_params* p, const DecodePlan& plan, void* wo
     if (prefill_mfma_supported(p)) {
         // Mixed batch: the matrix-core kernel takes every sequence with two or
         // more query tokens, the decode kernels the single-token ones; each
-        // writes only its own output rows.  (Running the two on separate
-        // streams gained ~3 %: neither kernel's waves fit beside the other's
-        // on a CU, so they take turns either way.)
+        // writes only its own output rows.  All on the caller's stream: the
+        // decode kernels on a side stream forked from it and joined back were
+        // slower (C3's mixed call 339 us against 319 us, its prefill rows
+        // alone 127 us against 105 us; the cross-queue waits cost more than
+        // the overlap saves, as neither kernel's waves fit beside the other's
+        // on a CU).
         const size_t items_off = plan.workspace_bytes - prefill_items_bytes(p);
         const int rc = launch_prefill_mfma(p, static_cast<char*>(workspace) + items_off, st);
         if (rc) return rc;
