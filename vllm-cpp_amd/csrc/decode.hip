@@ -1021,8 +1021,11 @@ __global__ __launch_bounds__(D) void decode_reduce_kernel(DecodeArgs a) {
             bo[k] = o[int64_t(i) * G * D];
         }
     };
+    // A prefill sequence of a mixed call is not decoded here: leave before
+    // loading its (stale) partial slots, which a call without single-token
+    // rows would otherwise read for every (sequence, head).
+    if (a.qsl && a.qsl[s + 1] - a.qsl[s] != 1) return;
     load_batch(0);
-    if (a.qsl && a.qsl[s + 1] - a.qsl[s] != 1) return;  // a prefill sequence: not decoded here
     const int ctx = row_context(a, s);
     const int P = a.num_cands > 1 ? __builtin_amdgcn_readfirstlane(a.counters[kChosenPartitionSlot]) : a.P;
     const int np = ctx > 0 ? (ctx + P - 1) / P : 0;
