@@ -378,3 +378,45 @@ def test_decode_default_partition_choice(vkv, oracle, cuda):
         ref = oracle.paged_decode(qn[s:s + 1], kk, vv, np.arange(nblk, dtype=np.int32)[None, :],
                                   np.array([n], np.int32), scale)
         assert_close(got[s:s + 1], ref, F16_ATOL, F16_RTOL, f"row {s} (partition {chosen})")
+
+
+def test_decode_config5_sampled(vkv, oracle, cuda):
+    """Full C5 (Llama-3-8B shape, FP8 e4m3 cache with per-(token, head) scales, B=256,
+    lognormal contexts up to 22.6k tokens): the pool is quantised by the GPU append,
+    one decode call covers every sequence (items claimed past the grid), and the
+    longest, the shortest and a few other sequences are recomputed by the oracle from
+    their own FP8 blocks and scales."""
+    import torch
+    from vllm_kv_amd import workloads
+    cfg = workloads.config5()
+    lay = cfg.layout
+    S, H, Hkv, D, bs = cfg.num_seqs, cfg.num_heads, cfg.num_kv_heads, cfg.head_dim, cfg.block_size
+    N = lay.num_blocks
+    g = torch.Generator(device=cuda).manual_seed(41)
+    kc = torch.empty((N, bs, Hkv, D), dtype=torch.uint8, device=cuda)
+    vc = torch.empty_like(kc)
+    ks = torch.empty((N, bs, Hkv), dtype=torch.float32, device=cuda)
+    vs = torch.empty_like(ks)
+    slots = torch.arange(N * bs, dtype=torch.int32, device=cuda)
+    chunk = 1 << 20
+    for s0 in range(0, N * bs, chunk):
+        n = min(chunk, N * bs - s0)
+        x = torch.randn((2, n, Hkv, D), generator=g, device=cuda).half()
+        vkv.reshape_and_cache(x[0], x[1], kc, vc, slots[s0:s0 + n], ks, vs)
+        del x
+    q = torch.randn((S, H, D), generator=g, device=cuda).half()
+    out = torch.zeros((S, H, D), dtype=torch.float16, device=cuda)
+    vkv.paged_decode(out, q, kc, vc, to_dev(lay.block_tables, cuda), to_dev(lay.context_lens, cuda), cfg.scale,
+                     key_scales=ks, value_scales=vs)
+    torch.cuda.synchronize()
+    got = to_np(out).astype(np.float32)
+    qn = to_np(q).astype(np.float32)
+    ctx = lay.context_lens
+    for s in sorted({int(np.argmax(ctx)), int(np.argmin(ctx)), 0, 100, S - 1}):
+        n = int(ctx[s])
+        nblk = (n + bs - 1) // bs
+        ids = torch.from_numpy(lay.block_tables[s, :nblk]).long().to(cuda)
+        ref = oracle.paged_decode(qn[s:s + 1], to_np(kc[ids]), to_np(vc[ids]),
+                                  np.arange(nblk, dtype=np.int32)[None, :], np.array([n], np.int32), cfg.scale,
+                                  key_scales=to_np(ks[ids]), value_scales=to_np(vs[ids]))
+        assert_close(got[s:s + 1], ref, F16_ATOL, F16_RTOL, f"sequence {s} (ctx {n})")
