@@ -132,6 +132,43 @@ def test_prefill_mixed_config3_sampled(vkv, oracle, cuda):
         assert_close(got[r:r + 1], ref, F16_ATOL, F16_RTOL, f"sequence {s} row {j}")
 
 
+def test_prefill_large_call_list_kernel(vkv, oracle, cuda):
+    """A call with more row blocks than the fp16 kernel orders in LDS (here 720
+    blocks of 256 (token, head) rows, 80 sequences of 300 tokens at group 7):
+    the separate list kernel builds the longest-first order.  Sampled rows
+    against the oracle (row j of a sequence is decode over prior + j + 1 keys)."""
+    import torch
+    from vllm_kv_amd import workloads
+    rng = np.random.default_rng(17)
+    H, Hkv, D, bs, S, qn_ = 28, 4, 128, 16, 80, 300
+    q_lens = np.full(S, qn_, np.int32)
+    prior = rng.integers(0, 700, S).astype(np.int32)
+    ctx = prior + q_lens
+    lay = workloads.make_layout(ctx, bs, rng, slack=0.1)
+    qsl = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    Tq = int(qsl[-1])
+    g = torch.Generator(device=cuda).manual_seed(17)
+    shape = (lay.num_blocks, bs, Hkv, D)
+    kc = (torch.randn(shape, generator=g, device=cuda) * 0.5).half()
+    vc = (torch.randn(shape, generator=g, device=cuda) * 0.5).half()
+    q = (torch.randn((Tq, H, D), generator=g, device=cuda) * 0.5).half()
+    out = torch.zeros((Tq, H, D), dtype=torch.float16, device=cuda)
+    vkv.paged_prefill(out, q, kc, vc, to_dev(lay.block_tables, cuda), to_dev(ctx, cuda), to_dev(qsl, cuda),
+                      qn_, float(1.0 / np.sqrt(np.float32(D))))
+    torch.cuda.synchronize()
+    got = to_np(out).astype(np.float32)
+    qh = to_np(q).astype(np.float32)
+    for s, j in [(0, 0), (0, 299), (31, 150), (79, 299), (int(np.argmax(prior)), 299)]:
+        n = int(prior[s]) + j + 1
+        nblk = (n + bs - 1) // bs
+        ids = torch.from_numpy(lay.block_tables[s, :nblk]).long().to(cuda)
+        r = int(qsl[s]) + j
+        ref = oracle.paged_decode(qh[r:r + 1], to_np(kc[ids]).view(np.uint16), to_np(vc[ids]).view(np.uint16),
+                                  np.arange(nblk, dtype=np.int32)[None, :], np.array([n], np.int32),
+                                  float(1.0 / np.sqrt(np.float32(D))))
+        assert_close(got[r:r + 1], ref, F16_ATOL, F16_RTOL, f"sequence {s} row {j}")
+
+
 def _mixed_inputs(cuda):
     import torch
     rng = np.random.default_rng(31)

@@ -81,9 +81,6 @@ constexpr int kAdaptMaxRows = 4096;
 // Fixed cost of one item (partial write, merge input, chain start-up) in
 // token-equivalents, for the span estimate of the partition choice.
 constexpr int kItemOverheadTokens = 128;
-// Workspace header int holding the partition size the partition kernel
-// chose, read by the merge kernel (the claim counters use ints 0, 32, ...).
-constexpr int kChosenPartitionSlot = 1;
 // LDS per CU on gfx950, for the resident-wave estimate.
 constexpr int kLdsPerCu = 160 * 1024;
 
@@ -1006,6 +1003,8 @@ __global__ __launch_bounds__(D) void decode_reduce_kernel(DecodeArgs a) {
     // The partition kernel has finished (same stream): return its claim
     // counters to zero for the next call.
     if (s == 0 && h == 0 && d < kClaimSequences) a.counters[d * kCounterStride] = 0;
+    // and the prefill kernel's, when it ran before in the same call
+    if (s == 0 && h == 0 && d == kClaimSequences) a.counters[kPrefillClaimSlot] = 0;
     const int G = a.num_heads / a.num_kv_heads;
     const int kvh = h / G;
     const int64_t slot0 = (int64_t(s) * a.num_kv_heads + kvh) * a.max_parts * G + (h - kvh * G);
@@ -1367,7 +1366,8 @@ int launch_prefill(const vkv_prefill_params* p, const DecodePlan& plan, void* wo
         // the overlap saves, as neither kernel's waves fit beside the other's
         // on a CU).
         const size_t items_off = plan.workspace_bytes - prefill_items_bytes(p);
-        const int rc = launch_prefill_mfma(p, static_cast<char*>(workspace) + items_off, st);
+        const int rc = launch_prefill_mfma(p, static_cast<char*>(workspace) + items_off,
+                                           static_cast<int32_t*>(workspace) + kPrefillClaimSlot, st);
         if (rc) return rc;
         const vkv_decode_params d = prefill_as_decode(p, true);
         return launch_rows(&d, plan, workspace, nullptr, nullptr, p->query_start_loc, st);

@@ -39,7 +39,12 @@ int launch_prefill(const vkv_prefill_params* p, const DecodePlan& plan, void* wo
 vkv_decode_params prefill_as_decode(const vkv_prefill_params* p, bool per_sequence);
 bool prefill_mfma_supported(const vkv_prefill_params* p);
 size_t prefill_items_bytes(const vkv_prefill_params* p);
-int launch_prefill_mfma(const vkv_prefill_params* p, void* item_space, hipStream_t st);
+// inline_claim: a zeroed int the merge kernel of the same call resets (the
+// fp16 kernel's claim counter when it builds its own work list), or nullptr.
+int launch_prefill_mfma(const vkv_prefill_params* p, void* item_space, int32_t* inline_claim, hipStream_t st);
+// Decode workspace header ints (the claim counters use 0, 32, 64, ...).
+constexpr int kChosenPartitionSlot = 1;  // partition size the partition kernel chose
+constexpr int kPrefillClaimSlot = 2;     // claim counter of the fp16 prefill kernel's in-kernel list
 
 struct PlaneSet {
     char* base[4];

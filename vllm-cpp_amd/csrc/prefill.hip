@@ -74,6 +74,13 @@ struct PrefillArgs {
     const int2* items;       // work list (s, b * Hkv + kvh), b the sequence's row block
     int32_t* item_count;     // [0] items, [1 + z] claim counter of head group z (zeroed by the list kernel)
     float scale_log2;
+    // fp16 kernel, calls of at most kInlineBlocks row blocks: every workgroup
+    // orders the blocks itself (no list kernel); inline_claim is the claim
+    // counter (zero at entry, reset by the merge kernel that follows)
+    int32_t inline_list;
+    int32_t* inline_claim;
+    int32_t rows_per_item;
+    int32_t nbins;
 };
 
 template <int D, int KVT>
@@ -516,6 +523,25 @@ struct WideBuffers {
     int* btc;  // block ids of the item (kWideBtc)
 };
 
+// Row blocks of a sequence with q query tokens (row_mult rows per token,
+// rows_per_item per block; single-token sequences belong to decode), at most
+// max_qblocks (max_query_len bounds q: caller contract).
+__device__ __forceinline__ int seq_row_blocks(int q, int row_mult, int rows_per_item, int max_qblocks) {
+    const int n = q >= 2 ? int((int64_t(q) * row_mult + rows_per_item - 1) / rows_per_item) : 0;
+    return n < max_qblocks ? n : max_qblocks;
+}
+// Bin of row block b: nbins - 1 - (key tiles it stages, capped), so that the
+// ascending bin order is the longest-first order.  Block b sees keys
+// 0 .. kend - 1, kend = prior + its last token + 1 (clamped to the table).
+__device__ __forceinline__ int row_block_bin(int prior, int q, int b, int row_mult, int rows_per_item,
+                                             int table_tokens, int nbins) {
+    const int64_t last = (int64_t(b + 1) * rows_per_item - 1) / row_mult + 1;
+    int64_t kend = prior + (last < q ? last : q);
+    kend = kend < table_tokens ? kend : table_tokens;
+    const int64_t tiles = kend > 0 ? (kend + kBK - 1) / kBK : 0;
+    return nbins - 1 - int(tiles < nbins - 1 ? tiles : nbins - 1);
+}
+
 template <int D>
 __device__ __forceinline__ void prefill_block_wide(const PrefillArgs& a, const int s, const int b, const int kvh,
                                                    const WideBuffers& buf) {
@@ -817,6 +843,71 @@ __device__ __forceinline__ void prefill_block_wide(const PrefillArgs& a, const i
     }
 }
 
+// In-kernel work list of a small call, built by every workgroup of the fp16
+// kernel alike (so no list kernel runs before it): the row blocks are
+// numbered in (sequence, block) order, each block's sort key is (bin, number)
+// and its place in the longest-first order is the count of smaller keys.  The
+// keys are distinct, so every workgroup computes the same order; the ranking
+// is quadratic, which at kInlineBlocks blocks is a few hundred LDS reads per
+// thread.  Returns the number of blocks; lblk holds them in order.
+constexpr int kInlineBlocks = 64 * kWideWaves;  // one per thread
+__device__ int inline_row_blocks(const PrefillArgs& a, int2* lblk) {
+    __shared__ int key[kInlineBlocks];
+    __shared__ int wave_tot[kWideWaves];
+    __shared__ int carry;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (tid == 0) carry = 0;
+    __syncthreads();
+    // number the blocks: sequences in chunks of one per thread, block counts
+    // scanned across the workgroup
+    for (int s0 = 0; s0 < a.num_seqs; s0 += kInlineBlocks) {
+        const int s = s0 + tid;
+        int q = 0, prior = 0, n = 0;
+        if (s < a.num_seqs) {
+            q = a.qsl[s + 1] - a.qsl[s];
+            prior = a.cl[s] - q;
+            n = seq_row_blocks(q, a.group, a.rows_per_item, a.qblocks);
+        }
+        int incl = n;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += y;
+        }
+        if (lane == 63) wave_tot[wave] = incl;
+        __syncthreads();
+        int before = carry;
+        for (int w = 0; w < wave; ++w) before += wave_tot[w];
+        for (int b = 0; b < n; ++b) {
+            const int i = before + incl - n + b;
+            if (i < kInlineBlocks) {  // (the host bound keeps every call within)
+                key[i] = (row_block_bin(prior, q, b, a.group, a.rows_per_item, a.table_tokens, a.nbins) << 9) | i;
+                lblk[i] = int2{s, b};
+            }
+        }
+        __syncthreads();
+        if (tid == 0) {
+            int t = carry;
+            for (int w = 0; w < kWideWaves; ++w) t += wave_tot[w];
+            carry = t;
+        }
+        __syncthreads();
+    }
+    const int total = carry < kInlineBlocks ? carry : kInlineBlocks;
+    // rank, then place (lblk is read before the barrier and written after it)
+    int2 mine = int2{0, 0};
+    int rank = 0;
+    if (tid < total) {
+        const int k = key[tid];
+        mine = lblk[tid];
+        for (int j = 0; j < total; ++j) rank += key[j] < k ? 1 : 0;
+    }
+    __syncthreads();
+    if (tid < total) lblk[rank] = mine;
+    __syncthreads();
+    return total;
+}
+
 template <int D>
 __global__ __launch_bounds__(64 * kWideWaves) void prefill_wide_kernel(PrefillArgs a) {
     __shared__ __attribute__((aligned(1024))) char k0[DmaTile<D>::BYTES];
@@ -829,14 +920,30 @@ __global__ __launch_bounds__(64 * kWideWaves) void prefill_wide_kernel(PrefillAr
     static_assert(kWideStages == 3, "three K and three V buffers");
     const WideBuffers buf = {{k0, k1, k2}, {v0, v1, v2}, btc};
     __shared__ int claimed;
-    const int count = a.item_count[0];
+    __shared__ int2 lblk[kInlineBlocks];  // inline list: (s, b) of row block i, then in longest-first order
+    int count;
+    int* claim;
+    if (a.inline_list) {
+        count = inline_row_blocks(a, lblk) * a.num_kv_heads;
+        claim = a.inline_claim;
+    } else {
+        count = a.item_count[0];
+        claim = a.item_count + 1;
+    }
     for (;;) {
-        if (threadIdx.x == 0) claimed = atomicAdd(a.item_count + 1, 1);
+        if (threadIdx.x == 0) claimed = atomicAdd(claim, 1);
         __syncthreads();
         const int it = claimed;
         __syncthreads();
         if (it >= count) break;
-        const int2 item = a.items[it];
+        // items (row block, kv head), kv head fastest
+        int2 item;
+        if (a.inline_list) {
+            const int2 blk = lblk[it / a.num_kv_heads];
+            item = int2{blk.x, blk.y * a.num_kv_heads + it % a.num_kv_heads};
+        } else {
+            item = a.items[it];
+        }
         prefill_block_wide<D>(a, item.x, item.y / a.num_kv_heads, item.y % a.num_kv_heads, buf);
     }
 }
@@ -897,18 +1004,9 @@ __global__ __launch_bounds__(256) void prefill_items_kernel(const int32_t* qsl, 
     const int tid = threadIdx.x;
     for (int i = tid; i < nbins; i += 256) off[i] = fill[i] = 0;
     __syncthreads();
-    // row blocks of sequence s (max_query_len bounds q_len: caller contract)
-    auto blocks = [&](int q) {
-        const int n = q >= 2 ? int((int64_t(q) * row_mult + rows_per_item - 1) / rows_per_item) : 0;
-        return n < max_qblocks ? n : max_qblocks;
-    };
-    // bin of row block b: nbins - 1 - (its key tiles), most tiles first
+    auto blocks = [&](int q) { return seq_row_blocks(q, row_mult, rows_per_item, max_qblocks); };
     auto bin = [&](int prior, int q, int b) {
-        const int64_t last = (int64_t(b + 1) * rows_per_item - 1) / row_mult + 1;
-        int64_t kend = prior + (last < q ? last : q);
-        kend = kend < table_tokens ? kend : table_tokens;
-        const int64_t tiles = kend > 0 ? (kend + kBK - 1) / kBK : 0;
-        return nbins - 1 - int(tiles < nbins - 1 ? tiles : nbins - 1);
+        return row_block_bin(prior, q, b, row_mult, rows_per_item, table_tokens, nbins);
     };
     for (int s = tid; s < num_seqs; s += 256) {
         const int q = qsl[s + 1] - qsl[s];
@@ -951,7 +1049,7 @@ size_t prefill_items_bytes(const vkv_prefill_params* p) {
     return 256 + size_t(int64_t(p->num_seqs) * qblocks * p->num_kv_heads) * sizeof(int2);
 }
 
-int launch_prefill_mfma(const vkv_prefill_params* p, void* item_space, hipStream_t st) {
+int launch_prefill_mfma(const vkv_prefill_params* p, void* item_space, int32_t* inline_claim, hipStream_t st) {
     PrefillArgs a;
     a.out = static_cast<_Float16*>(p->output);
     a.q = static_cast<const char*>(p->query);
@@ -988,9 +1086,20 @@ int launch_prefill_mfma(const vkv_prefill_params* p, void* item_space, hipStream
     // bins: every possible tile count (items past kMaxLevels - 1 tiles share the last)
     const int64_t max_tiles = (int64_t(a.table_tokens) + kBK - 1) / kBK;
     const int nbins = int(max_tiles + 1 < kMaxLevels ? max_tiles + 1 : kMaxLevels);
-    hipLaunchKernelGGL(prefill_items_kernel, dim3(1), dim3(256), 0, st, p->query_start_loc, p->context_lens,
-                       p->num_seqs, p->num_kv_heads, row_mult, rows_per_item, a.qblocks, a.table_tokens, nbins,
-                       items, count);
+    a.rows_per_item = rows_per_item;
+    a.nbins = nbins;
+    // Row blocks, at most: a sequence of q >= 2 tokens has ceil(q G / R) <=
+    // q G / R + 1 of them, and there are at most min(S, T / 2) such sequences
+    // (T query tokens).  Small calls order them in the kernel itself.
+    const int64_t T = p->num_query_tokens;
+    const int64_t nseq2 = p->num_seqs < T / 2 ? p->num_seqs : T / 2;
+    const int64_t bound = T * row_mult / rows_per_item + nseq2;
+    a.inline_list = wide && inline_claim != nullptr && bound <= kInlineBlocks;
+    a.inline_claim = inline_claim;
+    if (!a.inline_list)
+        hipLaunchKernelGGL(prefill_items_kernel, dim3(1), dim3(256), 0, st, p->query_start_loc, p->context_lens,
+                           p->num_seqs, p->num_kv_heads, row_mult, rows_per_item, a.qblocks, a.table_tokens, nbins,
+                           items, count);
     // Persistent grid, never more workgroups than there can be items: one per
     // CU for the wide kernel (its LDS and registers fill a CU); two per CU for
     // the FP8 kernel (at D = 128 one is resident, the other starts when a CU
