@@ -921,17 +921,13 @@ __global__ __launch_bounds__(64 * kWideWaves) void prefill_wide_kernel(PrefillAr
     const WideBuffers buf = {{k0, k1, k2}, {v0, v1, v2}, btc};
     __shared__ int claimed;
     __shared__ int2 lblk[kInlineBlocks];  // inline list: (s, b) of row block i, then in longest-first order
-    int count;
-    int* claim;
-    if (a.inline_list) {
-        count = inline_row_blocks(a, lblk) * a.num_kv_heads;
-        claim = a.inline_claim;
-    } else {
-        count = a.item_count[0];
-        claim = a.item_count + 1;
-    }
+    int* claim = a.inline_list ? a.inline_claim : a.item_count + 1;
+    // the first claim travels while the list is built (or its length loaded)
+    int first = 0;
+    if (threadIdx.x == 0) first = atomicAdd(claim, 1);
+    const int count = a.inline_list ? inline_row_blocks(a, lblk) * a.num_kv_heads : a.item_count[0];
+    if (threadIdx.x == 0) claimed = first;
     for (;;) {
-        if (threadIdx.x == 0) claimed = atomicAdd(claim, 1);
         __syncthreads();
         const int it = claimed;
         __syncthreads();
@@ -945,6 +941,7 @@ __global__ __launch_bounds__(64 * kWideWaves) void prefill_wide_kernel(PrefillAr
             item = a.items[it];
         }
         prefill_block_wide<D>(a, item.x, item.y / a.num_kv_heads, item.y % a.num_kv_heads, buf);
+        if (threadIdx.x == 0) claimed = atomicAdd(claim, 1);
     }
 }
 
