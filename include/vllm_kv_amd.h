@@ -189,11 +189,15 @@ int vkv_rope_cos_sin_host(float theta, int32_t head_dim, int32_t max_position, f
  *
  * Long contexts are split into partitions of partition_size tokens that are
  * reduced by a second kernel; that needs vkv_paged_decode_workspace_size()
- * bytes of device workspace.  workspace == NULL uses a buffer the library
+ * bytes of device workspace.  With partition_size 0 the kernels choose the
+ * size per call from the device-side context lengths (5/6 to 2 times the
+ * default; the workspace size covers the smallest), so results may differ in
+ * the last bits from an explicit size.  workspace == NULL uses a buffer the library
  * owns per device (grown with hipMalloc on first use, never shrunk).  A
  * caller workspace must have its first 1024 bytes zeroed before its first use
- * (work counters; every call leaves them zero again), and calls that may run
- * concurrently need distinct workspaces.  At most 16000 sequences per call.
+ * (work counters; every call leaves them zero again, apart from int 1, the
+ * partition size the call chose), and calls that may run concurrently need
+ * distinct workspaces.  At most 16000 sequences per call.
  * ------------------------------------------------------------------------- */
 typedef struct vkv_decode_params {
     void* output;               /* [num_seqs, num_heads, head_dim] io_dtype */
@@ -217,7 +221,7 @@ typedef struct vkv_decode_params {
     int32_t io_dtype;
     int32_t kv_dtype;
     int32_t accumulate;
-    int32_t partition_size;     /* tokens per split-K partition; 0 = library default */
+    int32_t partition_size;     /* tokens per split-K partition; 0 = the library picks it per call on the device */
     void* workspace;            /* optional, see above */
     size_t workspace_bytes;
 } vkv_decode_params;
