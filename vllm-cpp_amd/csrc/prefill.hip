@@ -7,9 +7,11 @@
 // sequence's paged cache, i.e. causal attention over the prior context plus
 // the chunk.  Keys are gathered through the block table like decode.
 //
-// Two kernels share the matrix-core layout below: prefill_wide_kernel for fp16
+// The kernels share the matrix-core layout below: prefill_wide_kernel for fp16
 // caches (work items of (token, head) rows, tiles staged by direct
-// global->LDS loads) and prefill_mfma_kernel for FP8 caches.  In the latter a
+// global->LDS loads), prefill_wide8_kernel for FP8 caches at head_dim 128 (the
+// same, with the code tiles converted to fp16 in LDS once per workgroup) and
+// prefill_mfma_kernel for FP8 caches at head_dim 64.  In the last a
 // workgroup owns (sequence, kv head, block of kBQ = 32 query tokens); wave w
 // computes query head kvh * G + w for those 32 tokens as two 16-row MFMA
 // tiles, so the G heads that share a kv head share every K/V tile staged in
@@ -464,6 +466,26 @@ struct DmaTile {
     __device__ static __forceinline__ int off(int row, int chunk) { return row * ROW + ((chunk ^ (row % CH)) << 4); }
 };
 
+// FP8 caches on the same kernel (D = 128): the codes reach LDS by direct
+// loads in rows of D bytes (same swizzle), the token scales by one 4-byte
+// direct load per wave (waves of one parity load the same 64 K or V scales),
+// and the workgroup converts each tile once into the fp16 tile that the fp16
+// path computes from (code x scale in fp32, rounded to fp16, as the
+// register-staged kernel does).
+template <int D>
+struct DmaTile8 {
+    static constexpr int ROW = D;
+    static constexpr int CH = ROW / 16;
+    static constexpr int RPI = 1024 / ROW;
+    static constexpr int INST = kBK / RPI;
+    static constexpr int BYTES = kBK * ROW;
+    __device__ static __forceinline__ int off(int row, int chunk) { return row * ROW + ((chunk ^ (row % CH)) << 4); }
+};
+constexpr bool kFp8Wide = true;  // FP8 at D = 128 on the direct-load kernel
+
+// Workgroup barrier without a vector-memory wait (LDS writes published).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory"); }
+
 // s_waitcnt with only the vector-memory count limited (GFX9 encoding: vmcnt
 // bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima).
 template <int N>
@@ -518,9 +540,12 @@ struct Wide {
 // another (with one shared array it waits for every load in flight before
 // each LDS read, which would undo the loads' lead).
 struct WideBuffers {
-    char* k[3];
+    char* k[3];    // fp16 tiles (FP8: k[0] / v[0], the converted tile)
     char* v[3];
-    int* btc;  // block ids of the item (kWideBtc)
+    int* btc;      // block ids of the item (kWideBtc)
+    char* f8k[3];  // FP8: the code tiles of the three stages
+    char* f8v[3];
+    float* sc[3];  // FP8: 64 key scales, then 64 value scales, per stage
 };
 
 // Row blocks of a sequence with q query tokens (row_mult rows per token,
@@ -542,16 +567,20 @@ __device__ __forceinline__ int row_block_bin(int prior, int q, int b, int row_mu
     return nbins - 1 - int(tiles < nbins - 1 ? tiles : nbins - 1);
 }
 
-template <int D>
+template <int D, bool FP8>
 __device__ __forceinline__ void prefill_block_wide(const PrefillArgs& a, const int s, const int b, const int kvh,
                                                    const WideBuffers& buf) {
-    using T = DmaTile<D>;
+    using T = DmaTile<D>;  // the fp16 tile the MFMAs read
+    using L = typename std::conditional<FP8, DmaTile8<D>, DmaTile<D>>::type;  // the tile the loads fill
+    constexpr int EB = FP8 ? 1 : 2;
     constexpr int DT = D / 16;  // output dim tiles
     constexpr int KS = D / 32;  // MFMA k-steps of Q K^T
     constexpr int RT = Wide<D>::RT;
     constexpr int kWideRows = Wide<D>::ROWS;
-    constexpr int JW = T::INST / kWideWaves;  // direct loads per K (or V) tile and wave
-    static_assert(T::INST % kWideWaves == 0, "the loads of a tile must split evenly over the waves");
+    constexpr int JW = L::INST / kWideWaves;  // direct loads per K (or V) tile and wave
+    constexpr int NLOAD = 2 * JW + (FP8 ? 1 : 0);  // vector-memory operations per tile and wave
+    static_assert(L::INST % kWideWaves == 0, "the loads of a tile must split evenly over the waves");
+    static_assert(!FP8 || D == 128, "FP8 conversion maps 512 threads to 64 rows x 8 chunks");
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -573,21 +602,21 @@ __device__ __forceinline__ void prefill_block_wide(const PrefillArgs& a, const i
 
     // ---------------- loads of tile t, through block ids held in LDS
     const int bs_mask = (1 << a.bs_log2) - 1;
-    const uint32_t row_bytes32 = uint32_t(a.num_kv_heads) * D * 2;
+    const uint32_t row_bytes32 = uint32_t(a.num_kv_heads) * D * EB;
     // this lane's bytes within the cache row of its load j: the kv head and
     // the chunk that the swizzle puts at its LDS slot (the same in every tile)
     uint32_t lane_off[JW];
 #pragma unroll
     for (int j = 0; j < JW; ++j) {
-        const int row = (wave * JW + j) * T::RPI + lane / T::CH;
-        lane_off[j] = uint32_t(kvh) * D * 2 + uint32_t(((lane % T::CH) ^ (row % T::CH)) * 16);
+        const int row = (wave * JW + j) * L::RPI + lane / L::CH;
+        lane_off[j] = uint32_t(kvh) * D * EB + uint32_t(((lane % L::CH) ^ (row % L::CH)) * 16);
     }
     const int32_t* table = a.bt + int64_t(s) * a.max_blocks_per_seq;
     // key of this lane's row in load j of tile t (keys past the end: kend - 1
     // again, masked; key 0 for an item with no keys at all, whose loads are
     // still issued so that the vmcnt counts below stay exact)
     auto load_key = [&](const int t, const int j) __attribute__((always_inline)) {
-        int k = t * kBK + (wave * JW + j) * T::RPI + lane / T::CH;
+        int k = t * kBK + (wave * JW + j) * L::RPI + lane / L::CH;
         k = k < kend ? k : kend - 1;
         return k > 0 ? k : 0;
     };
@@ -610,8 +639,8 @@ __device__ __forceinline__ void prefill_block_wide(const PrefillArgs& a, const i
     // (slots are int32 in the API: slot_mapping, num_blocks * block_size)
     auto load_tile = [&](auto stage, const int t) __attribute__((always_inline)) {
         constexpr int S = decltype(stage)::value;
-        char* kdst = buf.k[S];
-        char* vdst = buf.v[S];
+        char* kdst = FP8 ? buf.f8k[S] : buf.k[S];
+        char* vdst = FP8 ? buf.f8v[S] : buf.v[S];
 #pragma unroll
         for (int j = 0; j < JW; ++j) {
             const int jj = wave * JW + j;
@@ -624,6 +653,33 @@ __device__ __forceinline__ void prefill_block_wide(const PrefillArgs& a, const i
             __builtin_amdgcn_global_load_lds(a.vc + off, (__attribute__((address_space(3))) void*)(vdst + jj * 1024),
                                              16, 0, 0);
         }
+        if constexpr (FP8) {
+            // lane l: the scale of key t * 64 + l (clamped like the rows);
+            // even waves the key scales, odd waves the value scales
+            int k = t * kBK + lane;
+            k = k < kend ? k : kend - 1;
+            k = k > 0 ? k : 0;
+            const int id = btc[(k >> a.bs_log2) - win];
+            const uint32_t slot = (uint32_t(id) << a.bs_log2) + uint32_t(k & bs_mask);
+            const float* src = ((wave & 1) ? a.vs : a.ks) + (uint64_t(slot) * a.num_kv_heads + kvh);
+            __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(buf.sc[S] + 64 * (wave & 1)),
+                                             4, 0, 0);
+        }
+    };
+    // FP8: the codes of stage S into the fp16 tile (thread: key row tid / 8,
+    // 16 codes of chunk tid % 8, i.e. fp16 chunks 2 c and 2 c + 1)
+    auto convert = [&](auto stage) __attribute__((always_inline)) {
+        constexpr int S = decltype(stage)::value;
+        const int r = tid >> 3, c = tid & 7;
+        const int src = L::off(r, c);
+        const uint32_t ksb = __builtin_bit_cast(uint32_t, buf.sc[S][r]);
+        const uint32_t vsb = __builtin_bit_cast(uint32_t, buf.sc[S][64 + r]);
+        const u32x4 kw = *reinterpret_cast<const u32x4*>(buf.f8k[S] + src);
+        const u32x4 vw = *reinterpret_cast<const u32x4*>(buf.f8v[S] + src);
+        *reinterpret_cast<u32x4*>(buf.k[0] + T::off(r, 2 * c)) = to_half8<kFp8>(u32x4{kw[0], kw[1], ksb, 0u});
+        *reinterpret_cast<u32x4*>(buf.k[0] + T::off(r, 2 * c + 1)) = to_half8<kFp8>(u32x4{kw[2], kw[3], ksb, 0u});
+        *reinterpret_cast<u32x4*>(buf.v[0] + T::off(r, 2 * c)) = to_half8<kFp8>(u32x4{vw[0], vw[1], vsb, 0u});
+        *reinterpret_cast<u32x4*>(buf.v[0] + T::off(r, 2 * c + 1)) = to_half8<kFp8>(u32x4{vw[2], vw[3], vsb, 0u});
     };
 
     fill_window(0);
@@ -777,7 +833,7 @@ __device__ __forceinline__ void prefill_block_wide(const PrefillArgs& a, const i
     // masked: the causal / context mask may cut into the tile.
     auto tile = [&](auto stage, auto masked, const int t) __attribute__((always_inline)) {
         constexpr int S = decltype(stage)::value;
-        tile_barrier<2 * JW>();  // tile t published (t + 1 in flight); every wave has left tile t - 1
+        tile_barrier<NLOAD>();  // tile t published (t + 1 in flight); every wave has left tile t - 1
         {
             // the block ids of tile t + 2 must be in the window (every wave has
             // issued tile t + 1's loads, the last reads of the old window)
@@ -788,8 +844,12 @@ __device__ __forceinline__ void prefill_block_wide(const PrefillArgs& a, const i
             }
         }
         load_tile(std::integral_constant<int, (S + 2) % kWideStages>(), t + 2);  // buffer of tile t - 1
-        const char* kcur = buf.k[S];
-        const char* vcur = buf.v[S];
+        if constexpr (FP8) {
+            convert(stage);  // every wave has left the fp16 tile (barrier above)
+            lds_barrier();
+        }
+        const char* kcur = FP8 ? buf.k[0] : buf.k[S];
+        const char* vcur = FP8 ? buf.v[0] : buf.v[S];
         float4_t sv[RT][2];
         half8_t pop[RT];
         qk(kcur, sv);
@@ -908,17 +968,9 @@ __device__ int inline_row_blocks(const PrefillArgs& a, int2* lblk) {
     return total;
 }
 
-template <int D>
-__global__ __launch_bounds__(64 * kWideWaves) void prefill_wide_kernel(PrefillArgs a) {
-    __shared__ __attribute__((aligned(1024))) char k0[DmaTile<D>::BYTES];
-    __shared__ __attribute__((aligned(1024))) char k1[DmaTile<D>::BYTES];
-    __shared__ __attribute__((aligned(1024))) char k2[DmaTile<D>::BYTES];
-    __shared__ __attribute__((aligned(1024))) char v0[DmaTile<D>::BYTES];
-    __shared__ __attribute__((aligned(1024))) char v1[DmaTile<D>::BYTES];
-    __shared__ __attribute__((aligned(1024))) char v2[DmaTile<D>::BYTES];
-    __shared__ int btc[kWideBtc];
-    static_assert(kWideStages == 3, "three K and three V buffers");
-    const WideBuffers buf = {{k0, k1, k2}, {v0, v1, v2}, btc};
+// Persistent claim loop of the direct-load kernels.
+template <int D, bool FP8>
+__device__ __forceinline__ void wide_items(const PrefillArgs& a, const WideBuffers& buf) {
     __shared__ int claimed;
     __shared__ int2 lblk[kInlineBlocks];  // inline list: (s, b) of row block i, then in longest-first order
     int* claim = a.inline_list ? a.inline_claim : a.item_count + 1;
@@ -940,9 +992,44 @@ __global__ __launch_bounds__(64 * kWideWaves) void prefill_wide_kernel(PrefillAr
         } else {
             item = a.items[it];
         }
-        prefill_block_wide<D>(a, item.x, item.y / a.num_kv_heads, item.y % a.num_kv_heads, buf);
+        prefill_block_wide<D, FP8>(a, item.x, item.y / a.num_kv_heads, item.y % a.num_kv_heads, buf);
         if (threadIdx.x == 0) claimed = atomicAdd(claim, 1);
     }
+}
+
+template <int D>
+__global__ __launch_bounds__(64 * kWideWaves) void prefill_wide_kernel(PrefillArgs a) {
+    __shared__ __attribute__((aligned(1024))) char k0[DmaTile<D>::BYTES];
+    __shared__ __attribute__((aligned(1024))) char k1[DmaTile<D>::BYTES];
+    __shared__ __attribute__((aligned(1024))) char k2[DmaTile<D>::BYTES];
+    __shared__ __attribute__((aligned(1024))) char v0[DmaTile<D>::BYTES];
+    __shared__ __attribute__((aligned(1024))) char v1[DmaTile<D>::BYTES];
+    __shared__ __attribute__((aligned(1024))) char v2[DmaTile<D>::BYTES];
+    __shared__ int btc[kWideBtc];
+    static_assert(kWideStages == 3, "three K and three V buffers");
+    const WideBuffers buf = {{k0, k1, k2}, {v0, v1, v2}, btc, {nullptr, nullptr, nullptr},
+                             {nullptr, nullptr, nullptr}, {nullptr, nullptr, nullptr}};
+    wide_items<D, false>(a, buf);
+}
+
+// FP8 caches at D = 128: three stages of code tiles and scales, one fp16 tile.
+__global__ __launch_bounds__(64 * kWideWaves) void prefill_wide8_kernel(PrefillArgs a) {
+    constexpr int D = 128;
+    __shared__ __attribute__((aligned(1024))) char k0[DmaTile<D>::BYTES];
+    __shared__ __attribute__((aligned(1024))) char v0[DmaTile<D>::BYTES];
+    __shared__ __attribute__((aligned(1024))) char fk0[DmaTile8<D>::BYTES];
+    __shared__ __attribute__((aligned(1024))) char fk1[DmaTile8<D>::BYTES];
+    __shared__ __attribute__((aligned(1024))) char fk2[DmaTile8<D>::BYTES];
+    __shared__ __attribute__((aligned(1024))) char fv0[DmaTile8<D>::BYTES];
+    __shared__ __attribute__((aligned(1024))) char fv1[DmaTile8<D>::BYTES];
+    __shared__ __attribute__((aligned(1024))) char fv2[DmaTile8<D>::BYTES];
+    __shared__ __attribute__((aligned(256))) float sc0[2 * kBK];
+    __shared__ __attribute__((aligned(256))) float sc1[2 * kBK];
+    __shared__ __attribute__((aligned(256))) float sc2[2 * kBK];
+    __shared__ int btc[kWideBtc];
+    const WideBuffers buf = {{k0, nullptr, nullptr}, {v0, nullptr, nullptr}, btc, {fk0, fk1, fk2},
+                             {fv0, fv1, fv2}, {sc0, sc1, sc2}};
+    wide_items<D, true>(a, buf);
 }
 
 // Work list of the matrix-core kernels, in one workgroup: items (s, b * Hkv +
@@ -1063,7 +1150,7 @@ int launch_prefill_mfma(const vkv_prefill_params* p, void* item_space, int32_t* 
     a.group = p->num_heads / p->num_kv_heads;
     // fp16 caches: prefill_wide_kernel, Wide<D>::ROWS (token, head) rows per item;
     // FP8: prefill_mfma_kernel, up to kMaxWaves heads x kBQ tokens per item
-    const bool wide = p->kv_dtype == VKV_DTYPE_F16;
+    const bool wide = p->kv_dtype == VKV_DTYPE_F16 || (kFp8Wide && p->head_dim == 128);
     const int head_groups = wide ? 1 : (a.group + kMaxWaves - 1) / kMaxWaves;
     a.heads_per_wg = (a.group + head_groups - 1) / head_groups;
     a.bs_log2 = ilog2i(p->block_size);
@@ -1110,8 +1197,9 @@ int launch_prefill_mfma(const vkv_prefill_params* p, void* item_space, int32_t* 
     const dim3 grid(unsigned(wgs > 0 ? wgs : 1), 1u, unsigned(head_groups));
     const dim3 block(unsigned(64 * waves));
     if (p->head_dim == 128) {
-        if (wide) hipLaunchKernelGGL((prefill_wide_kernel<128>), grid, block, 0, st, a);
-        else hipLaunchKernelGGL((prefill_mfma_kernel<128, kFp8>), grid, block, 0, st, a);
+        if (!wide) hipLaunchKernelGGL((prefill_mfma_kernel<128, kFp8>), grid, block, 0, st, a);
+        else if (p->kv_dtype == VKV_DTYPE_F16) hipLaunchKernelGGL((prefill_wide_kernel<128>), grid, block, 0, st, a);
+        else hipLaunchKernelGGL(prefill_wide8_kernel, grid, block, 0, st, a);
     } else {
         if (wide) hipLaunchKernelGGL((prefill_wide_kernel<64>), grid, block, 0, st, a);
         else hipLaunchKernelGGL((prefill_mfma_kernel<64, kFp8>), grid, block, 0, st, a);
