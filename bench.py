@@ -32,22 +32,52 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
+def source_blob(rel):
+    """git's blob id of a committed source file (sha1 of "blob <size>\\0" + bytes),
+    computed without git, so that a summary can name the exact kernel source it
+    measured and the GPU box (no .git there) can check it."""
+    import hashlib
+    with open(os.path.join(ROOT, rel), "rb") as f:
+        data = f.read()
+    return hashlib.sha1(b"blob %d\0" % len(data) + data).hexdigest()
+
+
+DECODE_SRC = "vllm-cpp_amd/csrc/decode.hip"
+
+
 def measured_traffic():
     """HBM bytes per decode call from the committed rocprofv3 PMC summary
-    (profiles/decode_c2_traffic.md: FETCH_SIZE and WRITE_SIZE, calibrated on a
-    1 GiB copy); None if that summary is absent."""
+    (profiles/decode_c2_traffic.json: FETCH_SIZE and WRITE_SIZE, calibrated on a
+    1 GiB copy), or None with the reason when that summary is absent or was
+    measured on another decode.hip than the one built here."""
     path = os.path.join(ROOT, "profiles", "decode_c2_traffic.json")
     try:
         with open(path) as f:
-            return int(json.load(f)["traffic_bytes_per_launch"])
+            d = json.load(f)
+        traffic = int(d["traffic_bytes_per_launch"])
     except (OSError, ValueError, KeyError):
-        return None
+        return None, "no committed traffic summary"
+    if d.get("decode_hip_blob") != source_blob(DECODE_SRC):
+        return None, "the committed traffic summary measured another decode.hip"
+    return traffic, f"profiles/decode_c2_traffic.json (commit {d.get('commit', '?')})"
 
 
-def cpu_baseline(kc, vc, q, lay, cfg, num_seqs=64, min_seconds=10.0):
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(kc, vc, q, lay, cfg, num_seqs=64, min_seconds=10.0, min_seconds_1t=8.0):
     """CPU oracle decode (oracle/kv_oracle.c, a C restatement of the reference
     kernel) on the first num_seqs sequences, repeated until min_seconds have
-    passed; threads = host cores (<= 16)."""
+    passed, on the host's cores (<= 16 threads), then on one thread."""
     import numpy as np
     import torch
     from oracle import oracle
@@ -66,20 +96,28 @@ def cpu_baseline(kc, vc, q, lay, cfg, num_seqs=64, min_seconds=10.0):
     qn = q[idx].float().cpu().numpy()
     threads = max(1, min(16, os.cpu_count() or 1))
     oracle.paged_decode(qn[:1], kk, vv, tables[:1], np.minimum(ctx[:1], 16), cfg.scale, nthreads=1)  # tables init
-    reps = 0
-    t0 = time.perf_counter()
-    while True:
-        oracle.paged_decode(qn, kk, vv, tables, ctx, cfg.scale, nthreads=threads)
-        reps += 1
-        dt = time.perf_counter() - t0
-        if dt >= min_seconds:
-            break
-    sample_bytes = reps * int(ctx.astype(np.int64).sum()) * cfg.num_kv_heads * cfg.head_dim * 2 * 2
-    return {"value": round(sample_bytes / dt / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+
+    def timed(nthreads, seconds):
+        reps = 0
+        t0 = time.perf_counter()
+        while True:
+            oracle.paged_decode(qn, kk, vv, tables, ctx, cfg.scale, nthreads=nthreads)
+            reps += 1
+            dt = time.perf_counter() - t0
+            if dt >= seconds:
+                return dt, reps
+
+    dt, reps = timed(threads, min_seconds)
+    dt1, reps1 = timed(1, min_seconds_1t)
+    call_bytes = int(ctx.astype(np.int64).sum()) * cfg.num_kv_heads * cfg.head_dim * 2 * 2
+    return {"value": round(reps * call_bytes / dt / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
             "us_per_call": round(dt / reps * 1e6, 1),
+            "value_1_thread": round(reps1 * call_bytes / dt1 / 1e9, 4),
+            "us_per_call_1_thread": round(dt1 / reps1 * 1e6, 1),
+            "cpu_model": cpu_model(), "host_cpus": os.cpu_count(),
             "sample": f"oracle decode (C restatement of the reference kernel) of {num_seqs} of the "
-                      f"{cfg.num_seqs} C2 sequences ({int(ctx.sum())} KV tokens, fp16 KV, fp32 math), "
-                      f"{reps} calls in {dt:.1f} s on {threads} threads"}
+                      f"{cfg.num_seqs} C2 sequences ({int(ctx.sum())} KV tokens, fp16 KV, fp32 math): "
+                      f"{reps} calls in {dt:.1f} s on {threads} threads, {reps1} calls in {dt1:.1f} s on 1 thread"}
 
 
 def main():
@@ -166,6 +204,7 @@ def main():
     log(f"[bench] decode {ms_decode * 1e3:.1f} us, append {ms_append * 1e3:.1f} us")
 
     kv_bytes = cfg.kv_bytes(2)
+    traffic, traffic_note = measured_traffic()
     value = kv_bytes / (ms_step * 1e-3) / 1e9
     achieved = kv_bytes / (ms_decode * 1e-3) / 1e9
     append_bytes = S * Hkv * D * 2 * 2 * 2 + S * 4
@@ -193,7 +232,9 @@ def main():
         "append_gbs": round(append_bytes / (ms_append * 1e-3) / 1e9, 2),
         "kv_bytes_per_call": kv_bytes,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_over_algorithmic": None if traffic is None else round(traffic / kv_bytes, 4),
+                     "traffic_source": traffic_note,
                      "kernel": "paged decode (partition + merge kernels), event-timed on the launch stream",
                      "achieved_note": "algorithmic KV bytes per call / decode call time"},
     }
@@ -706,6 +747,7 @@ def suite_c4(dev, steps, warmup):
     b = torch.from_numpy(free).long().to(dev)
     swap_exact = all(torch.equal(pl[l][b], pl[l][a]) for pl in planes for l in range(L))
     swap_bytes = nsw * hb
+    beside = _decode_beside_swap(dev, planes, host, nsw, out_pairs, swap_bytes)
     from oracle import oracle
     Ls, Ps = 4, 256
     sub_ids = np.unique(np.concatenate([cfg.copy_pairs[:Ps, 0], cfg.copy_pairs[:Ps, 1]]))
@@ -724,8 +766,57 @@ def suite_c4(dev, steps, warmup):
             "swap_out_gbs": round(swap_bytes / (t_out[0] * 1e-3) / 1e9, 1),
             "swap_in_gbs": round(swap_bytes / (t_in[0] * 1e-3) / 1e9, 1),
             "swap_round_trip_bit_exact": bool(swap_exact),
+            "decode_beside_swap": beside,
             "cpu_baseline": {"copy_gbs": round(cpu_copy_bytes / sec / 1e9, 3), "cores": 1, "kind": "port",
                              "sample": f"oracle copy_blocks of {Ps} pairs x {Ls} layers x K,V, {reps} calls"}}
+
+
+def _decode_beside_swap(dev, planes, host, nsw, out_pairs, swap_bytes, reps=40):
+    """C2's decode on the default stream alone, then while a swap-out of the C4
+    blocks runs on a side stream: decode us per call both ways, and the swap's
+    rate while the decodes run (HIP events on each stream)."""
+    import numpy as np
+    import torch
+    import vllm_kv_amd as vkv
+    from vllm_kv_amd import workloads
+    cfg = workloads.config2()
+    lay = cfg.layout
+    g = torch.Generator(device=dev).manual_seed(cfg.seed)
+    shape = (lay.num_blocks, cfg.block_size, cfg.num_kv_heads, cfg.head_dim)
+    kc = _rand_half(shape, g, dev, cfg.sigma)
+    vc = _rand_half(shape, g, dev, cfg.sigma)
+    q = _rand_half((cfg.num_seqs, cfg.num_heads, cfg.head_dim), g, dev, cfg.sigma)
+    out = torch.empty_like(q)
+    bt = torch.from_numpy(lay.block_tables).to(dev)
+    cl = torch.from_numpy(lay.context_lens).to(dev)
+    main = torch.cuda.current_stream()
+    side = torch.cuda.Stream()
+
+    def decode():
+        vkv.paged_decode(out, q, kc, vc, bt, cl, cfg.scale, stream=main)
+
+    for _ in range(5):
+        decode()
+    torch.cuda.synchronize()
+    solo = _events_ms(decode, reps, main)[0]
+    s0 = torch.cuda.Event(enable_timing=True)
+    s1 = torch.cuda.Event(enable_timing=True)
+    d0 = torch.cuda.Event(enable_timing=True)
+    d1 = torch.cuda.Event(enable_timing=True)
+    s0.record(side)
+    vkv.swap_blocks(planes, host, nsw, out_pairs, 0, stream=side)
+    s1.record(side)
+    d0.record(main)
+    for _ in range(reps):
+        decode()
+    d1.record(main)
+    torch.cuda.synchronize()
+    busy = d0.elapsed_time(d1) / reps
+    swap_ms = s0.elapsed_time(s1)
+    return {"decode_us_alone": round(solo * 1e3, 2), "decode_us_beside_swap": round(busy * 1e3, 2),
+            "decodes_inside_swap": bool(d1.elapsed_time(s1) > 0),
+            "swap_out_gbs_beside_decode": round(swap_bytes / (swap_ms * 1e-3) / 1e9, 1),
+            "workload": f"C2 decode x {reps} on the default stream; swap-out of {nsw} C4 blocks on a side stream"}
 
 
 SUITES = {"stream": suite_stream, "c1": suite_c1, "append": suite_append, "rope": suite_rope, "step": suite_step,

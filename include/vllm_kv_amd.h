@@ -192,12 +192,19 @@ int vkv_rope_cos_sin_host(float theta, int32_t head_dim, int32_t max_position, f
  * bytes of device workspace.  With partition_size 0 the kernels choose the
  * size per call from the device-side context lengths (5/6 to 2 times the
  * default; the workspace size covers the smallest), so results may differ in
- * the last bits from an explicit size.  workspace == NULL uses a buffer the library
- * owns per device (grown with hipMalloc on first use, never shrunk).  A
- * caller workspace must have its first 1024 bytes zeroed before its first use
- * (work counters; every call leaves them zero again, apart from int 1, the
- * partition size the call chose), and calls that may run concurrently need
- * distinct workspaces.  At most 16000 sequences per call.
+ * the last bits from an explicit size.
+ *
+ * Workspace.  A caller workspace must have its first 1024 bytes zeroed before
+ * its first use (work counters; every call leaves them zero again, apart from
+ * int 1, the partition size the call chose), and calls that may run
+ * concurrently need distinct workspaces.  workspace == NULL uses a buffer the
+ * library keeps per (device, stream): calls on different streams never share
+ * it.  It grows with hipMalloc when a call needs more (an outgrown buffer is
+ * kept, not freed, so graphs captured before stay valid); a call that would
+ * grow it while its stream is being captured fails with VKV_ERR_WORKSPACE
+ * instead, so capture after one eager call of the largest size, or pass a
+ * workspace.  Calls over many sequences are split into consecutive ranges of
+ * rows inside the library (same results).
  * ------------------------------------------------------------------------- */
 typedef struct vkv_decode_params {
     void* output;               /* [num_seqs, num_heads, head_dim] io_dtype */
@@ -242,8 +249,12 @@ int vkv_paged_decode(const vkv_decode_params* p, vkv_stream_t stream);
  * (rows past it are not computed).  fp16 queries at head_dim 64/128 over fp16
  * or FP8 caches run sequences with q_len >= 2 on the matrix cores and the
  * q_len 1 ones through split-K decode; other combinations decode every row
- * with its causal context.  Uses the library's per-device workspace (calls
- * that may run concurrently on one device race on it).
+ * with its causal context.  max_context_len > 0 clamps every row's key count
+ * as decode does (the reference's max_context_len, paged_attention.cu:20);
+ * 0 leaves only the table clamp.  Workspace: as for decode, a caller buffer of
+ * vkv_paged_prefill_workspace_size() bytes (first 1024 bytes zeroed before
+ * its first use) or, with workspace == NULL, the library's buffer of the
+ * stream.
  * ------------------------------------------------------------------------- */
 typedef struct vkv_prefill_params {
     void* output;               /* [num_query_tokens, num_heads, head_dim] io_dtype */
@@ -268,8 +279,12 @@ typedef struct vkv_prefill_params {
     float scale;
     int32_t io_dtype;
     int32_t kv_dtype;
+    int32_t max_context_len;    /* > 0: clamp of every row's keys; 0: none */
+    void* workspace;            /* optional, see above */
+    size_t workspace_bytes;
 } vkv_prefill_params;
 
+size_t vkv_paged_prefill_workspace_size(const vkv_prefill_params* p);
 int vkv_paged_prefill(const vkv_prefill_params* p, vkv_stream_t stream);
 
 /* -------------------------------------------------------------------------

@@ -25,7 +25,7 @@ def test_library_exports_every_declared_symbol(vkv):
     lib = vkv.load()
     for name in declared_functions():
         assert hasattr(lib, name), name
-    assert lib.vkv_abi_version() == 1
+    assert lib.vkv_abi_version() == 2
 
 
 def test_struct_sizes_match_header_layout(vkv):
@@ -34,6 +34,9 @@ def test_struct_sizes_match_header_layout(vkv):
     assert ctypes.sizeof(vkv.DecodeParams) == 8 * 8 + 8 + 14 * 4 + 8 + 8
     assert ctypes.sizeof(vkv.BlockPlane) == 24
     assert ctypes.sizeof(vkv.RopeAppendParams) == 3 * 8 + 3 * 8 + 2 * 8 + 2 * 4 + 5 * 8 + 8 * 4
+    # 9 pointers, query_stride, 13 int32/float (padded to 8), workspace pointer and size
+    assert ctypes.sizeof(vkv.PrefillParams) == 9 * 8 + 8 + 13 * 4 + 4 + 8 + 8
+    assert vkv.PrefillParams.workspace.offset == 136
 
 
 def _decode_params(vkv, **over):
@@ -162,3 +165,29 @@ def test_kv_pool_sizing_with_element_type(vkv):
     assert vkv.kv_pool_num_blocks(budget, non_kv, L, bs, Hkv, D, vkv.DTYPE_F16, 2, 100) == 2 * 7
     with pytest.raises(vkv.VkvError):
         vkv.kv_block_bytes(L, bs, Hkv, D, 7)
+
+
+def _prefill_params(vkv, **over):
+    p = vkv.PrefillParams(output=16, query=16, key_cache=16, value_cache=16, block_tables=16, context_lens=16,
+                          query_start_loc=16, num_seqs=3, num_query_tokens=600, max_query_len=512, num_heads=28,
+                          num_kv_heads=4, head_dim=128, block_size=32, max_blocks_per_seq=80, num_blocks=1000,
+                          scale=0.088, io_dtype=1, kv_dtype=1)
+    for k, v in over.items():
+        setattr(p, k, v)
+    return p
+
+
+def test_prefill_argument_errors_and_workspace(vkv):
+    lib = vkv.load()
+    assert lib.vkv_paged_prefill(ctypes.byref(_prefill_params(vkv, query_start_loc=0)), None) == -1
+    assert lib.vkv_paged_prefill(ctypes.byref(_prefill_params(vkv, max_query_len=0)), None) == -2
+    assert lib.vkv_paged_prefill(ctypes.byref(_prefill_params(vkv, max_context_len=-1)), None) == -2
+    assert lib.vkv_paged_prefill(ctypes.byref(_prefill_params(vkv, num_query_tokens=0)), None) == 0
+    need = lib.vkv_paged_prefill_workspace_size(ctypes.byref(_prefill_params(vkv)))
+    # at least the 1 KiB header and the partials of the 3 sequences' decode rows
+    assert need >= 1024 + 3 * 28 * (128 + 2) * 4
+    p = _prefill_params(vkv, workspace=256, workspace_bytes=need - 16)
+    assert lib.vkv_paged_prefill(ctypes.byref(p), None) == -4       # too small
+    p = _prefill_params(vkv, workspace=8, workspace_bytes=need)
+    assert lib.vkv_paged_prefill(ctypes.byref(p), None) == -5       # misaligned
+    assert lib.vkv_paged_prefill_workspace_size(ctypes.byref(_prefill_params(vkv, head_dim=0))) == 0

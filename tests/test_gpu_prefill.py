@@ -25,41 +25,11 @@ def _case(H, Hkv, D, bs, q_lens, prior, seed):
     return lay, ctx, qsl, q, k, v, float(1.0 / np.sqrt(np.float32(D)))
 
 
-# fp16 queries at head_dim 64/128 run sequences with >= 2 query tokens on the
-# matrix-core kernel and single-token ones through split-K decode.
-@pytest.mark.parametrize("H,Hkv,D,bs,q_lens,prior", [
-    (32, 8, 128, 16, [5, 1, 17], [0, 30, 40]),
-    (28, 4, 128, 32, [64, 1, 1, 33], [100, 500, 0, 7]),
-    (14, 2, 64, 16, [40], [0]),
-    (16, 2, 128, 16, [40, 3, 1], [10, 0, 77]),      # group 8: two head groups (grid.z), one claim counter each
-    (8, 8, 64, 8, [70, 2], [9000, 5]),              # MHA; 1131 blocks: block-id window reloads (FP8 kernel)
-    (8, 8, 64, 8, [40, 3], [17000, 9]),             # 2130 blocks: the fp16 kernel's 2048-id window refills
-    (8, 2, 128, 8, [20, 1], [16500, 40]),           # the same at D 128
-    (16, 4, 128, 64, [33, 1, 100], [64, 0, 129]),   # blocks larger than a key tile
-    (12, 4, 128, 16, [2, 31, 32, 65], [0, 1, 15, 300]),
-    # groups 5 and 6: 256-row work items end inside a token's heads
-    (10, 2, 128, 16, [77, 1, 300, 52], [3, 40, 129, 0]),
-    (24, 4, 64, 32, [129, 7, 1, 250], [600, 0, 33, 64]),
-])
-def test_prefill_vs_oracle(vkv, oracle, cuda, H, Hkv, D, bs, q_lens, prior):
+def _quantise(vkv, cuda, k, v):
+    """FP8 cache (codes + per-(slot, head) scales) of fp16 pools [N, bs, Hkv, D],
+    quantised by the GPU append; returns device tensors and their host copies."""
     import torch
-    lay, ctx, qsl, q, k, v, scale = _case(H, Hkv, D, bs, q_lens, prior, sum(q_lens) + H)
-    Tq = q.shape[0]
-    ref = oracle.paged_prefill(q.astype(np.float32), k.view(np.uint16), v.view(np.uint16), lay.block_tables,
-                               ctx, qsl, scale)
-    out = torch.zeros((Tq, H, D), dtype=torch.float16, device=cuda)
-    vkv.paged_prefill(out, to_dev(q, cuda), to_dev(k, cuda), to_dev(v, cuda), to_dev(lay.block_tables, cuda),
-                      to_dev(ctx, cuda), to_dev(qsl, cuda), int(max(q_lens)), scale)
-    torch.cuda.synchronize()
-    assert_close(to_np(out).astype(np.float32), ref, F16_ATOL, F16_RTOL, "prefill")
-
-
-@pytest.mark.parametrize("H,Hkv,D,bs", [(28, 4, 128, 32), (16, 2, 64, 16)])  # groups 7 and 8
-def test_prefill_fp8_vs_oracle(vkv, oracle, cuda, H, Hkv, D, bs):
-    """FP8 cache (quantised by the GPU append): against the oracle on the same codes and scales."""
-    import torch
-    lay, ctx, qsl, q, k, v, scale = _case(H, Hkv, D, bs, [48, 1, 130], [20, 300, 64], 9)
-    N = lay.num_blocks
+    N, bs, Hkv, D = k.shape
     kc = torch.zeros((N, bs, Hkv, D), dtype=torch.uint8, device=cuda)
     vc = torch.zeros_like(kc)
     ks = torch.zeros((N, bs, Hkv), dtype=torch.float32, device=cuda)
@@ -67,12 +37,67 @@ def test_prefill_fp8_vs_oracle(vkv, oracle, cuda, H, Hkv, D, bs):
     slots = to_dev(np.arange(N * bs, dtype=np.int32), cuda)
     vkv.reshape_and_cache(to_dev(k.reshape(-1, Hkv, D), cuda), to_dev(v.reshape(-1, Hkv, D), cuda), kc, vc, slots,
                           ks, vs)
+    torch.cuda.synchronize()
+    return (kc, vc, ks, vs), (to_np(kc), to_np(vc), to_np(ks), to_np(vs))
+
+
+def _cache(vkv, cuda, kvt, k, v):
+    """(device K, V, K scales, V scales), (host copies for the oracle) of a pool."""
+    if kvt == "f16":
+        return (to_dev(k, cuda), to_dev(v, cuda), None, None), (k.view(np.uint16), v.view(np.uint16), None, None)
+    return _quantise(vkv, cuda, k, v)
+
+
+def _threads():
+    import os
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+# fp16 queries at head_dim 64/128 run sequences with >= 2 query tokens on the
+# matrix-core kernels and single-token ones through split-K decode; each case
+# runs over an fp16 cache and over its FP8 quantisation (against the oracle
+# on the same codes and scales).
+@pytest.mark.parametrize("kvt", ["f16", "fp8"])
+@pytest.mark.parametrize("H,Hkv,D,bs,q_lens,prior", [
+    (32, 8, 128, 16, [5, 1, 17], [0, 30, 40]),
+    (28, 4, 128, 32, [64, 1, 1, 33], [100, 500, 0, 7]),
+    (14, 2, 64, 16, [40], [0]),
+    (16, 2, 128, 16, [40, 3, 1], [10, 0, 77]),      # group 8
+    (8, 8, 64, 8, [70, 2], [9000, 5]),              # MHA; 1131 blocks: FP8 D 64 kernel's 1024-id window reloads
+    (8, 8, 64, 8, [40, 3], [17000, 9]),             # 2130 blocks: the wide kernels' 2048-id window refills
+    (8, 2, 128, 8, [20, 1], [16500, 40]),           # the same at D 128
+    (16, 4, 128, 64, [33, 1, 100], [64, 0, 129]),   # blocks larger than a key tile
+    (12, 4, 128, 16, [2, 31, 32, 65], [0, 1, 15, 300]),
+    # groups 5 and 6: 256-row work items end inside a token's heads
+    (10, 2, 128, 16, [77, 1, 300, 52], [3, 40, 129, 0]),
+    (24, 4, 64, 32, [129, 7, 1, 250], [600, 0, 33, 64]),
+])
+def test_prefill_vs_oracle(vkv, oracle, cuda, kvt, H, Hkv, D, bs, q_lens, prior):
+    import torch
+    lay, ctx, qsl, q, k, v, scale = _case(H, Hkv, D, bs, q_lens, prior, sum(q_lens) + H)
+    Tq = q.shape[0]
+    (kc, vc, ks, vs), (hk, hv, hks, hvs) = _cache(vkv, cuda, kvt, k, v)
+    ref = oracle.paged_prefill(q.astype(np.float32), hk, hv, lay.block_tables, ctx, qsl, scale,
+                               key_scales=hks, value_scales=hvs, nthreads=_threads())
+    out = torch.zeros((Tq, H, D), dtype=torch.float16, device=cuda)
+    vkv.paged_prefill(out, to_dev(q, cuda), kc, vc, to_dev(lay.block_tables, cuda), to_dev(ctx, cuda),
+                      to_dev(qsl, cuda), int(max(q_lens)), scale, key_scales=ks, value_scales=vs)
+    torch.cuda.synchronize()
+    assert_close(to_np(out).astype(np.float32), ref, F16_ATOL, F16_RTOL, f"prefill ({kvt} cache)")
+
+
+@pytest.mark.parametrize("H,Hkv,D,bs", [(28, 4, 128, 32), (16, 2, 64, 16)])  # groups 7 and 8
+def test_prefill_fp8_vs_oracle(vkv, oracle, cuda, H, Hkv, D, bs):
+    """FP8 cache (quantised by the GPU append): against the oracle on the same codes and scales."""
+    import torch
+    lay, ctx, qsl, q, k, v, scale = _case(H, Hkv, D, bs, [48, 1, 130], [20, 300, 64], 9)
+    (kc, vc, ks, vs), (hk, hv, hks, hvs) = _quantise(vkv, cuda, k, v)
     out = torch.zeros((q.shape[0], H, D), dtype=torch.float16, device=cuda)
     vkv.paged_prefill(out, to_dev(q, cuda), kc, vc, to_dev(lay.block_tables, cuda), to_dev(ctx, cuda),
                       to_dev(qsl, cuda), 130, scale, key_scales=ks, value_scales=vs)
     torch.cuda.synchronize()
-    ref = oracle.paged_prefill(q.astype(np.float32), to_np(kc), to_np(vc), lay.block_tables, ctx, qsl, scale,
-                               key_scales=to_np(ks), value_scales=to_np(vs))
+    ref = oracle.paged_prefill(q.astype(np.float32), hk, hv, lay.block_tables, ctx, qsl, scale,
+                               key_scales=hks, value_scales=hvs)
     assert_close(to_np(out).astype(np.float32), ref, F16_ATOL, F16_RTOL, "fp8 prefill")
 
 
@@ -94,12 +119,15 @@ def test_prefill_many_items(vkv, oracle, cuda):
     assert_close(to_np(out).astype(np.float32), ref, F16_ATOL, F16_RTOL, "prefill")
 
 
-def test_prefill_mixed_config3_sampled(vkv, oracle, cuda):
+@pytest.mark.parametrize("kvt", ["f16", "fp8"])
+def test_prefill_mixed_config3(vkv, oracle, cuda, kvt):
     """C3's mixed call at its full size: 8 chunks of 512 query tokens (prior
-    U[0, 2048]) on the matrix-core kernel and 120 single-token sequences
+    U[0, 2048]) on the matrix-core kernels and 120 single-token sequences
     (contexts U[1024, 8192]) through split-K decode with the partition size
-    picked on the device.  Sampled query rows of both kinds against the oracle
-    (row j of a chunk is decode over prior + j + 1 keys)."""
+    picked on the device, over an fp16 cache and over its FP8 quantisation.
+    Every row of the chunks with the longest and the shortest prior context,
+    and every decode row, against the oracle (row j of a chunk is decode over
+    prior + j + 1 keys)."""
     import torch
     from vllm_kv_amd import workloads
     cfg = workloads.config3()
@@ -109,34 +137,45 @@ def test_prefill_mixed_config3_sampled(vkv, oracle, cuda):
     Tq = int(qsl[-1])
     g = torch.Generator(device=cuda).manual_seed(23)
     shape = (lay.num_blocks, bs, Hkv, D)
-    kc = (torch.randn(shape, generator=g, device=cuda) * 0.5).half()
-    vc = (torch.randn(shape, generator=g, device=cuda) * 0.5).half()
+    k16 = (torch.randn(shape, generator=g, device=cuda) * 0.5).half()
+    v16 = (torch.randn(shape, generator=g, device=cuda) * 0.5).half()
     q = (torch.randn((Tq, H, D), generator=g, device=cuda) * 0.5).half()
+    if kvt == "f16":
+        kc, vc, ks, vs = k16, v16, None, None
+        hk, hv, hks, hvs = to_np(kc).view(np.uint16), to_np(vc).view(np.uint16), None, None
+    else:
+        kc = torch.empty(shape, dtype=torch.uint8, device=cuda)
+        vc = torch.empty_like(kc)
+        ks = torch.empty(shape[:3], dtype=torch.float32, device=cuda)
+        vs = torch.empty_like(ks)
+        slots = torch.arange(lay.num_blocks * bs, dtype=torch.int32, device=cuda)
+        vkv.reshape_and_cache(k16.view(-1, Hkv, D), v16.view(-1, Hkv, D), kc, vc, slots, ks, vs)
+        hk, hv, hks, hvs = to_np(kc), to_np(vc), to_np(ks), to_np(vs)
+    del k16, v16
     out = torch.zeros((Tq, H, D), dtype=torch.float16, device=cuda)
     vkv.paged_prefill(out, q, kc, vc, to_dev(lay.block_tables, cuda), to_dev(lay.context_lens, cuda),
-                      to_dev(qsl, cuda), int(cfg.q_lens.max()), cfg.scale)
+                      to_dev(qsl, cuda), int(cfg.q_lens.max()), cfg.scale, key_scales=ks, value_scales=vs)
     torch.cuda.synchronize()
     got = to_np(out).astype(np.float32)
     qn = to_np(q).astype(np.float32)
     npf = int((cfg.q_lens > 1).sum())
-    rows = [(0, 0), (0, 511), (3, 200), (7, 511), (npf, 0), (npf + 60, 0), (len(cfg.q_lens) - 1, 0)]
-    for s, j in rows:
-        n = int(cfg.prior_lens[s]) + j + 1
-        nblk = (n + bs - 1) // bs
-        ids = torch.from_numpy(lay.block_tables[s, :nblk]).long().to(cuda)
-        kk = to_np(kc[ids]).view(np.uint16)
-        vv = to_np(vc[ids]).view(np.uint16)
-        r = int(qsl[s]) + j
-        ref = oracle.paged_decode(qn[r:r + 1], kk, vv, np.arange(nblk, dtype=np.int32)[None, :],
-                                  np.array([n], np.int32), cfg.scale)
-        assert_close(got[r:r + 1], ref, F16_ATOL, F16_RTOL, f"sequence {s} row {j}")
+    prior = cfg.prior_lens[:npf]
+    seqs = sorted({int(np.argmax(prior)), int(np.argmin(prior))}) + list(range(npf, len(cfg.q_lens)))
+    rows = np.concatenate([np.arange(qsl[s], qsl[s + 1]) for s in seqs])
+    sub_qsl = np.concatenate([[0], np.cumsum([qsl[s + 1] - qsl[s] for s in seqs])]).astype(np.int32)
+    ref = oracle.paged_prefill(qn[rows], hk, hv, np.ascontiguousarray(lay.block_tables[seqs]),
+                               np.ascontiguousarray(lay.context_lens[seqs]), sub_qsl, cfg.scale,
+                               key_scales=hks, value_scales=hvs, nthreads=_threads())
+    assert_close(got[rows], ref, F16_ATOL, F16_RTOL, f"C3 ({kvt} cache): 2 chunks and 120 decode rows")
 
 
-def test_prefill_large_call_list_kernel(vkv, oracle, cuda):
+@pytest.mark.parametrize("kvt", ["f16", "fp8"])
+def test_prefill_large_call_list_kernel(vkv, oracle, cuda, kvt):
     """A call with more row blocks than the fp16 kernel orders in LDS (here 720
     blocks of 256 (token, head) rows, 80 sequences of 300 tokens at group 7):
-    the separate list kernel builds the longest-first order.  Sampled rows
-    against the oracle (row j of a sequence is decode over prior + j + 1 keys)."""
+    the separate list kernel builds the longest-first order (the FP8 kernel
+    always uses it).  Sampled rows against the oracle (row j of a sequence is
+    decode over prior + j + 1 keys), on the same codes and scales for FP8."""
     import torch
     from vllm_kv_amd import workloads
     rng = np.random.default_rng(17)
@@ -147,26 +186,22 @@ def test_prefill_large_call_list_kernel(vkv, oracle, cuda):
     lay = workloads.make_layout(ctx, bs, rng, slack=0.1)
     qsl = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
     Tq = int(qsl[-1])
-    g = torch.Generator(device=cuda).manual_seed(17)
-    shape = (lay.num_blocks, bs, Hkv, D)
-    kc = (torch.randn(shape, generator=g, device=cuda) * 0.5).half()
-    vc = (torch.randn(shape, generator=g, device=cuda) * 0.5).half()
-    q = (torch.randn((Tq, H, D), generator=g, device=cuda) * 0.5).half()
+    k, v = workloads.fill_pool_numpy(rng, lay.num_blocks, bs, Hkv, D, 0.5)
+    (kc, vc, ks, vs), (hk, hv, hks, hvs) = _cache(vkv, cuda, kvt, k, v)
+    q = (rng.standard_normal((Tq, H, D), dtype=np.float32) * 0.5).astype(np.float16)
     out = torch.zeros((Tq, H, D), dtype=torch.float16, device=cuda)
-    vkv.paged_prefill(out, q, kc, vc, to_dev(lay.block_tables, cuda), to_dev(ctx, cuda), to_dev(qsl, cuda),
-                      qn_, float(1.0 / np.sqrt(np.float32(D))))
+    scale = float(1.0 / np.sqrt(np.float32(D)))
+    vkv.paged_prefill(out, to_dev(q, cuda), kc, vc, to_dev(lay.block_tables, cuda), to_dev(ctx, cuda),
+                      to_dev(qsl, cuda), qn_, scale, key_scales=ks, value_scales=vs)
     torch.cuda.synchronize()
     got = to_np(out).astype(np.float32)
-    qh = to_np(q).astype(np.float32)
-    for s, j in [(0, 0), (0, 299), (31, 150), (79, 299), (int(np.argmax(prior)), 299)]:
-        n = int(prior[s]) + j + 1
-        nblk = (n + bs - 1) // bs
-        ids = torch.from_numpy(lay.block_tables[s, :nblk]).long().to(cuda)
-        r = int(qsl[s]) + j
-        ref = oracle.paged_decode(qh[r:r + 1], to_np(kc[ids]).view(np.uint16), to_np(vc[ids]).view(np.uint16),
-                                  np.arange(nblk, dtype=np.int32)[None, :], np.array([n], np.int32),
-                                  float(1.0 / np.sqrt(np.float32(D))))
-        assert_close(got[r:r + 1], ref, F16_ATOL, F16_RTOL, f"sequence {s} row {j}")
+    seqs = [0, 31, 79, int(np.argmax(prior))]
+    rows = np.concatenate([np.arange(qsl[s], qsl[s + 1]) for s in seqs])
+    sub_qsl = np.concatenate([[0], np.cumsum([qsl[s + 1] - qsl[s] for s in seqs])]).astype(np.int32)
+    ref = oracle.paged_prefill(q[rows].astype(np.float32), hk, hv, np.ascontiguousarray(lay.block_tables[seqs]),
+                               np.ascontiguousarray(ctx[seqs]), sub_qsl, scale, key_scales=hks, value_scales=hvs,
+                               nthreads=_threads())
+    assert_close(got[rows], ref, F16_ATOL, F16_RTOL, f"720-block call ({kvt} cache), every row of 4 sequences")
 
 
 def _mixed_inputs(cuda):
@@ -322,3 +357,56 @@ def test_prefill_growing_logits(vkv, oracle, cuda, kvt):
         # contract (3e-2 relative) per output row instead of element-wise.
         err = np.linalg.norm(got - ref, axis=-1) / np.maximum(np.linalg.norm(ref, axis=-1), 1e-6)
         assert err.max() <= 3e-2, f"FP8 prefill with growing logits: row error {err.max():.3e}"
+
+
+def test_prefill_caller_workspace(vkv, cuda):
+    """A caller workspace of vkv_paged_prefill_workspace_size() bytes (header
+    zeroed) gives the library workspace's result bit for bit, twice in a row."""
+    import torch
+    out, args, mql, scale = _mixed_inputs(cuda)
+    vkv.paged_prefill(out, *args, mql, scale)
+    need = vkv.prefill_workspace_size(out, *args, mql, scale)
+    assert need > 1024
+    ws = torch.zeros(need // 4 + 4, dtype=torch.int32, device=cuda)
+    for _ in range(2):
+        out2 = torch.full_like(out, float("nan"))
+        vkv.paged_prefill(out2, *args, mql, scale, workspace=ws)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), out2.view(torch.int16))
+    small = torch.zeros(64, dtype=torch.int32, device=cuda)
+    with pytest.raises(vkv.VkvError) as e:
+        vkv.paged_prefill(out, *args, mql, scale, workspace=small)
+    assert e.value.code == -4
+
+
+@pytest.mark.parametrize("io", ["f16", "f32"])
+def test_prefill_max_context_len_clamp(vkv, oracle, cuda, io):
+    """max_context_len clamps every row's key count as decode does (the
+    reference's min(ctx, max_context_len), paged_attention.cu:20): row j of a
+    sequence attends keys 0 .. min(prior + j + 1, max_context_len) - 1, on the
+    matrix-core path (fp16) and the per-row decode path (fp32), with the
+    single-token rows of the call clamped the same way."""
+    import torch
+    from helpers import F32_ATOL, F32_RTOL
+    H, Hkv, D, bs = 28, 4, 128, 16
+    q_lens, prior = [100, 1, 60, 1], [150, 300, 20, 40]
+    lay, ctx, qsl, q, k, v, scale = _case(H, Hkv, D, bs, q_lens, prior, 77)
+    max_ctx = 180
+    # per-row reference: each query row is a decode over its clamped causal context
+    seq_of = np.repeat(np.arange(len(q_lens)), q_lens)
+    j = np.arange(q.shape[0]) - qsl[seq_of]
+    row_ctx = np.asarray(prior)[seq_of] + j + 1
+    qf = q.astype(np.float32)
+    ref = oracle.paged_decode(qf, k.view(np.uint16), v.view(np.uint16),
+                              np.ascontiguousarray(lay.block_tables[seq_of]), row_ctx.astype(np.int32), scale,
+                              max_context_len=max_ctx)
+    if io == "f16":
+        qd, out = to_dev(q, cuda), torch.zeros((q.shape[0], H, D), dtype=torch.float16, device=cuda)
+        tol = (F16_ATOL, F16_RTOL)
+    else:
+        qd, out = to_dev(qf, cuda), torch.zeros((q.shape[0], H, D), dtype=torch.float32, device=cuda)
+        tol = (F32_ATOL, 1e-3)
+    vkv.paged_prefill(out, qd, to_dev(k, cuda), to_dev(v, cuda), to_dev(lay.block_tables, cuda), to_dev(ctx, cuda),
+                      to_dev(qsl, cuda), max(q_lens), scale, max_context_len=max_ctx)
+    torch.cuda.synchronize()
+    assert_close(to_np(out).astype(np.float32), ref, *tol, f"prefill clamped to {max_ctx} keys ({io})")

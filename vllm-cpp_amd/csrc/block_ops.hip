@@ -9,9 +9,12 @@
 // (pair, plane, layer) block; 256 lanes each move 4 x 16 bytes with
 // non-temporal loads/stores (the data is not reused, so it should not
 // displace anything in L2/MALL).  A grid-stride loop over units keeps the grid
-// at a few workgroups per CU regardless of the pair count.  Swap reads or
-// writes host memory that hipHostMalloc mapped into the device address space,
-// so the same loop drives the PCIe/host link directly from the CUs.
+// at a fixed size regardless of the pair count: copy fills the chip, swap
+// takes a few workgroups.  Swap reads or writes host memory that hipHostMalloc
+// mapped into the device address space, so the same loop drives the PCIe/host
+// link directly from the CUs.
+#include <cstdlib>
+
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -139,12 +142,29 @@ BlockCopyArgs make_args(const PlaneSet& planes, int32_t num_layers, const int32_
     return a;
 }
 
-int grid_for_units(int64_t units) {
-    int64_t g = units;
-    const int64_t cap = int64_t(256) * 16;  // 16 workgroups per CU on a 256-CU part
-    if (g > cap) g = cap;
-    if (g < 1) g = 1;
-    return int(g);
+int grid_for_units(int64_t units, int64_t cap) {
+    int64_t g = units < cap ? units : cap;
+    return int(g < 1 ? 1 : g);
+}
+
+// Copy: HBM-bound, so the grid fills the chip (16 workgroups per CU on a
+// 256-CU part).
+constexpr int64_t kCopyWorkgroups = int64_t(256) * 16;
+
+// Swap: bound by the host link (~55 GB/s), which a few workgroups with 16 KiB
+// in flight each keep busy; the rest of the chip stays free for the decode
+// that a side-stream swap runs beside.  VKV_SWAP_WORKGROUPS overrides it
+// (tuning).
+#ifndef VKV_SWAP_WORKGROUPS_DEFAULT
+#define VKV_SWAP_WORKGROUPS_DEFAULT 64
+#endif
+int64_t swap_workgroups() {
+    static const int64_t v = [] {
+        const char* e = std::getenv("VKV_SWAP_WORKGROUPS");
+        const long n = e ? std::atol(e) : 0;
+        return n > 0 ? int64_t(n) : int64_t(VKV_SWAP_WORKGROUPS_DEFAULT);
+    }();
+    return v;
 }
 
 }  // namespace
@@ -154,7 +174,8 @@ int launch_copy_blocks(const PlaneSet& planes, int32_t num_layers, int32_t num_b
     BlockCopyArgs a = make_args(planes, num_layers, pairs, num_pairs);
     a.num_dev_blocks = num_blocks;
     if (a.total_units == 0) return 0;
-    hipLaunchKernelGGL(copy_blocks_kernel, dim3(grid_for_units(a.total_units)), dim3(kThreads), 0, st, a);
+    hipLaunchKernelGGL(copy_blocks_kernel, dim3(grid_for_units(a.total_units, kCopyWorkgroups)), dim3(kThreads), 0,
+                       st, a);
     return 0;
 }
 
@@ -168,7 +189,8 @@ int launch_swap_blocks(const PlaneSet& planes, int32_t num_layers, int32_t num_d
     a.num_host_blocks = num_host_blocks;
     a.direction = direction;
     if (a.total_units == 0) return 0;
-    hipLaunchKernelGGL(swap_blocks_kernel, dim3(grid_for_units(a.total_units)), dim3(kThreads), 0, st, a);
+    hipLaunchKernelGGL(swap_blocks_kernel, dim3(grid_for_units(a.total_units, swap_workgroups())), dim3(kThreads), 0,
+                       st, a);
     return 0;
 }
 

@@ -2,7 +2,7 @@
 //
 // Every entry point validates its arguments on the host (so that no kernel is
 // launched with a shape it does not support), then calls the launcher.  No
-// entry point synchronises the device.  The only allocation is the per-device
+// entry point synchronises the device.  The only allocation is the per-stream
 // split-K workspace used when the caller passes none.
 #include <hip/hip_runtime.h>
 
@@ -42,42 +42,69 @@ int after_launch(int rc, const char* what) {
 
 bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
 
-// The decode kernel keeps one prefix entry per sequence (row) in LDS.
-constexpr int kMaxRows = 16000;
-
-// Per-device workspace owned by the library (grow-only).
-struct DeviceWorkspace {
-    void* ptr = nullptr;
-    size_t bytes = 0;
+// Library-owned workspaces, one per (device, stream): calls on different
+// streams never share one, calls on one stream are ordered by it.  A buffer
+// only grows.  An outgrown buffer is retired, not freed: queued work or a
+// captured graph may still use it, and freeing would need a device-wide
+// synchronisation.  Growth doubles, so the retired buffers of a stream never
+// exceed its current one.  A stream that is being captured cannot grow its
+// buffer (that would allocate inside the capture): the call fails instead.
+struct StreamWorkspace {
+    int device;
+    hipStream_t stream;
+    void* ptr;
+    size_t bytes;
 };
 std::mutex g_ws_mutex;
-std::vector<DeviceWorkspace> g_ws;
+std::vector<StreamWorkspace> g_ws;
+std::vector<void*> g_ws_retired;
 
-int library_workspace(size_t need, void** out) {
+int library_workspace(size_t need, hipStream_t stream, void** out) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return hip_status(e, "hipGetDevice");
     std::lock_guard<std::mutex> lock(g_ws_mutex);
-    if (size_t(dev) >= g_ws.size()) g_ws.resize(size_t(dev) + 1);
-    DeviceWorkspace& w = g_ws[size_t(dev)];
-    if (w.bytes < need) {
-        if (w.ptr) {
-            // The old buffer may still be in use by queued work on any stream.
-            e = hipDeviceSynchronize();
-            if (e != hipSuccess) return hip_status(e, "hipDeviceSynchronize (workspace grow)");
-            (void)hipFree(w.ptr);
-            w.ptr = nullptr;
-            w.bytes = 0;
-        }
-        size_t sz = need < (size_t(1) << 20) ? (size_t(1) << 20) : need;
-        e = hipMalloc(&w.ptr, sz);
-        if (e != hipSuccess) return hip_status(e, "hipMalloc (decode workspace)");
-        // The first 1 KiB holds the decode claim counters, which must start at zero.
-        e = hipMemset(w.ptr, 0, 1024);
-        if (e != hipSuccess) return hip_status(e, "hipMemset (decode workspace header)");
-        w.bytes = sz;
+    StreamWorkspace* w = nullptr;
+    for (StreamWorkspace& x : g_ws)
+        if (x.device == dev && x.stream == stream) w = &x;
+    if (!w) {
+        g_ws.push_back(StreamWorkspace{dev, stream, nullptr, 0});
+        w = &g_ws.back();
     }
-    *out = w.ptr;
+    if (w->bytes < need) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        e = hipStreamIsCapturing(stream, &cs);
+        if (e != hipSuccess) return hip_status(e, "hipStreamIsCapturing");
+        if (cs != hipStreamCaptureStatusNone)
+            return fail(VKV_ERR_WORKSPACE,
+                        "the library workspace of this stream must grow to %zu bytes, which cannot happen while "
+                        "the stream is captured: make one eager call of this size first, or pass a workspace",
+                        need);
+        size_t sz = w->bytes * 2;
+        if (sz < need) sz = need;
+        if (sz < (size_t(1) << 20)) sz = size_t(1) << 20;
+        void* p = nullptr;
+        e = hipMalloc(&p, sz);
+        if (e != hipSuccess) return hip_status(e, "hipMalloc (library workspace)");
+        // The first 1 KiB holds the claim counters, which must start at zero;
+        // the clear is ordered before the call's kernels on the same stream.
+        e = hipMemsetAsync(p, 0, 1024, stream);
+        if (e != hipSuccess) {
+            (void)hipFree(p);
+            return hip_status(e, "hipMemsetAsync (workspace header)");
+        }
+        if (w->ptr) g_ws_retired.push_back(w->ptr);
+        w->ptr = p;
+        w->bytes = sz;
+    }
+    *out = w->ptr;
+    return VKV_OK;
+}
+
+// A caller workspace: large enough, 16-byte aligned.
+int check_workspace(void* ws, size_t have, size_t need) {
+    if (have < need) return fail(VKV_ERR_WORKSPACE, "workspace %zu bytes < %zu needed", have, need);
+    if (reinterpret_cast<uintptr_t>(ws) & 15u) return fail(VKV_ERR_ALIGN, "workspace must be 16-byte aligned");
     return VKV_OK;
 }
 
@@ -117,9 +144,20 @@ int check_decode(const vkv_decode_params* p) {
         (reinterpret_cast<uintptr_t>(p->output) & uintptr_t(io_eb - 1)))
         return fail(VKV_ERR_ALIGN, "query/output misaligned for their dtype");
     if (p->partition_size < 0) return fail(VKV_ERR_SHAPE, "partition_size < 0");
-    if (p->num_seqs > kMaxRows)
-        return fail(VKV_ERR_UNSUPPORTED, "more than %d sequences (rows) per call", kMaxRows);
     return VKV_OK;
+}
+
+int check_prefill(const vkv_prefill_params* p) {
+    if (!p) return fail(VKV_ERR_NULL, "vkv_paged_prefill: params is NULL");
+    if (p->num_seqs < 0 || p->num_query_tokens < 0) return fail(VKV_ERR_SHAPE, "negative size");
+    if (p->num_seqs == 0 || p->num_query_tokens == 0) return VKV_OK;
+    if (!p->query_start_loc) return fail(VKV_ERR_NULL, "query_start_loc is NULL");
+    if (p->max_query_len < 1) return fail(VKV_ERR_SHAPE, "max_query_len must be >= 1");
+    if (p->max_context_len < 0) return fail(VKV_ERR_SHAPE, "max_context_len < 0");
+    // Shape/dtype rules are those of decode; the decode rows are the
+    // sequences (mixed matrix-core path) or the query tokens (row path).
+    const vkv_decode_params d = vkv::prefill_as_decode(p, vkv::prefill_mfma_supported(p));
+    return check_decode(&d);
 }
 
 int check_append(const vkv_append_params* p) {
@@ -226,11 +264,27 @@ int fill_planes(const vkv_block_plane* planes, int32_t num_planes, vkv::PlaneSet
 
 }  // namespace
 
+namespace vkv {
+
+int check_decode_args(const vkv_decode_params* p) { return check_decode(p); }
+
+int report_error(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int report_launch(int rc, const char* what) { return after_launch(rc, what); }
+
+}  // namespace vkv
+
 extern "C" {
 
 const char* vkv_last_error(void) { return g_last_error; }
 
-int vkv_abi_version(void) { return 1; }
+int vkv_abi_version(void) { return 2; }
 
 int vkv_reshape_and_cache(const vkv_append_params* p, vkv_stream_t stream) {
     int rc = check_append(p);
@@ -312,38 +366,30 @@ size_t vkv_paged_decode_workspace_size(const vkv_decode_params* p) {
 int vkv_paged_decode(const vkv_decode_params* p, vkv_stream_t stream) {
     int rc = check_decode(p);
     if (rc != VKV_OK || p->num_seqs == 0) return rc;
+    const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const vkv::DecodePlan plan = vkv::plan_decode(p);
     void* ws = p->workspace;
-    if (ws) {
-        if (p->workspace_bytes < plan.workspace_bytes)
-            return fail(VKV_ERR_WORKSPACE, "workspace %zu bytes < %zu needed", p->workspace_bytes,
-                        plan.workspace_bytes);
-        if (reinterpret_cast<uintptr_t>(ws) & 15u) return fail(VKV_ERR_ALIGN, "workspace must be 16-byte aligned");
-    } else {
-        rc = library_workspace(plan.workspace_bytes, &ws);
-        if (rc != VKV_OK) return rc;
-    }
-    return after_launch(vkv::launch_decode(p, plan, ws, reinterpret_cast<hipStream_t>(stream)), "vkv_paged_decode");
+    rc = ws ? check_workspace(ws, p->workspace_bytes, plan.workspace_bytes)
+            : library_workspace(plan.workspace_bytes, st, &ws);
+    if (rc != VKV_OK) return rc;
+    return after_launch(vkv::launch_decode(p, plan, ws, st), "vkv_paged_decode");
+}
+
+size_t vkv_paged_prefill_workspace_size(const vkv_prefill_params* p) {
+    if (check_prefill(p) != VKV_OK || p->num_seqs == 0 || p->num_query_tokens == 0) return 0;
+    return vkv::plan_prefill(p).workspace_bytes;
 }
 
 int vkv_paged_prefill(const vkv_prefill_params* p, vkv_stream_t stream) {
-    if (!p) return fail(VKV_ERR_NULL, "vkv_paged_prefill: params is NULL");
-    if (p->num_seqs < 0 || p->num_query_tokens < 0) return fail(VKV_ERR_SHAPE, "negative size");
-    if (p->num_seqs == 0 || p->num_query_tokens == 0) return VKV_OK;
-    if (!p->query_start_loc) return fail(VKV_ERR_NULL, "query_start_loc is NULL");
-    if (p->max_query_len < 1) return fail(VKV_ERR_SHAPE, "max_query_len must be >= 1");
-    // Shape/dtype rules are those of decode; the decode rows are the
-    // sequences (mixed matrix-core path) or the query tokens (row path).
-    const bool mfma = vkv::prefill_mfma_supported(p);
-    const vkv_decode_params d = vkv::prefill_as_decode(p, mfma);
-    int rc = check_decode(&d);
-    if (rc != VKV_OK) return rc;
+    int rc = check_prefill(p);
+    if (rc != VKV_OK || p->num_seqs == 0 || p->num_query_tokens == 0) return rc;
+    const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const vkv::DecodePlan plan = vkv::plan_prefill(p);
-    void* ws = nullptr;
-    rc = library_workspace(plan.workspace_bytes, &ws);
+    void* ws = p->workspace;
+    rc = ws ? check_workspace(ws, p->workspace_bytes, plan.workspace_bytes)
+            : library_workspace(plan.workspace_bytes, st, &ws);
     if (rc != VKV_OK) return rc;
-    return after_launch(vkv::launch_prefill(p, plan, ws, reinterpret_cast<hipStream_t>(stream)),
-                        "vkv_paged_prefill");
+    return after_launch(vkv::launch_prefill(p, plan, ws, st), "vkv_paged_prefill");
 }
 
 int vkv_check_block_pairs_host(const int32_t* block_pairs, int32_t num_pairs, int32_t num_blocks) {

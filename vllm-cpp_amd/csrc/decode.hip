@@ -83,6 +83,11 @@ constexpr int kAdaptMaxRows = 4096;
 constexpr int kItemOverheadTokens = 128;
 // LDS per CU on gfx950, for the resident-wave estimate.
 constexpr int kLdsPerCu = 160 * 1024;
+// Rows (sequences or query rows) per partition launch: the kernel keeps one
+// prefix entry per row in LDS.  Larger calls run as consecutive launches.
+constexpr int kMaxRowsPerLaunch = 8192;
+// Rows of the largest launch of a call (the partials are sized for it).
+inline int launch_rows_max(int num_rows) { return num_rows < kMaxRowsPerLaunch ? num_rows : kMaxRowsPerLaunch; }
 
 struct DecodeArgs {
     void* out;
@@ -1215,8 +1220,8 @@ DecodePlan plan_decode(const vkv_decode_params* p) {
     }
     plan.max_parts = int((max_ctx + smallest - 1) / smallest);
     if (plan.max_parts < 1) plan.max_parts = 1;
-    plan.workspace_bytes = kWorkspaceHeader +
-                           size_t(p->num_seqs) * p->num_heads * plan.max_parts * (p->head_dim + 2) * sizeof(float);
+    plan.workspace_bytes = kWorkspaceHeader + size_t(launch_rows_max(p->num_seqs)) * p->num_heads * plan.max_parts *
+                                                  (p->head_dim + 2) * sizeof(float);
     return plan;
 }
 
@@ -1254,11 +1259,11 @@ int launch_rows(const vkv_decode_params* p, const DecodePlan& plan, void* worksp
     a.row_seq = row_seq;
     a.row_ctx = row_ctx;
     a.qsl = qsl;
-    const size_t o_elems = size_t(p->num_seqs) * p->num_heads * plan.max_parts * p->head_dim;
+    const int rows = launch_rows_max(p->num_seqs);
+    const size_t o_elems = size_t(rows) * p->num_heads * plan.max_parts * p->head_dim;
     a.counters = static_cast<int*>(workspace);
     a.part_o = reinterpret_cast<float*>(static_cast<char*>(workspace) + kWorkspaceHeader);
     a.part_ml = a.part_o + o_elems;
-    a.num_rows = p->num_seqs;
     a.mfma_enabled = mfma_enabled();
     a.q_stride = p->query_stride ? p->query_stride : int64_t(p->num_heads) * p->head_dim;
     a.num_heads = p->num_heads;
@@ -1278,33 +1283,58 @@ int launch_rows(const vkv_decode_params* p, const DecodePlan& plan, void* worksp
     a.accumulate = p->accumulate;
 
     const int G = p->num_heads / p->num_kv_heads;
-    // Persistent grid (sized in launch_g from the kernel's occupancy), never
-    // more workgroups than item groups.
-    const int64_t max_items = int64_t(p->num_seqs) * plan.max_parts * p->num_kv_heads;
-    int64_t item_wgs = (max_items + kWavesPerBlock - 1) / kWavesPerBlock;
-    if (item_wgs > (int64_t(1) << 30)) item_wgs = int64_t(1) << 30;
-    const int grid_x = int(item_wgs < 1 ? 1 : item_wgs);
-    const int grid_y = 1;
-    const size_t lds = (size_t(p->num_seqs) + 1) * sizeof(int);
     const int D = p->head_dim;
-    int rc;
-    if (p->io_dtype == VKV_DTYPE_F32) {
-        switch (p->kv_dtype) {
-            case VKV_DTYPE_F32: rc = dispatch_d<float, kF32>(D, G, a, grid_x, grid_y, 1, lds, st); break;
-            case VKV_DTYPE_F16: rc = dispatch_d<float, kF16>(D, G, a, grid_x, grid_y, 1, lds, st); break;
-            case VKV_DTYPE_FP8_E4M3: rc = dispatch_d<float, kFp8>(D, G, a, grid_x, grid_y, 1, lds, st); break;
-            default: return VKV_ERR_UNSUPPORTED;
+    const int io_eb = p->io_dtype == VKV_DTYPE_F32 ? 4 : 2;
+    // Consecutive ranges of at most kMaxRowsPerLaunch rows, each a partition
+    // launch and a merge launch on the stream; the ranges reuse the partials.
+    for (int r0 = 0; r0 < p->num_seqs; r0 += kMaxRowsPerLaunch) {
+        const int n = p->num_seqs - r0 < kMaxRowsPerLaunch ? p->num_seqs - r0 : kMaxRowsPerLaunch;
+        DecodeArgs c = a;
+        c.num_rows = n;
+        if (qsl) {
+            // rows are sequences; their query rows (qsl values) stay absolute
+            c.qsl = qsl + r0;
+            c.cl = a.cl + r0;
+            c.bt = a.bt + int64_t(r0) * p->max_blocks_per_seq;
+        } else {
+            c.q = static_cast<const char*>(a.q) + int64_t(r0) * a.q_stride * io_eb;
+            c.out = static_cast<char*>(a.out) + int64_t(r0) * p->num_heads * D * io_eb;
+            if (row_seq) {
+                // rows are query tokens; their sequences index the tables
+                c.row_seq = row_seq + r0;
+                c.row_ctx = row_ctx + r0;
+            } else {
+                c.cl = a.cl + r0;
+                c.bt = a.bt + int64_t(r0) * p->max_blocks_per_seq;
+            }
+        }
+        // Persistent grid (sized in launch_g from the kernel's occupancy), never
+        // more workgroups than item groups.
+        const int64_t max_items = int64_t(n) * plan.max_parts * p->num_kv_heads;
+        int64_t item_wgs = (max_items + kWavesPerBlock - 1) / kWavesPerBlock;
+        if (item_wgs > (int64_t(1) << 30)) item_wgs = int64_t(1) << 30;
+        const int grid_x = int(item_wgs < 1 ? 1 : item_wgs);
+        const size_t lds = (size_t(n) + 1) * sizeof(int);
+        int rc;
+        if (p->io_dtype == VKV_DTYPE_F32) {
+            switch (p->kv_dtype) {
+                case VKV_DTYPE_F32: rc = dispatch_d<float, kF32>(D, G, c, grid_x, 1, 1, lds, st); break;
+                case VKV_DTYPE_F16: rc = dispatch_d<float, kF16>(D, G, c, grid_x, 1, 1, lds, st); break;
+                case VKV_DTYPE_FP8_E4M3: rc = dispatch_d<float, kFp8>(D, G, c, grid_x, 1, 1, lds, st); break;
+                default: return VKV_ERR_UNSUPPORTED;
+            }
+            if (!rc) rc = launch_reduce<float>(D, c, p->num_heads, n, st);
+        } else {
+            switch (p->kv_dtype) {
+                case VKV_DTYPE_F16: rc = dispatch_d<_Float16, kF16>(D, G, c, grid_x, 1, 1, lds, st); break;
+                case VKV_DTYPE_FP8_E4M3: rc = dispatch_d<_Float16, kFp8>(D, G, c, grid_x, 1, 1, lds, st); break;
+                default: return VKV_ERR_UNSUPPORTED;
+            }
+            if (!rc) rc = launch_reduce<_Float16>(D, c, p->num_heads, n, st);
         }
         if (rc) return rc;
-        return launch_reduce<float>(D, a, p->num_heads, p->num_seqs, st);
     }
-    switch (p->kv_dtype) {
-        case VKV_DTYPE_F16: rc = dispatch_d<_Float16, kF16>(D, G, a, grid_x, grid_y, 1, lds, st); break;
-        case VKV_DTYPE_FP8_E4M3: rc = dispatch_d<_Float16, kFp8>(D, G, a, grid_x, grid_y, 1, lds, st); break;
-        default: return VKV_ERR_UNSUPPORTED;
-    }
-    if (rc) return rc;
-    return launch_reduce<_Float16>(D, a, p->num_heads, p->num_seqs, st);
+    return 0;
 }
 
 int launch_decode(const vkv_decode_params* p, const DecodePlan& plan, void* workspace, hipStream_t st) {
@@ -1329,7 +1359,7 @@ vkv_decode_params prefill_as_decode(const vkv_prefill_params* p, bool per_sequen
     d.num_kv_heads = p->num_kv_heads;
     d.head_dim = p->head_dim;
     d.block_size = p->block_size;
-    d.max_context_len = 0x7FFFFFFF;
+    d.max_context_len = p->max_context_len > 0 ? p->max_context_len : 0x7FFFFFFF;
     d.max_blocks_per_seq = p->max_blocks_per_seq;
     d.num_blocks = p->num_blocks;
     d.scale = p->scale;
@@ -1379,11 +1409,11 @@ int launch_prefill(const vkv_prefill_params* p, const DecodePlan& plan, void* wo
     const size_t partial_bytes = plan.workspace_bytes - size_t(p->num_query_tokens) * 2 * sizeof(int32_t);
     int32_t* row_seq = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + partial_bytes);
     int32_t* row_ctx = row_seq + p->num_query_tokens;
-    const int32_t table_tokens = int32_t(int64_t(p->max_blocks_per_seq) * p->block_size > 0x7FFFFFFF
-                                             ? 0x7FFFFFFF
-                                             : int64_t(p->max_blocks_per_seq) * p->block_size);
+    int64_t max_keys = int64_t(p->max_blocks_per_seq) * p->block_size;
+    if (p->max_context_len > 0 && p->max_context_len < max_keys) max_keys = p->max_context_len;
+    const int32_t max_ctx = int32_t(max_keys > 0x7FFFFFFF ? 0x7FFFFFFF : max_keys);
     hipLaunchKernelGGL(prefill_rows_kernel, dim3((p->num_query_tokens + 255) / 256), dim3(256), 0, st,
-                       p->query_start_loc, p->context_lens, p->num_seqs, p->num_query_tokens, table_tokens, row_seq,
+                       p->query_start_loc, p->context_lens, p->num_seqs, p->num_query_tokens, max_ctx, row_seq,
                        row_ctx);
     return launch_rows(&d, plan, workspace, row_seq, row_ctx, nullptr, st);
 }

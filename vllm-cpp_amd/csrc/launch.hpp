@@ -9,6 +9,14 @@
 
 namespace vkv {
 
+// Argument checks and error reporting of the C ABI (capi.cpp), for entry
+// points defined in other files: the decode argument check, setting the
+// thread's last-error message (returns code), and the status after a launch
+// (a non-zero launcher result or a pending HIP error).
+int check_decode_args(const vkv_decode_params* p);
+int report_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int report_launch(int rc, const char* what);
+
 int launch_append(const vkv_append_params* p, hipStream_t st);
 int launch_rope_append(const vkv_rope_append_params* p, hipStream_t st);
 

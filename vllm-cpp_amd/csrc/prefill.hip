@@ -481,7 +481,6 @@ struct DmaTile8 {
     static constexpr int BYTES = kBK * ROW;
     __device__ static __forceinline__ int off(int row, int chunk) { return row * ROW + ((chunk ^ (row % CH)) << 4); }
 };
-constexpr bool kFp8Wide = true;  // FP8 at D = 128 on the direct-load kernel
 
 // Workgroup barrier without a vector-memory wait (LDS writes published).
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory"); }
@@ -1148,15 +1147,18 @@ int launch_prefill_mfma(const vkv_prefill_params* p, void* item_space, int32_t* 
     a.num_heads = p->num_heads;
     a.num_kv_heads = p->num_kv_heads;
     a.group = p->num_heads / p->num_kv_heads;
-    // fp16 caches: prefill_wide_kernel, Wide<D>::ROWS (token, head) rows per item;
-    // FP8: prefill_mfma_kernel, up to kMaxWaves heads x kBQ tokens per item
-    const bool wide = p->kv_dtype == VKV_DTYPE_F16 || (kFp8Wide && p->head_dim == 128);
+    // fp16 caches and FP8 caches at D = 128: prefill_wide_kernel /
+    // prefill_wide8_kernel, Wide<D>::ROWS (token, head) rows per item; FP8 at
+    // D = 64: prefill_mfma_kernel, up to kMaxWaves heads x kBQ tokens per item
+    const bool wide = p->kv_dtype == VKV_DTYPE_F16 || p->head_dim == 128;
     const int head_groups = wide ? 1 : (a.group + kMaxWaves - 1) / kMaxWaves;
     a.heads_per_wg = (a.group + head_groups - 1) / head_groups;
     a.bs_log2 = ilog2i(p->block_size);
     a.max_blocks_per_seq = p->max_blocks_per_seq;
     a.num_blocks = p->num_blocks;
-    const int64_t tt = int64_t(p->max_blocks_per_seq) * p->block_size;
+    // keys any row may see: the table, and the caller's max_context_len clamp
+    int64_t tt = int64_t(p->max_blocks_per_seq) * p->block_size;
+    if (p->max_context_len > 0 && p->max_context_len < tt) tt = p->max_context_len;
     a.table_tokens = int32_t(tt > 0x7FFFFFFF ? 0x7FFFFFFF : tt);
     const int row_mult = wide ? a.group : 1;
     const int rows_per_item = wide ? (p->head_dim == 128 ? Wide<128>::ROWS : Wide<64>::ROWS) : kBQ;
@@ -1197,8 +1199,7 @@ int launch_prefill_mfma(const vkv_prefill_params* p, void* item_space, int32_t* 
     const dim3 grid(unsigned(wgs > 0 ? wgs : 1), 1u, unsigned(head_groups));
     const dim3 block(unsigned(64 * waves));
     if (p->head_dim == 128) {
-        if (!wide) hipLaunchKernelGGL((prefill_mfma_kernel<128, kFp8>), grid, block, 0, st, a);
-        else if (p->kv_dtype == VKV_DTYPE_F16) hipLaunchKernelGGL((prefill_wide_kernel<128>), grid, block, 0, st, a);
+        if (p->kv_dtype == VKV_DTYPE_F16) hipLaunchKernelGGL((prefill_wide_kernel<128>), grid, block, 0, st, a);
         else hipLaunchKernelGGL(prefill_wide8_kernel, grid, block, 0, st, a);
     } else {
         if (wide) hipLaunchKernelGGL((prefill_wide_kernel<64>), grid, block, 0, st, a);

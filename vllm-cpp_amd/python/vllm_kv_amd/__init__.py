@@ -32,7 +32,8 @@ ERRORS = {
 # Every symbol the C header declares; tests check the library exports them all.
 EXPORTED = [
     "vkv_last_error", "vkv_abi_version", "vkv_reshape_and_cache", "vkv_slot_mapping_host",
-    "vkv_paged_decode_workspace_size", "vkv_paged_decode", "vkv_paged_prefill",
+    "vkv_paged_decode_workspace_size", "vkv_paged_decode", "vkv_paged_prefill_workspace_size",
+    "vkv_paged_prefill",
     "vkv_copy_blocks", "vkv_check_block_pairs_host", "vkv_swap_host_block_bytes",
     "vkv_swap_blocks", "vkv_rope_reshape_and_cache", "vkv_rope_cos_sin_host",
     "vkv_kv_block_bytes", "vkv_kv_pool_num_blocks",
@@ -107,6 +108,8 @@ class PrefillParams(ctypes.Structure):
         ("block_size", ctypes.c_int32), ("max_blocks_per_seq", ctypes.c_int32),
         ("num_blocks", ctypes.c_int32), ("scale", ctypes.c_float),
         ("io_dtype", ctypes.c_int32), ("kv_dtype", ctypes.c_int32),
+        ("max_context_len", ctypes.c_int32),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
     ]
 
 
@@ -144,6 +147,8 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
         f.restype = ctypes.c_int
     lib.vkv_paged_decode_workspace_size.argtypes = [ctypes.POINTER(DecodeParams)]
     lib.vkv_paged_decode_workspace_size.restype = ctypes.c_size_t
+    lib.vkv_paged_prefill_workspace_size.argtypes = [ctypes.POINTER(PrefillParams)]
+    lib.vkv_paged_prefill_workspace_size.restype = ctypes.c_size_t
     lib.vkv_slot_mapping_host.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
                                           ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]
     lib.vkv_slot_mapping_host.restype = ctypes.c_int
@@ -314,14 +319,12 @@ def decode_workspace_size(out, query, key_cache, value_cache, block_tables, cont
     return int(load().vkv_paged_decode_workspace_size(ctypes.byref(p)))
 
 
-def paged_prefill(out, query, key_cache, value_cache, block_tables, context_lens, query_start_loc,
-                  max_query_len, scale, key_scales=None, value_scales=None, stream=None) -> None:
-    """out/query [Tq, H, D]; query_start_loc int32 [S+1]; context_lens counts the step's tokens."""
-    _require_cuda(out, query, key_cache, value_cache, block_tables, context_lens, query_start_loc,
-                  key_scales, value_scales)
+def prefill_params(out, query, key_cache, value_cache, block_tables, context_lens, query_start_loc,
+                   max_query_len, scale, key_scales=None, value_scales=None, max_context_len=0,
+                   workspace=None) -> PrefillParams:
     Tq, H, D = out.shape
     N, bs, Hkv, _ = key_cache.shape
-    p = PrefillParams(
+    return PrefillParams(
         output=_ptr(out), query=_ptr(query), key_cache=_ptr(key_cache), value_cache=_ptr(value_cache),
         key_scales=_ptr(key_scales), value_scales=_ptr(value_scales),
         block_tables=_ptr(block_tables), context_lens=_ptr(context_lens),
@@ -329,8 +332,28 @@ def paged_prefill(out, query, key_cache, value_cache, block_tables, context_lens
         num_seqs=context_lens.shape[0], num_query_tokens=Tq, max_query_len=max_query_len,
         num_heads=H, num_kv_heads=Hkv, head_dim=D, block_size=bs,
         max_blocks_per_seq=block_tables.shape[1], num_blocks=N, scale=scale,
-        io_dtype=_dtype_code(out), kv_dtype=_dtype_code(key_cache))
+        io_dtype=_dtype_code(out), kv_dtype=_dtype_code(key_cache), max_context_len=max_context_len,
+        workspace=_ptr(workspace),
+        workspace_bytes=0 if workspace is None else workspace.numel() * workspace.element_size())
+
+
+def paged_prefill(out, query, key_cache, value_cache, block_tables, context_lens, query_start_loc,
+                  max_query_len, scale, key_scales=None, value_scales=None, max_context_len=0,
+                  workspace=None, stream=None) -> None:
+    """out/query [Tq, H, D]; query_start_loc int32 [S+1]; context_lens counts the step's tokens.
+    max_context_len > 0 clamps every row's keys; workspace (optional) as for paged_decode."""
+    _require_cuda(out, query, key_cache, value_cache, block_tables, context_lens, query_start_loc,
+                  key_scales, value_scales, workspace)
+    p = prefill_params(out, query, key_cache, value_cache, block_tables, context_lens, query_start_loc,
+                       max_query_len, scale, key_scales, value_scales, max_context_len, workspace)
     check(load().vkv_paged_prefill(ctypes.byref(p), _stream(stream)))
+
+
+def prefill_workspace_size(out, query, key_cache, value_cache, block_tables, context_lens, query_start_loc,
+                           max_query_len, scale, key_scales=None, value_scales=None, max_context_len=0) -> int:
+    p = prefill_params(out, query, key_cache, value_cache, block_tables, context_lens, query_start_loc,
+                       max_query_len, scale, key_scales, value_scales, max_context_len, None)
+    return int(load().vkv_paged_prefill_workspace_size(ctypes.byref(p)))
 
 
 def planes_of(tensors: Sequence, num_layers: int):
