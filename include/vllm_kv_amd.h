@@ -236,6 +236,20 @@ typedef struct vkv_decode_params {
 size_t vkv_paged_decode_workspace_size(const vkv_decode_params* p);
 int vkv_paged_decode(const vkv_decode_params* p, vkv_stream_t stream);
 
+/* Paged decode that allocates nothing.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops and harnesses that forbid hipMalloc).  Same
+ * arguments, kernels and results as vkv_paged_decode, except that workspace /
+ * workspace_bytes are ignored: the split-K partials and claim counters live in
+ * a fixed 64 MiB device array of the library (one per device, held from the
+ * first call on that device until the process ends; the counters are cleared
+ * by a kernel at the start of each call).  A call whose
+ * vkv_paged_decode_workspace_size() exceeds 64 MiB fails with
+ * VKV_ERR_WORKSPACE before any launch.  All calls on one device share the
+ * array: calls that overlap on one device (other streams, other threads) race
+ * and give wrong results; serialise them.  Calls no hipMalloc or hipFree. */
+int vkv_paged_decode_noalloc(const vkv_decode_params* p, vkv_stream_t stream);
+
 /* -------------------------------------------------------------------------
  * Chunked-prefill (and mixed) paged attention, causal.
  *

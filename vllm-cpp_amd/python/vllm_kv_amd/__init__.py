@@ -32,7 +32,8 @@ ERRORS = {
 # Every symbol the C header declares; tests check the library exports them all.
 EXPORTED = [
     "vkv_last_error", "vkv_abi_version", "vkv_reshape_and_cache", "vkv_slot_mapping_host",
-    "vkv_paged_decode_workspace_size", "vkv_paged_decode", "vkv_paged_prefill_workspace_size",
+    "vkv_paged_decode_workspace_size", "vkv_paged_decode", "vkv_paged_decode_noalloc",
+    "vkv_paged_prefill_workspace_size",
     "vkv_paged_prefill",
     "vkv_copy_blocks", "vkv_check_block_pairs_host", "vkv_swap_host_block_bytes",
     "vkv_swap_blocks", "vkv_rope_reshape_and_cache", "vkv_rope_cos_sin_host",
@@ -140,6 +141,7 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.vkv_last_error.restype = ctypes.c_char_p
     lib.vkv_abi_version.restype = ctypes.c_int
     for name, ptype in (("vkv_reshape_and_cache", AppendParams), ("vkv_paged_decode", DecodeParams),
+                        ("vkv_paged_decode_noalloc", DecodeParams),
                         ("vkv_paged_prefill", PrefillParams),
                         ("vkv_rope_reshape_and_cache", RopeAppendParams)):
         f = getattr(lib, name)
@@ -309,6 +311,17 @@ def paged_decode(out, query, key_cache, value_cache, block_tables, context_lens,
     p = decode_params(out, query, key_cache, value_cache, block_tables, context_lens, scale,
                       key_scales, value_scales, max_context_len, accumulate, partition_size, workspace)
     check(load().vkv_paged_decode(ctypes.byref(p), _stream(stream)))
+
+
+def paged_decode_noalloc(out, query, key_cache, value_cache, block_tables, context_lens, scale,
+                         key_scales=None, value_scales=None, max_context_len=None, accumulate=False,
+                         partition_size=0, stream=None) -> None:
+    """paged_decode with the split-K workspace in the library's fixed device array
+    (no allocation; overlapping calls on one device race)."""
+    _require_cuda(out, query, key_cache, value_cache, block_tables, context_lens, key_scales, value_scales)
+    p = decode_params(out, query, key_cache, value_cache, block_tables, context_lens, scale,
+                      key_scales, value_scales, max_context_len, accumulate, partition_size, None)
+    check(load().vkv_paged_decode_noalloc(ctypes.byref(p), _stream(stream)))
 
 
 def decode_workspace_size(out, query, key_cache, value_cache, block_tables, context_lens, scale,
