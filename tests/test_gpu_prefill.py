@@ -238,8 +238,9 @@ def test_prefill_mixed_on_caller_stream(vkv, cuda):
 def test_prefill_mixed_graph_replays(vkv, cuda):
     """A mixed call captured in a graph (work-list, prefill, decode and merge
     kernels; the claim counters are reset by kernels, not memsets) replays to
-    the eager result, with eager calls on the same library workspace and
-    synchronisations between the replays."""
+    the eager result, with eager calls on the capture stream's library
+    workspace and synchronisations between the replays.  The capture stream's
+    workspace is sized by one eager call first (it cannot grow under capture)."""
     import torch
     out, args, mql, scale = _mixed_inputs(cuda)
     vkv.paged_prefill(out, *args, mql, scale)
@@ -249,13 +250,15 @@ def test_prefill_mixed_graph_replays(vkv, cuda):
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
+        vkv.paged_prefill(torch.empty_like(out), *args, mql, scale, stream=s)
         out.zero_()
         with torch.cuda.graph(g, stream=s):
             vkv.paged_prefill(out, *args, mql, scale, stream=s)
     torch.cuda.synchronize()
     for i in range(3):
         out.fill_(float("nan"))
-        vkv.paged_prefill(torch.empty_like(out), *args, mql, scale)  # eager work between replays
+        with torch.cuda.stream(s):
+            vkv.paged_prefill(torch.empty_like(out), *args, mql, scale, stream=s)  # eager work between replays
         torch.cuda.synchronize()
         g.replay()
         torch.cuda.synchronize()
