@@ -3,8 +3,10 @@
 // vllm::paged_attention_forward against a direct host computation.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
+#include <cstdio>
 #include <random>
 #include <vector>
 
@@ -136,6 +138,126 @@ TEST_CASE(append_and_paged_attention_forward_fp32) {
     (void)hipFree(dslots);
     (void)hipFree(dtable);
     (void)hipFree(dctx);
+}
+
+// vllm::paged_attention_forward (fp32, the reference's types) at shapes the
+// reference kernel accepts beyond the fixed-shape kernels: head_dim 80 / 96 /
+// 98, groups 16 / 32 / 64 (MQA), block sizes 12 / 24 / 7.  Several sequences
+// over randomly permuted blocks, `out +=` on a zeroed output, against an fp64
+// host computation of softmax(scale q K^T) V.
+namespace {
+struct Shape {
+    int H, Hkv, D, bs;
+    std::vector<int> ctx;
+};
+
+double forward_case(const Shape& c, unsigned seed) {
+    const int S = int(c.ctx.size());
+    int MB = 1, need = 0;
+    for (int n : c.ctx) {
+        MB = std::max(MB, (n + c.bs - 1) / c.bs);
+        need += (n + c.bs - 1) / c.bs;
+    }
+    const int N = need + 3;
+    std::mt19937 gen(seed);
+    std::normal_distribution<float> nd(0.f, 0.5f);
+    const size_t pool = size_t(N) * c.bs * c.Hkv * c.D;
+    std::vector<float> k(pool), v(pool), q(size_t(S) * c.H * c.D);
+    for (auto& x : k) x = nd(gen);
+    for (auto& x : v) x = nd(gen);
+    for (auto& x : q) x = nd(gen);
+    std::vector<int32_t> perm(N);
+    for (int i = 0; i < N; ++i) perm[i] = i;
+    std::shuffle(perm.begin(), perm.end(), gen);
+    std::vector<int32_t> table(size_t(S) * MB, 0), ctx(c.ctx.begin(), c.ctx.end());
+    int next = 0;
+    for (int s = 0; s < S; ++s)
+        for (int b = 0; b < (c.ctx[s] + c.bs - 1) / c.bs; ++b) table[size_t(s) * MB + b] = perm[next++];
+    float *dk, *dv, *dq, *dout;
+    int32_t *dtable, *dctx;
+    VLLM_HIP_CHECK(hipMalloc(&dk, pool * 4));
+    VLLM_HIP_CHECK(hipMalloc(&dv, pool * 4));
+    VLLM_HIP_CHECK(hipMalloc(&dq, q.size() * 4));
+    VLLM_HIP_CHECK(hipMalloc(&dout, q.size() * 4));
+    VLLM_HIP_CHECK(hipMalloc(&dtable, table.size() * 4));
+    VLLM_HIP_CHECK(hipMalloc(&dctx, S * 4));
+    VLLM_HIP_CHECK(hipMemcpy(dk, k.data(), pool * 4, hipMemcpyHostToDevice));
+    VLLM_HIP_CHECK(hipMemcpy(dv, v.data(), pool * 4, hipMemcpyHostToDevice));
+    VLLM_HIP_CHECK(hipMemcpy(dq, q.data(), q.size() * 4, hipMemcpyHostToDevice));
+    VLLM_HIP_CHECK(hipMemcpy(dtable, table.data(), table.size() * 4, hipMemcpyHostToDevice));
+    VLLM_HIP_CHECK(hipMemcpy(dctx, ctx.data(), S * 4, hipMemcpyHostToDevice));
+    VLLM_HIP_CHECK(hipMemset(dout, 0, q.size() * 4));
+    vllm::PagedAttentionParams p{};
+    p.output = dout;
+    p.query = dq;
+    p.key_cache = dk;
+    p.value_cache = dv;
+    p.block_tables = dtable;
+    p.context_lens = dctx;
+    p.num_seqs = S;
+    p.num_heads = c.H;
+    p.num_kv_heads = c.Hkv;
+    p.head_dim = c.D;
+    p.block_size = c.bs;
+    p.max_context_len = MB * c.bs;
+    p.max_blocks_per_seq = MB;
+    p.scale = 1.0f / std::sqrt(float(c.D));
+    p.stream = nullptr;
+    vllm::paged_attention_forward(p);
+    std::vector<float> out(q.size());
+    VLLM_HIP_CHECK(hipMemcpy(out.data(), dout, out.size() * 4, hipMemcpyDeviceToHost));
+    double worst = 0;
+    const int G = c.H / c.Hkv;
+    for (int s = 0; s < S; ++s) {
+        for (int h = 0; h < c.H; ++h) {
+            const int kvh = h / G;
+            auto row = [&](const std::vector<float>& x, int t) {
+                const int blk = table[size_t(s) * MB + t / c.bs];
+                return &x[((size_t(blk) * c.bs + t % c.bs) * c.Hkv + kvh) * c.D];
+            };
+            const float* qh = &q[(size_t(s) * c.H + h) * c.D];
+            std::vector<double> w(c.ctx[s]);
+            double m = -1e300, sum = 0;
+            for (int t = 0; t < c.ctx[s]; ++t) {
+                const float* kr = row(k, t);
+                double d = 0;
+                for (int i = 0; i < c.D; ++i) d += double(qh[i]) * kr[i];
+                w[t] = d * p.scale;
+                m = std::max(m, w[t]);
+            }
+            for (int t = 0; t < c.ctx[s]; ++t) sum += (w[t] = std::exp(w[t] - m));
+            for (int i = 0; i < c.D; ++i) {
+                double o = 0;
+                for (int t = 0; t < c.ctx[s]; ++t) o += w[t] / sum * row(v, t)[i];
+                const double got = out[(size_t(s) * c.H + h) * c.D + i];
+                worst = std::max(worst, std::fabs(o - got) / (2e-5 + 1e-4 * std::fabs(o)));
+            }
+        }
+    }
+    (void)hipFree(dk);
+    (void)hipFree(dv);
+    (void)hipFree(dq);
+    (void)hipFree(dout);
+    (void)hipFree(dtable);
+    (void)hipFree(dctx);
+    return worst;
+}
+}  // namespace
+
+TEST_CASE(paged_attention_forward_any_shape) {
+    const Shape shapes[] = {
+        {32, 2, 80, 12, {1, 12, 13, 250}},    // head_dim 80, group 16, block 12
+        {64, 2, 96, 24, {7, 24, 300}},        // head_dim 96, group 32, block 24
+        {64, 1, 80, 24, {2, 100}},            // MQA: group 64
+        {6, 3, 98, 7, {1, 8, 90}},            // element loads, block 7
+    };
+    unsigned seed = 11;
+    for (const Shape& c : shapes) {
+        const double worst = forward_case(c, seed++);
+        if (worst > 1.0)
+            std::printf("  H%d Hkv%d D%d bs%d: worst error ratio %.3f\n", c.H, c.Hkv, c.D, c.bs, worst);
+        CHECK(worst <= 1.0);
+    }
 }
 
 TEST_CASE(copy_blocks_through_kv_cache) {

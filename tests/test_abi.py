@@ -51,13 +51,13 @@ def _decode_params(vkv, **over):
 
 @pytest.mark.parametrize("over,code", [
     (dict(num_heads=30), -2),            # not a multiple of num_kv_heads
-    (dict(num_heads=80), -3),            # group 10 > 8
-    (dict(head_dim=96), -3),
-    (dict(block_size=24), -3),           # not a power of two
+    (dict(head_dim=0), -2),
+    (dict(head_dim=1025), -3),           # beyond the generic kernel's largest head_dim
+    (dict(block_size=0), -2),
     (dict(io_dtype=1, kv_dtype=0), -3),  # fp32 KV with fp16 io
     (dict(kv_dtype=2), -1),              # fp8 without scales
     (dict(query=0), -1),
-    (dict(key_cache=24), -5),            # misaligned
+    (dict(key_cache=25), -5),            # not even fp16-aligned
     (dict(max_blocks_per_seq=0), -2),
 ])
 def test_decode_argument_errors(vkv, over, code):

@@ -65,6 +65,95 @@ def test_decode_f16_vs_oracle(vkv, oracle, cuda, H, Hkv, D, bs, ctx):
     assert_close(got, ref, F16_ATOL, F16_RTOL, "fp16 decode")
 
 
+# Shapes outside the fixed-shape kernels (head_dim 64/128/256, group <= 8,
+# power-of-two blocks) run on the generic variant: any head_dim up to 1024
+# (whole 16-byte vectors or single elements), any group size (query heads in
+# chunks), any block size.  (H, Hkv, D, bs, contexts, io dtype, kv dtype)
+GENERIC_CASES = [
+    (32, 2, 80, 12, [1, 13, 300, 1000], "f16", "f16"),    # group 16, head_dim 80
+    (64, 2, 96, 24, [5, 24, 25, 777], "f16", "f16"),      # group 32
+    (64, 1, 128, 16, [3, 200, 1500], "f16", "f16"),       # MQA, group 64
+    (16, 16, 112, 16, [9, 400], "f16", "f16"),            # group 1, head_dim 112
+    (12, 4, 100, 10, [1, 11, 250], "f16", "f16"),         # 200-byte heads: element loads
+    (8, 8, 33, 5, [1, 6, 77], "f16", "f16"),              # odd head_dim and block size
+    (8, 2, 64, 1, [1, 2, 100], "f16", "f16"),             # one-token blocks
+    (4, 1, 576, 16, [2, 300], "f16", "f16"),              # head_dim 576 (two vectors per lane)
+    (8, 2, 1024, 8, [17, 129], "f16", "f16"),             # the largest head_dim
+    (20, 5, 128, 48, [47, 48, 49, 2000], "f16", "f16"),   # power-of-two head_dim, block 48
+    (32, 2, 80, 12, [1, 40, 900], "f32", "f32"),          # the reference API's dtype
+    (6, 3, 98, 7, [3, 70], "f32", "f32"),                 # fp32 element loads
+    (20, 2, 96, 24, [8, 333], "f32", "f16"),
+    (32, 2, 96, 16, [1, 130, 600], "f16", "fp8"),         # FP8 cache, group 16
+    (24, 8, 64, 12, [12, 13, 500], "f16", "fp8"),         # FP8, non-power-of-two blocks
+    (16, 4, 104, 8, [5, 300], "f32", "fp8"),              # FP8 104-byte heads: element loads
+]
+
+
+@pytest.mark.parametrize("H,Hkv,D,bs,ctx,io,kv", GENERIC_CASES)
+def test_decode_generic_shapes_vs_oracle(vkv, oracle, cuda, H, Hkv, D, bs, ctx, io, kv):
+    import torch
+    rng = np.random.default_rng(H * 7 + D * 3 + bs)
+    lay = _layout(rng, ctx, bs)
+    N = lay.num_blocks
+    kf = rng.standard_normal((N, bs, Hkv, D), dtype=np.float32) * 0.5
+    vf = rng.standard_normal((N, bs, Hkv, D), dtype=np.float32) * 0.5
+    q = rng.standard_normal((len(ctx), H, D), dtype=np.float32) * 0.5
+    scale = float(1.0 / np.sqrt(np.float32(D)))
+    ks = vs = hks = hvs = None
+    if kv == "f32":
+        hk, hv, kc, vc = kf, vf, to_dev(kf, cuda), to_dev(vf, cuda)
+    elif kv == "f16":
+        hk, hv = kf.astype(np.float16).view(np.uint16), vf.astype(np.float16).view(np.uint16)
+        kc, vc = to_dev(hk.view(np.float16), cuda), to_dev(hv.view(np.float16), cuda)
+    else:  # FP8 codes and scales from the oracle's quantisation of the fp16 pool
+        k16, v16 = kf.astype(np.float16).view(np.uint16), vf.astype(np.float16).view(np.uint16)
+        hk = np.zeros((N, bs, Hkv, D), np.uint8)
+        hv = np.zeros_like(hk)
+        hks = np.zeros((N, bs, Hkv), np.float32)
+        hvs = np.zeros_like(hks)
+        oracle.reshape_and_cache(k16.reshape(-1, Hkv, D), v16.reshape(-1, Hkv, D), hk, hv,
+                                 np.arange(N * bs, dtype=np.int32), hks, hvs)
+        kc, vc, ks, vs = (to_dev(x, cuda) for x in (hk, hv, hks, hvs))
+    if io == "f16":
+        q = q.astype(np.float16).astype(np.float32)
+    ref = oracle.paged_decode(q, hk, hv, lay.block_tables, lay.context_lens, scale, key_scales=hks,
+                              value_scales=hvs)
+    out = torch.zeros((len(ctx), H, D), dtype=torch.float16 if io == "f16" else torch.float32, device=cuda)
+    qd = to_dev(q.astype(np.float16) if io == "f16" else q, cuda)
+    vkv.paged_decode(out, qd, kc, vc, to_dev(lay.block_tables, cuda), to_dev(lay.context_lens, cuda), scale,
+                     key_scales=ks, value_scales=vs)
+    torch.cuda.synchronize()
+    tol = {"f16": (F16_ATOL, F16_RTOL), "f32": (F32_ATOL, F32_RTOL if kv == "f32" else 1e-3)}[io]
+    assert_close(to_np(out).astype(np.float32), ref, *tol, f"generic decode {H}/{Hkv}/{D}/bs{bs} {io}/{kv}")
+
+
+def test_decode_generic_unaligned_cache(vkv, oracle, cuda):
+    """Caches that are only element-aligned (an fp16 pool starting 2 bytes into
+    its allocation) at a fixed-kernel shape take the generic variant with
+    element loads; same result as the oracle."""
+    import torch
+    rng = np.random.default_rng(41)
+    H, Hkv, D, bs, ctx = 32, 8, 128, 16, [3, 300, 1100]
+    lay = _layout(rng, ctx, bs)
+    k, v = _pool(rng, lay.num_blocks, bs, Hkv, D, 0.5)
+    q = (rng.standard_normal((len(ctx), H, D), dtype=np.float32) * 0.5).astype(np.float16)
+    scale = float(1.0 / np.sqrt(np.float32(D)))
+    ref = oracle.paged_decode(q.astype(np.float32), k.view(np.uint16), v.view(np.uint16), lay.block_tables,
+                              lay.context_lens, scale)
+    flat_k = torch.zeros(k.size + 8, dtype=torch.float16, device=cuda)
+    flat_v = torch.zeros(v.size + 8, dtype=torch.float16, device=cuda)
+    flat_k[1:1 + k.size] = to_dev(k.reshape(-1), cuda)
+    flat_v[1:1 + v.size] = to_dev(v.reshape(-1), cuda)
+    kc = flat_k[1:1 + k.size].view(k.shape)
+    vc = flat_v[1:1 + v.size].view(v.shape)
+    assert kc.data_ptr() % 16 == 2
+    got = torch.zeros((len(ctx), H, D), dtype=torch.float16, device=cuda)
+    vkv.paged_decode(got, to_dev(q, cuda), kc, vc, to_dev(lay.block_tables, cuda), to_dev(lay.context_lens, cuda),
+                     scale)
+    torch.cuda.synchronize()
+    assert_close(to_np(got).astype(np.float32), ref, F16_ATOL, F16_RTOL, "unaligned fp16 cache")
+
+
 @pytest.mark.parametrize("partition_size", [16, 64, 128, 512])
 def test_decode_partition_sizes(vkv, oracle, cuda, partition_size):
     """Split-K merging is independent of where the context is cut."""

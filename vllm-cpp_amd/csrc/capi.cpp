@@ -42,6 +42,12 @@ int after_launch(int rc, const char* what) {
 
 bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
 
+// Decode shape domain: any group size H / Hkv, head_dim and block_size up to
+// these bounds (the reference kernel has none; these keep every per-lane
+// register tile and partition size within the generic kernel's layout).
+constexpr int kMaxHeadDim = 1024;
+constexpr int kMaxBlockSize = 1 << 20;
+
 // Library-owned workspaces, one per (device, stream): calls on different
 // streams never share one, calls on one stream are ordered by it.  A buffer
 // only grows.  An outgrown buffer is retired, not freed: queued work or a
@@ -117,12 +123,11 @@ int check_decode(const vkv_decode_params* p) {
     if (p->num_heads <= 0 || p->num_kv_heads <= 0 || p->num_heads % p->num_kv_heads != 0)
         return fail(VKV_ERR_SHAPE, "num_heads (%d) must be a positive multiple of num_kv_heads (%d)", p->num_heads,
                     p->num_kv_heads);
-    const int G = p->num_heads / p->num_kv_heads;
-    if (G > 8) return fail(VKV_ERR_UNSUPPORTED, "group size %d > 8 not built", G);
-    if (p->head_dim != 64 && p->head_dim != 128 && p->head_dim != 256)
-        return fail(VKV_ERR_UNSUPPORTED, "head_dim %d not built (64, 128, 256)", p->head_dim);
-    if (!is_pow2(p->block_size) || p->block_size > 1024)
-        return fail(VKV_ERR_UNSUPPORTED, "block_size %d must be a power of two <= 1024", p->block_size);
+    if (p->head_dim < 1 || p->head_dim > kMaxHeadDim)
+        return fail(p->head_dim < 1 ? VKV_ERR_SHAPE : VKV_ERR_UNSUPPORTED, "head_dim %d outside 1..%d",
+                    p->head_dim, kMaxHeadDim);
+    if (p->block_size < 1 || p->block_size > kMaxBlockSize)
+        return fail(VKV_ERR_SHAPE, "block_size %d outside 1..%d", p->block_size, kMaxBlockSize);
     if (p->max_blocks_per_seq <= 0) return fail(VKV_ERR_SHAPE, "max_blocks_per_seq must be > 0");
     if (p->num_blocks < 0) return fail(VKV_ERR_SHAPE, "num_blocks < 0");
     if (p->io_dtype != VKV_DTYPE_F32 && p->io_dtype != VKV_DTYPE_F16)
@@ -138,8 +143,10 @@ int check_decode(const vkv_decode_params* p) {
     if (qs < int64_t(p->num_heads) * p->head_dim)
         return fail(VKV_ERR_SHAPE, "query_stride smaller than num_heads*head_dim");
     const int io_eb = p->io_dtype == VKV_DTYPE_F32 ? 4 : 2;
-    if ((reinterpret_cast<uintptr_t>(p->key_cache) | reinterpret_cast<uintptr_t>(p->value_cache)) & 15u)
-        return fail(VKV_ERR_ALIGN, "key_cache/value_cache must be 16-byte aligned");
+    const int kv_eb = p->kv_dtype == VKV_DTYPE_F32 ? 4 : (p->kv_dtype == VKV_DTYPE_F16 ? 2 : 1);
+    if ((reinterpret_cast<uintptr_t>(p->key_cache) | reinterpret_cast<uintptr_t>(p->value_cache)) &
+        uintptr_t(kv_eb - 1))
+        return fail(VKV_ERR_ALIGN, "key_cache/value_cache misaligned for their dtype");
     if ((reinterpret_cast<uintptr_t>(p->query) & uintptr_t(io_eb - 1)) ||
         (reinterpret_cast<uintptr_t>(p->output) & uintptr_t(io_eb - 1)))
         return fail(VKV_ERR_ALIGN, "query/output misaligned for their dtype");

@@ -1,0 +1,356 @@
+// decode_common.hpp — what the split-K decode kernels of decode.hip (fixed
+// shapes) and decode_generic.hip (any head_dim, group size and block size)
+// share: the argument block, the row helpers, the per-lane K/V loads, the
+// device-side partition choice and the persistent item loop.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdlib>
+
+#include "common.hpp"
+#include "launch.hpp"
+
+namespace vkv {
+namespace dec {
+
+constexpr int kWavesPerBlock = 4;
+// Workspace layout: a 1 KiB header holding the work-claim counters (zero
+// between calls: the merge kernel resets them) followed by the partials.
+constexpr size_t kWorkspaceHeader = 1024;
+constexpr int kClaimSequences = 8;
+constexpr int kCounterStride = 32;  // ints: one 128-byte line per counter
+constexpr float kLog2e = 1.4426950408889634f;
+// Fixed cost of one item (partial write, merge input, chain start-up) in
+// token-equivalents, for the span estimate of the partition choice.
+constexpr int kItemOverheadTokens = 128;
+// LDS per CU on gfx950, for the resident-wave estimate.
+constexpr int kLdsPerCu = 160 * 1024;
+// Rows (sequences or query rows) per partition launch: the kernel keeps one
+// prefix entry per row in LDS.  Larger calls run as consecutive launches.
+constexpr int kMaxRowsPerLaunch = 8192;
+// Rows of the largest launch of a call (the partials are sized for it).
+inline int launch_rows_max(int num_rows) { return num_rows < kMaxRowsPerLaunch ? num_rows : kMaxRowsPerLaunch; }
+
+struct DecodeArgs {
+    void* out;
+    const void* q;
+    const char* kc;
+    const char* vc;
+    const float* ks;
+    const float* vs;
+    const int32_t* bt;
+    const int32_t* cl;
+    const int32_t* row_seq;  // prefill: query row -> sequence (NULL for decode: row == sequence)
+    const int32_t* row_ctx;  // prefill: keys visible to the row (causal), replaces the ctx clamp
+    // Mixed prefill batch (rows = sequences): query_start_loc.  Only sequences
+    // with one query token are decoded here (query row qsl[s]); the others
+    // belong to the prefill kernel and have no partitions.
+    const int32_t* qsl;
+    // Partials, item-major so that one item's G heads are contiguous:
+    // slot ((s * Hkv + kvh) * max_parts + part) * G + g for head kvh * G + g.
+    float* part_o;   // [S][Hkv][max_parts][G][D]
+    float* part_ml;  // [S][Hkv][max_parts][G][2] (max in log2 domain, sum)
+    int64_t q_stride;
+    int32_t num_heads;
+    int32_t num_kv_heads;
+    int32_t bs_log2;
+    int32_t max_ctx;
+    int32_t max_blocks_per_seq;
+    int32_t num_blocks;
+    int32_t P;
+    int32_t max_parts;
+    float scale_log2;
+    int32_t accumulate;
+    int32_t num_rows;         // sequences (decode) or query rows (prefill)
+    int* counters;            // claim counters in the workspace header (zero between calls)
+    int32_t mfma_enabled;     // use the matrix-core QK^T variant where it applies
+    // num_cands > 1: P is the default size, the kernel picks the partition
+    // size among cands (ascending) and records it in the workspace header.
+    int32_t num_cands;
+    int32_t cands[kMaxPartitionCandidates];
+    int32_t wave_slots;       // waves of this launch resident at once (estimate)
+    // generic variant (any head_dim / group size / block size) only
+    int32_t head_dim;
+    int32_t block_size;
+    int32_t io_f32;           // query and output are fp32 (else fp16)
+    int32_t vec_loads;        // whole-vector K/V loads (head_dim and cache alignment allow them)
+};
+
+// The shapes decode.hip's fixed-shape kernels are built for; every other
+// shape runs on decode_generic.hip.
+inline bool fixed_decode_shape(int head_dim, int group, int block_size, const void* kc, const void* vc) {
+    const bool pow2_bs = block_size > 0 && block_size <= 1024 && (block_size & (block_size - 1)) == 0;
+    const bool aligned = ((reinterpret_cast<uintptr_t>(kc) | reinterpret_cast<uintptr_t>(vc)) & 15u) == 0;
+    return (head_dim == 64 || head_dim == 128 || head_dim == 256) && group >= 1 && group <= 8 && pow2_bs && aligned;
+}
+
+// Partition kernel of the generic variant (decode_generic.hip) for one launch
+// of rows; max_pairs bounds the (row, partition) pairs.  0 or VKV_ERR_*.
+int launch_decode_generic(DecodeArgs& a, int kv_dtype, int64_t max_pairs, size_t lds, hipStream_t st);
+
+// Keys row r attends (clamped to the table) and the query/output row it uses.
+__device__ __forceinline__ int row_context(const DecodeArgs& a, int r) {
+    int ctx;
+    if (a.row_ctx) ctx = a.row_ctx[r];
+    else if (a.qsl) ctx = (a.qsl[r + 1] - a.qsl[r] == 1) ? a.cl[r] : 0;
+    else ctx = a.cl[r];
+    return ctx < a.max_ctx ? ctx : a.max_ctx;
+}
+__device__ __forceinline__ int64_t query_row(const DecodeArgs& a, int r) { return a.qsl ? a.qsl[r] : r; }
+
+template <int KVT>
+struct LaneLoad {
+    static constexpr int bytes = KVT == kFp8 ? 8 : 16;  // bytes per lane per load
+    static constexpr int words = bytes / 4;
+    static constexpr int elems = bytes / KvTraits<KVT>::bytes;
+};
+
+// K/V lane loads are non-temporal: every cache byte is read once per call, so
+// the stream should not displace other lines (measured: 14% faster gathers).
+template <int KVT>
+__device__ __forceinline__ void load_lane(const char* p, uint32_t* w) {
+    if constexpr (LaneLoad<KVT>::bytes == 16) {
+        const u32x4 v = load16_nt(p);
+        w[0] = v[0];
+        w[1] = v[1];
+        w[2] = v[2];
+        w[3] = v[3];
+    } else {
+        typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+        const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+        w[0] = v[0];
+        w[1] = v[1];
+    }
+}
+
+// Unpack one lane load into EPL floats in dimension order.  FP8 values come out
+// scaled by 2^-8 (the caller folds 256 into its per-token scale).
+template <int KVT>
+__device__ __forceinline__ void unpack_lane(const uint32_t* w, float* v) {
+    if constexpr (KVT == kF32) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = as_f32(w[i]);
+    } else if constexpr (KVT == kF16) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const half2_t h = as_half2(w[i]);
+            v[2 * i] = static_cast<float>(h[0]);
+            v[2 * i + 1] = static_cast<float>(h[1]);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            uint32_t lo, hi;
+            fp8x4_to_half2x2_scaled(w[i], lo, hi);
+            const half2_t a = as_half2(lo), b = as_half2(hi);
+            v[4 * i + 0] = static_cast<float>(a[0]);
+            v[4 * i + 1] = static_cast<float>(b[0]);
+            v[4 * i + 2] = static_cast<float>(a[1]);
+            v[4 * i + 3] = static_cast<float>(b[1]);
+        }
+    }
+}
+
+// Partition size of a call that left it to the library.  Every workgroup
+// evaluates the same candidates over the rows' context lengths (each thread
+// brings its row tile's partition count per candidate), so all reach the same
+// size.  Items run in rounds of wave_slots resident waves.  A call whose
+// default-size items fit in one round keeps the default: it is
+// bandwidth-bound, and longer partitions only lengthen each wave's chain
+// (C2's batch: 105 us at 768 tokens, 116 us at 1 024).  Between one and two
+// rounds a second round that is only partly filled costs nearly a whole one,
+// so the candidate with the least rounds x (P + kItemOverheadTokens) wins
+// (ties: the smaller size): C3's decode rows fill 1.6 rounds at 768 tokens
+// (227 us) and one at 1 280 (the choice, 207 us).  Beyond two rounds the
+// default stays: waves that claim items as they finish fill the last round
+// with the short final partitions of the rows, and C5's batch (3.3 rounds at
+// 768) measured 361 us at 768 against 365 us at 640, the size this estimate
+// would take.
+__device__ inline int choose_partition(const DecodeArgs& a, const int (&cnt)[kMaxPartitionCandidates]) {
+    __shared__ int sums[kWavesPerBlock][kMaxPartitionCandidates];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+#pragma unroll
+    for (int c = 0; c < kMaxPartitionCandidates; ++c) {
+        int v = cnt[c];
+#pragma unroll
+        for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+        if (lane == 0) sums[wave][c] = v;
+    }
+    __syncthreads();
+    const unsigned W = a.wave_slots > 0 ? unsigned(a.wave_slots) : 1u;
+    const unsigned cap = 0x7FFFFFFFu / unsigned(a.num_kv_heads);
+    unsigned items0 = 0;
+    uint64_t best_cost = ~uint64_t(0);
+    int best = a.P;
+#pragma unroll
+    for (int c = 0; c < kMaxPartitionCandidates; ++c) {
+        if (c >= a.num_cands) break;
+        unsigned pairs = 0;
+#pragma unroll
+        for (int w = 0; w < kWavesPerBlock; ++w) pairs += unsigned(sums[w][c]);
+        const unsigned items = (pairs < cap ? pairs : cap) * unsigned(a.num_kv_heads);
+        if (a.cands[c] == a.P) items0 = items;
+        const uint64_t cost = uint64_t((items + W - 1) / W) * unsigned(a.cands[c] + kItemOverheadTokens);
+        if (cost < best_cost) {
+            best_cost = cost;
+            best = a.cands[c];
+        }
+    }
+    return (items0 <= W || items0 > 2 * W) ? a.P : best;
+}
+
+// The item loop of the persistent partition kernels.  Items are numbered
+// densely, pair-major: pair = (row, partition), items_per_pair items each
+// (kv heads, or kv heads x query-head chunks), so no wave is launched for a
+// partition that does not exist (the context lengths live on the device, so
+// a fixed grid would carry many empty slots for long-tailed batches) and the
+// waves of a workgroup hold adjacent items of the same blocks.  Workgroups
+// claim item groups dynamically, so all stay busy until the list runs out.
+// Nothing waits on another workgroup.  item(P, row, partition, sub) runs
+// one item on the calling wave.
+template <class Item>
+__device__ __forceinline__ void run_partitions(const DecodeArgs& a, const int items_per_pair, Item&& item) {
+    extern __shared__ int prefix[];  // [num_rows + 1] exclusive prefix of partitions per row
+    const int lane = threadIdx.x & (kWave - 1);
+    const int nrows = a.num_rows;
+
+    // Partitions per row and their exclusive prefix, scanned by the whole
+    // workgroup: each thread sums a contiguous tile of rows, the 256 tile sums
+    // are scanned with wave shuffles plus one LDS step, then each thread writes
+    // its tile's prefix entries.  A call that leaves the partition size to the
+    // library counts its tile for every candidate size in the same pass and
+    // picks the size first (power-of-two block sizes only).
+    __shared__ int wave_total[kWavesPerBlock];
+    int P = a.P;
+    auto parts_of = [&](int r) {
+        const int ctx = row_context(a, r);
+        return ctx > 0 ? (ctx + P - 1) / P : 0;
+    };
+    const int per = (nrows + int(blockDim.x) - 1) / int(blockDim.x);
+    const int r0 = int(threadIdx.x) * per;
+    int local = 0;
+    if (a.num_cands > 1) {
+        int cnt[kMaxPartitionCandidates];
+#pragma unroll
+        for (int c = 0; c < kMaxPartitionCandidates; ++c) cnt[c] = 0;
+        for (int i = 0; i < per; ++i) {
+            const int ctx = r0 + i < nrows ? row_context(a, r0 + i) : 0;
+            if (ctx > 0) {
+                // candidates are block multiples m * bs: ceil(ctx / (m * bs)) = ceil(nb / m)
+                const int nb = ((ctx - 1) >> a.bs_log2) + 1;
+#pragma unroll
+                for (int c = 0; c < kMaxPartitionCandidates; ++c) {
+                    const int m = a.cands[c] >> a.bs_log2;  // >= 1 (the host pads unused entries)
+                    cnt[c] += (nb + m - 1) / m;
+                }
+            }
+        }
+        P = __builtin_amdgcn_readfirstlane(choose_partition(a, cnt));  // wave-uniform: keep it scalar
+#pragma unroll
+        for (int c = 0; c < kMaxPartitionCandidates; ++c)
+            if (a.cands[c] == P) local = cnt[c];
+        // for the merge kernel (same stream, after this grid)
+        if (blockIdx.x == 0 && threadIdx.x == 0) a.counters[kChosenPartitionSlot] = P;
+    } else {
+        for (int i = 0; i < per; ++i)
+            if (r0 + i < nrows) local += parts_of(r0 + i);
+    }
+    int incl = local;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+        const int y = __shfl_up(incl, o, kWave);
+        if (lane >= o) incl += y;
+    }
+    const int wave = threadIdx.x / kWave;
+    if (lane == kWave - 1) wave_total[wave] = incl;
+    __syncthreads();
+    int before = 0;
+    for (int w = 0; w < wave; ++w) before += wave_total[w];
+    int run = before + incl - local;
+    for (int i = 0; i < per; ++i) {
+        if (r0 + i < nrows) {
+            prefix[r0 + i] = run;
+            run += parts_of(r0 + i);
+        }
+    }
+    if (threadIdx.x == blockDim.x - 1) prefix[nrows] = before + incl;
+    __syncthreads();
+    const int num_pairs = prefix[nrows];
+    const int num_items = num_pairs * items_per_pair;
+
+    // Item groups of 4 consecutive items go to a workgroup, one item per
+    // wave.  Round 0 is static: workgroup b takes group b.  Later groups
+    // g >= gridDim.x are dealt in 8 interleaved sequences g = gridDim.x + 8k +
+    // q, each with its own counter (separate cache lines, so claims on
+    // different sequences do not queue on one address).  A workgroup claims
+    // from sequence blockIdx.x % 8 first and moves on to the next sequence when
+    // one is exhausted, so every group is processed exactly once wherever the
+    // workgroups run.
+    __shared__ int next_group;
+    const int num_groups = (num_items + kWavesPerBlock - 1) / kWavesPerBlock;
+    const int g0 = int(gridDim.x);
+    int g = blockIdx.x;
+    int q = blockIdx.x % kClaimSequences;
+    int tried = 0;
+    while (g < num_groups) {
+        const int it = g * kWavesPerBlock + wave;
+        if (it < num_items) {
+            const int pair = it / items_per_pair;
+            const int sub = it - pair * items_per_pair;
+            int lo = 0, hi = nrows - 1;  // row = last r with prefix[r] <= pair
+            while (lo < hi) {
+                const int mid = (lo + hi + 1) >> 1;
+                if (prefix[mid] <= pair) lo = mid;
+                else hi = mid - 1;
+            }
+            item(P, lo, pair - prefix[lo], sub);
+        }
+        if (g0 >= num_groups) break;  // the grid covers every group: nothing to claim
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            int next = num_groups;
+            while (tried < kClaimSequences) {
+                const int k = atomicAdd(a.counters + q * kCounterStride, 1);
+                const int cand = g0 + kClaimSequences * k + q;
+                if (cand < num_groups) {
+                    next = cand;
+                    break;
+                }
+                q = (q + 1) % kClaimSequences;  // this sequence is exhausted
+                ++tried;
+            }
+            next_group = next;
+        }
+        __syncthreads();
+        g = next_group;
+    }
+}
+
+// VKV_DECODE_BLOCKS_PER_CU=<n> overrides the grid's workgroups per CU
+// (tuning; default: as many as are resident at once).
+inline int blocks_per_cu(int fits) {
+    static const int v = [] {
+        const char* e = std::getenv("VKV_DECODE_BLOCKS_PER_CU");
+        return e ? std::atoi(e) : 0;
+    }();
+    return v > 0 ? v : fits;
+}
+
+inline int device_cu_count() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
+
+}  // namespace dec
+}  // namespace vkv

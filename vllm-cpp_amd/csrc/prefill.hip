@@ -1122,8 +1122,14 @@ int ilog2i(int x) {
 }  // namespace
 
 bool prefill_mfma_supported(const vkv_prefill_params* p) {
+    // 16-byte direct/vector loads of K, V and Q rows; power-of-two blocks
+    const int64_t qs = p->query_stride ? p->query_stride : int64_t(p->num_heads) * p->head_dim;
+    const uintptr_t align = reinterpret_cast<uintptr_t>(p->key_cache) | reinterpret_cast<uintptr_t>(p->value_cache) |
+                            reinterpret_cast<uintptr_t>(p->query) | uintptr_t(qs * 2);
+    const bool pow2_bs = p->block_size >= 1 && p->block_size <= 1024 && (p->block_size & (p->block_size - 1)) == 0;
     return p->io_dtype == VKV_DTYPE_F16 && (p->kv_dtype == VKV_DTYPE_F16 || p->kv_dtype == VKV_DTYPE_FP8_E4M3) &&
-           (p->head_dim == 64 || p->head_dim == 128) && p->max_query_len >= 2 &&
+           (p->head_dim == 64 || p->head_dim == 128) && p->max_query_len >= 2 && pow2_bs && (align & 15u) == 0 &&
+           p->num_kv_heads > 0 && p->num_heads % p->num_kv_heads == 0 &&
            p->num_heads / p->num_kv_heads <= kMaxHeadGroups * kMaxWaves;
 }
 
