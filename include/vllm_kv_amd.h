@@ -66,6 +66,10 @@ int vkv_abi_version(void);
  * block_table[pos / block_size] * block_size + pos % block_size;
  * vkv_slot_mapping_host() builds exactly that on the host.
  *
+ * Any head_dim and token stride; pointers aligned to their element size
+ * (16-byte rows take the vector kernels, other rows an element kernel with
+ * the same results).
+ *
  * cache_dtype F32 requires src F32 (bit copy); F16 takes F16 (bit copy) or
  * F32 (round to nearest even); FP8_E4M3 takes F16 or F32 and quantises per
  * (token, kv head): amax = max|x| over head_dim, scale = amax / 448 (IEEE
@@ -184,8 +188,11 @@ int vkv_rope_cos_sin_host(float theta, int32_t head_dim, int32_t max_position, f
  * output first, src/layers/attention.cpp:128); accumulate = 0 overwrites.
  *
  * io_dtype (query and output): F32 or F16.  kv_dtype: F32 (io F32 only),
- * F16 or FP8_E4M3 (needs key_scales / value_scales).  head_dim 64, 128 or
- * 256; num_heads / num_kv_heads in 1..8.
+ * F16 or FP8_E4M3 (needs key_scales / value_scales).  Any group size
+ * num_heads / num_kv_heads, head_dim 1..1024 and block_size >= 1 (the
+ * reference kernel's domain); pointers aligned to their element size.  head_dim
+ * 64/128/256 with groups up to 8, power-of-two blocks and 16-byte-aligned
+ * caches run on the tuned kernels, everything else on a generic one.
  *
  * Long contexts are split into partitions of partition_size tokens that are
  * reduced by a second kernel; that needs vkv_paged_decode_workspace_size()

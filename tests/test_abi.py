@@ -95,6 +95,8 @@ def test_append_argument_errors(vkv):
     assert lib.vkv_reshape_and_cache(ctypes.byref(p), None) == -1  # fp8 needs scales
     p = vkv.AppendParams(**{**base, "src_dtype": 1, "cache_dtype": 0})
     assert lib.vkv_reshape_and_cache(ctypes.byref(p), None) == -3
+    p = vkv.AppendParams(**{**base, "key": 17})
+    assert lib.vkv_reshape_and_cache(ctypes.byref(p), None) == -5  # not fp16-aligned
     p = vkv.AppendParams(**{**base, "num_tokens": 0})
     assert lib.vkv_reshape_and_cache(ctypes.byref(p), None) == 0
 

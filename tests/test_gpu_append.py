@@ -240,3 +240,52 @@ def test_append_fp8_non_finite_inputs(vkv, oracle, cuda):
     assert np.array_equal(to_np(vc), vc_ref)
     assert np.array_equal(to_np(ks).view(np.uint32), ks_ref.view(np.uint32))
     assert np.array_equal(to_np(vs).view(np.uint32), vs_ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("src,cache,Hkv,D,bs,stride_pad", [
+    (np.float32, np.float32, 3, 98, 12, 0),    # 1176-byte rows: the element kernel
+    (np.float16, np.float16, 8, 33, 5, 0),     # odd head_dim and block size
+    (np.float32, np.float16, 2, 80, 16, 1),    # a source stride of one extra element (misaligned rows)
+    (np.float16, "fp8", 2, 96, 16, 0),         # FP8 at head_dim 96 (6 sixteen-element pieces)
+    (np.float32, "fp8", 4, 100, 8, 0),
+    (np.float16, "fp8", 1, 1024, 4, 0),        # FP8, the largest decode head_dim
+])
+def test_append_any_shape_bitexact(vkv, oracle, cuda, src, cache, Hkv, D, bs, stride_pad):
+    """Rows that are not whole 16-byte pieces (or FP8 heads that are not a power
+    of two of 16-element pieces) take the element kernel: the same bytes, codes
+    and scales as the oracle."""
+    import torch
+    rng = np.random.default_rng(D * 11 + Hkv + bs)
+    N, T = 30, 47
+    slots = rng.permutation(N * bs)[:T].astype(np.int32)
+    slots[5] = -1
+    row = Hkv * D + stride_pad
+    base = (rng.standard_normal((T, row), dtype=np.float32) * 0.9)
+    base[rng.random(base.shape) < 0.01] *= 8
+    k_all = base.astype(src)
+    v_all = (base[:, ::-1] * 0.5).astype(src)
+    k = np.ascontiguousarray(k_all[:, :Hkv * D].reshape(T, Hkv, D))
+    v = np.ascontiguousarray(v_all[:, :Hkv * D].reshape(T, Hkv, D))
+    bits = (lambda a: a.view(np.uint16)) if src == np.float16 else (lambda a: a)
+    fp8 = cache == "fp8"
+    cdt = np.uint8 if fp8 else cache
+    kc_ref = np.zeros((N, bs, Hkv, D), cdt)
+    vc_ref = np.zeros_like(kc_ref)
+    ks_ref = np.zeros((N, bs, Hkv), np.float32) if fp8 else None
+    vs_ref = np.zeros_like(ks_ref) if fp8 else None
+    cbits = (lambda a: a.view(np.uint16)) if cdt == np.float16 else (lambda a: a)
+    oracle.reshape_and_cache(bits(k), bits(v), cbits(kc_ref), cbits(vc_ref), slots, ks_ref, vs_ref)
+    tdt = {np.float16: torch.float16, np.float32: torch.float32, np.uint8: torch.uint8}[cdt]
+    kc = torch.zeros((N, bs, Hkv, D), dtype=tdt, device=cuda)
+    vc = torch.zeros_like(kc)
+    ks = torch.zeros((N, bs, Hkv), dtype=torch.float32, device=cuda) if fp8 else None
+    vs = torch.zeros_like(ks) if fp8 else None
+    tk = to_dev(np.ascontiguousarray(k_all), cuda)[:, :Hkv * D].view(T, Hkv, D)
+    tv = to_dev(np.ascontiguousarray(v_all), cuda)[:, :Hkv * D].view(T, Hkv, D)
+    vkv.reshape_and_cache(tk, tv, kc, vc, to_dev(slots, cuda), ks, vs)
+    torch.cuda.synchronize()
+    assert np.array_equal(to_np(kc).view(np.uint8), kc_ref.view(np.uint8))
+    assert np.array_equal(to_np(vc).view(np.uint8), vc_ref.view(np.uint8))
+    if fp8:
+        assert np.array_equal(to_np(ks).view(np.uint32), ks_ref.view(np.uint32))
+        assert np.array_equal(to_np(vs).view(np.uint32), vs_ref.view(np.uint32))

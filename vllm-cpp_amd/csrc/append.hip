@@ -192,6 +192,56 @@ __global__ __launch_bounds__(256) void append_fp8_kernel(AppendArgs a) {
     }
 }
 
+// Any head_dim, any alignment (the reference's append is a per-token memcpy of
+// any row, src/layers/attention.cpp:93-101): one wave per (token, kv head),
+// lanes stride over head_dim one element at a time.  Same conversion (fp32 ->
+// fp16 RNE) and FP8 rule (wave amax, scale = amax / 448, exact quotient,
+// software e4m3fn encoder) as the vector kernels, so results are identical.
+template <typename SRC, int DST>
+__global__ __launch_bounds__(256) void append_elems_kernel(AppendArgs a, int head_dim) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t wave = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) / kWave;
+    const int64_t waves = int64_t(gridDim.x) * blockDim.x / kWave;
+    const int64_t pairs = a.total;  // (token, kv head) pairs
+    for (int64_t i = wave; i < pairs; i += waves) {
+        const int64_t t = i / a.num_kv_heads;
+        const int head = int(i - t * a.num_kv_heads);
+        const int64_t slot = a.slot_mapping[t];
+        if (slot < 0 || slot >= a.num_slots) continue;
+        const SRC* src[2] = {reinterpret_cast<const SRC*>(a.key + t * a.key_stride_bytes) + int64_t(head) * head_dim,
+                             reinterpret_cast<const SRC*>(a.value + t * a.value_stride_bytes) +
+                                 int64_t(head) * head_dim};
+        char* dst[2] = {a.key_cache + slot * a.row_bytes, a.value_cache + slot * a.row_bytes};
+        if constexpr (DST == kFp8) {
+            float amax[2] = {0.0f, 0.0f};
+            for (int d = lane; d < head_dim; d += kWave)
+#pragma unroll
+                for (int kv = 0; kv < 2; ++kv) amax[kv] = fmaxf(amax[kv], fabsf(static_cast<float>(src[kv][d])));
+#pragma unroll
+            for (int kv = 0; kv < 2; ++kv) {
+                const float scale = fp8_scale_from_amax(group_max<kWave>(amax[kv]));
+                const float rinv = 1.0f / scale;
+                uint8_t* out = reinterpret_cast<uint8_t*>(dst[kv]) + int64_t(head) * head_dim;
+                for (int d = lane; d < head_dim; d += kWave)
+                    out[d] = uint8_t(f32_to_fp8_sat(quotient(static_cast<float>(src[kv][d]), scale, rinv)));
+                if (lane == 0) (kv ? a.value_scales : a.key_scales)[slot * a.num_kv_heads + head] = scale;
+            }
+        } else {
+#pragma unroll
+            for (int kv = 0; kv < 2; ++kv) {
+                for (int d = lane; d < head_dim; d += kWave) {
+                    if constexpr (DST == kF16)
+                        reinterpret_cast<uint16_t*>(dst[kv])[int64_t(head) * head_dim + d] =
+                            sizeof(SRC) == 2 ? reinterpret_cast<const uint16_t*>(src[kv])[d]
+                                             : f32_to_f16_bits(static_cast<float>(src[kv][d]));
+                    else
+                        reinterpret_cast<float*>(dst[kv])[int64_t(head) * head_dim + d] = static_cast<float>(src[kv][d]);
+                }
+            }
+        }
+    }
+}
+
 int grid_for(int64_t total) {
     int64_t blocks = (total + 255) / 256;
     const int64_t cap = int64_t(256) * 64;  // 64 workgroups per CU, then grid-stride
@@ -233,8 +283,36 @@ int launch_append(const vkv_append_params* p, hipStream_t st) {
     a.row_bytes = row * dst_eb;
     a.num_slots = int64_t(p->num_blocks) * p->block_size;
     a.num_kv_heads = p->num_kv_heads;
+    // The vector kernels move 16-byte pieces of whole rows (FP8: 16 elements
+    // per lane, a power-of-two number of lanes per head); anything else takes
+    // the element kernel.
+    const uintptr_t bits = reinterpret_cast<uintptr_t>(p->key) | reinterpret_cast<uintptr_t>(p->value) |
+                           uintptr_t(a.key_stride_bytes) | uintptr_t(a.value_stride_bytes) |
+                           reinterpret_cast<uintptr_t>(p->key_cache) | reinterpret_cast<uintptr_t>(p->value_cache);
+    const int lpt = p->head_dim / 16;
+    const bool vector_rows = (bits & 15u) == 0 && (a.row_bytes % 16) == 0 &&
+                             (p->cache_dtype != VKV_DTYPE_FP8_E4M3 ||
+                              (p->head_dim % 16 == 0 && lpt <= 16 && (lpt & (lpt - 1)) == 0));
+    if (!vector_rows) {
+        a.total = int64_t(p->num_tokens) * p->num_kv_heads;
+        const int g = grid_for(a.total * kWave);
+        const int D = p->head_dim;
+        if (p->src_dtype == VKV_DTYPE_F32) {
+            switch (p->cache_dtype) {
+                case VKV_DTYPE_F32: hipLaunchKernelGGL((append_elems_kernel<float, kF32>), dim3(g), dim3(256), 0, st, a, D); break;
+                case VKV_DTYPE_F16: hipLaunchKernelGGL((append_elems_kernel<float, kF16>), dim3(g), dim3(256), 0, st, a, D); break;
+                default: hipLaunchKernelGGL((append_elems_kernel<float, kFp8>), dim3(g), dim3(256), 0, st, a, D); break;
+            }
+        } else {
+            switch (p->cache_dtype) {
+                case VKV_DTYPE_F16: hipLaunchKernelGGL((append_elems_kernel<_Float16, kF16>), dim3(g), dim3(256), 0, st, a, D); break;
+                case VKV_DTYPE_FP8_E4M3: hipLaunchKernelGGL((append_elems_kernel<_Float16, kFp8>), dim3(g), dim3(256), 0, st, a, D); break;
+                default: return -1;
+            }
+        }
+        return 0;
+    }
     if (p->cache_dtype == VKV_DTYPE_FP8_E4M3) {
-        const int lpt = p->head_dim / 16;
         a.chunks_per_row = 0;
         a.total = int64_t(p->num_tokens) * p->num_kv_heads * lpt;
         if (p->src_dtype == VKV_DTYPE_F32) return launch_fp8<float>(a, lpt, st);

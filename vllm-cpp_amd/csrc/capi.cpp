@@ -183,26 +183,21 @@ int check_append(const vkv_append_params* p) {
     const int64_t ks = p->key_stride ? p->key_stride : row;
     const int64_t vs = p->value_stride ? p->value_stride : row;
     if (ks < row || vs < row) return fail(VKV_ERR_SHAPE, "token stride smaller than num_kv_heads*head_dim");
-    const uintptr_t src_bits = reinterpret_cast<uintptr_t>(p->key) | reinterpret_cast<uintptr_t>(p->value) |
-                               uintptr_t(ks * src_eb) | uintptr_t(vs * src_eb);
-    const uintptr_t dst_bits = reinterpret_cast<uintptr_t>(p->key_cache) | reinterpret_cast<uintptr_t>(p->value_cache);
-    if ((src_bits | dst_bits) & 15u)
-        return fail(VKV_ERR_ALIGN, "key/value/caches and token strides must be 16-byte aligned");
+    const int dst_eb = p->cache_dtype == VKV_DTYPE_F32 ? 4 : (p->cache_dtype == VKV_DTYPE_F16 ? 2 : 1);
+    if ((reinterpret_cast<uintptr_t>(p->key) | reinterpret_cast<uintptr_t>(p->value)) & uintptr_t(src_eb - 1))
+        return fail(VKV_ERR_ALIGN, "key/value misaligned for their dtype");
+    if ((reinterpret_cast<uintptr_t>(p->key_cache) | reinterpret_cast<uintptr_t>(p->value_cache)) &
+        uintptr_t(dst_eb - 1))
+        return fail(VKV_ERR_ALIGN, "caches misaligned for their dtype");
     switch (p->cache_dtype) {
         case VKV_DTYPE_F32:
             if (p->src_dtype != VKV_DTYPE_F32) return fail(VKV_ERR_UNSUPPORTED, "fp32 cache needs fp32 source");
-            if ((row * 4) % 16) return fail(VKV_ERR_ALIGN, "row bytes must be a multiple of 16");
             break;
         case VKV_DTYPE_F16:
-            if ((row * 2) % 16) return fail(VKV_ERR_ALIGN, "row bytes must be a multiple of 16");
             break;
-        case VKV_DTYPE_FP8_E4M3: {
+        case VKV_DTYPE_FP8_E4M3:
             if (!p->key_scales || !p->value_scales) return fail(VKV_ERR_NULL, "FP8 cache needs scale arrays");
-            const int lpt = p->head_dim / 16;
-            if (p->head_dim % 16 || !is_pow2(lpt) || lpt > 16)
-                return fail(VKV_ERR_UNSUPPORTED, "FP8 append needs head_dim in {16,32,64,128,256}");
             break;
-        }
         default:
             return fail(VKV_ERR_UNSUPPORTED, "cache_dtype %d unsupported", p->cache_dtype);
     }
