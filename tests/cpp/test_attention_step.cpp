@@ -16,6 +16,7 @@
 #include <cmath>
 #include <cstdint>
 #include <cstring>
+#include <deque>
 #include <random>
 #include <vector>
 
@@ -23,6 +24,7 @@
 #include "kv_oracle.h"
 #include "vllm/attention/attention_step.hpp"
 #include "vllm/core/block_manager.hpp"
+#include "vllm/core/swap_preemption.hpp"
 #include "vllm/memory/kv_cache.hpp"
 #include "vllm/utils/hip_utils.hpp"
 
@@ -303,7 +305,96 @@ void run_fork_swap_scenario(const Geometry& g, uint32_t seed) {
     (void)hipHostFree(host);
 }
 
+// The reference's preemption pressure test (tests/unit/test_scheduler.cpp:47-89)
+// with swap instead of recompute: a 3-block pool of 16-token blocks; A's
+// 16-token prompt takes one block and its first decode a second; B's 16-token
+// prompt takes the last one; when A reaches 32 tokens and needs a third block
+// the victim is the last running sequence other than A, which is B; B is
+// swapped out (not freed) and requeued, A grows to 3 blocks and decodes; when
+// A finishes B is swapped back in, its blocks' bytes equal those it had before
+// (every layer, K and V), and it decodes on.  Attention is checked against the
+// oracle at every step.
+void run_swap_preemption_scenario(const Geometry& g, uint32_t seed) {
+    Harness h(g, seed, 3);
+    CHECK_EQ(h.bm.num_total_gpu_blocks(), 3u);
+    const size_t hbb = h.cache.host_block_bytes();
+    void* host = nullptr;
+    VLLM_HIP_CHECK(hipHostMalloc(&host, hbb * 3, hipHostMallocDefault));
+    vllm::SwapPreemption swap(h.bm, h.cache, host);
+    vllm::SwappableSequence a, b;
+    a.seq_id = 1;
+    b.seq_id = 2;
+    std::vector<vllm::SwappableSequence*> running;
+    std::deque<vllm::SwappableSequence*> waiting;
+
+    a.block_table = h.bm.allocate_for_sequence(16);  // the prompt: one block
+    running.push_back(&a);
+    h.step({&a.block_table}, {0}, {16}, "prefill A");
+    CHECK(h.bm.ensure_sequence_capacity(a.block_table, 17));
+    CHECK_EQ(a.block_table.size(), 2u);
+    h.step({&a.block_table}, {16}, {1}, "decode A");
+
+    b.block_table = h.bm.allocate_for_sequence(16);
+    CHECK_EQ(b.block_table.size(), 1u);
+    running.push_back(&b);
+    h.step({&b.block_table}, {0}, {16}, "prefill B");
+    CHECK_EQ(h.bm.num_free_gpu_blocks(), 0u);
+    h.step({&a.block_table}, {17}, {15}, "A runs to 32 tokens");
+
+    // A needs a third block for position 33: preempt (scheduler.cpp:107-118)
+    const int32_t b_gpu = b.block_table[0];
+    const size_t be = h.block_elems() * eb(g.kv);
+    std::vector<std::vector<uint8_t>> b_k(g.L), b_v(g.L);
+    for (int l = 0; l < g.L; ++l) {
+        b_k[l].resize(be);
+        b_v[l].resize(be);
+        VLLM_HIP_CHECK(hipMemcpy(b_k[l].data(), h.cache.k_ptr(size_t(l), size_t(b_gpu)), be, hipMemcpyDeviceToHost));
+        VLLM_HIP_CHECK(hipMemcpy(b_v[l].data(), h.cache.v_ptr(size_t(l), size_t(b_gpu)), be, hipMemcpyDeviceToHost));
+    }
+    CHECK(!h.bm.ensure_sequence_capacity(a.block_table, 33));
+    CHECK_EQ(vllm::SwapPreemption::pick_victim(running, &a), 1);
+    CHECK(swap.preempt_one(running, waiting, &a, nullptr));
+    CHECK(h.bm.ensure_sequence_capacity(a.block_table, 33));
+    CHECK_EQ(a.block_table.size(), 3u);
+    CHECK(b.swapped_out);
+    CHECK_EQ(b.block_table.size(), 1u);  // now a CPU block id
+    CHECK_EQ(waiting.size(), 1u);
+    CHECK_EQ(running.size(), 1u);
+    CHECK(running[0] == &a);
+    CHECK(!swap.preempt_one(running, waiting, &a, nullptr));  // A alone: no victim
+    h.step({&a.block_table}, {32}, {1}, "decode A in the third block");  // may overwrite B's old block
+
+    // A finishes; B is re-admitted by swap-in, not replay
+    h.bm.free_sequence(a.block_table);
+    a.block_table.clear();
+    a.finished = true;
+    running.clear();
+    CHECK(swap.swap_in(b, nullptr));
+    waiting.pop_front();
+    running.push_back(&b);
+    CHECK(!b.swapped_out);
+    VLLM_HIP_CHECK(hipDeviceSynchronize());
+    const int32_t b_new = b.block_table[0];
+    for (int l = 0; l < g.L; ++l) {
+        std::vector<uint8_t> k(be), v(be);
+        VLLM_HIP_CHECK(hipMemcpy(k.data(), h.cache.k_ptr(size_t(l), size_t(b_new)), be, hipMemcpyDeviceToHost));
+        VLLM_HIP_CHECK(hipMemcpy(v.data(), h.cache.v_ptr(size_t(l), size_t(b_new)), be, hipMemcpyDeviceToHost));
+        CHECK(k == b_k[l]);
+        CHECK(v == b_v[l]);
+        std::memcpy(h.hk[l].data() + size_t(b_new) * be, b_k[l].data(), be);  // the oracle's mirror follows
+        std::memcpy(h.hv[l].data() + size_t(b_new) * be, b_v[l].data(), be);
+    }
+    CHECK(h.bm.ensure_sequence_capacity(b.block_table, 17));
+    CHECK_EQ(b.block_table.size(), 2u);
+    h.step({&b.block_table}, {16}, {1}, "decode B after swap-in");
+    (void)hipHostFree(host);
+}
+
 }  // namespace
+
+TEST_CASE(preemption_by_swap_reference_pressure_test) {
+    run_swap_preemption_scenario({2, 3, 16, 14, 2, 64, vllm::KVDtype::kF16, vllm::KVDtype::kF16}, 6);
+}
 
 TEST_CASE(attention_step_f16_qwen05b_shape) {
     run_scenario({2, 48, 16, 14, 2, 64, vllm::KVDtype::kF16, vllm::KVDtype::kF16}, 1);
