@@ -731,8 +731,6 @@ __global__ __launch_bounds__(DT ? DT : 1024) void decode_reduce_kernel(DecodeArg
     // The partition kernel has finished (same stream): return its claim
     // counters to zero for the next call.
     if (s == 0 && h == 0 && d < kClaimSequences) a.counters[d * kCounterStride] = 0;
-    // and the prefill kernel's, when it ran before in the same call
-    if (s == 0 && h == 0 && d == kClaimSequences) a.counters[kPrefillClaimSlot] = 0;
     const int D = DT ? DT : a.head_dim;
     if (DT == 0 && d >= D) return;
     const int G = a.num_heads / a.num_kv_heads;
@@ -1111,17 +1109,19 @@ int launch_prefill(const vkv_prefill_params* p, const DecodePlan& plan, void* wo
     if (prefill_mfma_supported(p)) {
         // Mixed batch: the matrix-core kernel takes every sequence with two or
         // more query tokens, the decode kernels the single-token ones; each
-        // writes only its own output rows.  All on the caller's stream: the
-        // decode kernels on a side stream forked from it and joined back were
-        // slower (C3's mixed call 339 us against 319 us, its prefill rows
-        // alone 127 us against 105 us; the cross-queue waits cost more than
-        // the overlap saves, as neither kernel's waves fit beside the other's
-        // on a CU).
+        // writes only its own output rows.  All on the caller's stream, one
+        // after the other: the decode kernels on a side stream forked from it
+        // and joined back were slower (C3's mixed call 339 us against 319 us,
+        // its prefill rows alone 127 us against 105 us), and so was giving the
+        // prefill kernel 64-192 of the 256 CUs with the decode rows beside it
+        // on a side stream (333-348 us against 324 us): neither kernel's waves
+        // fit beside the other's on a CU, and the decode rows need nearly every
+        // CU to keep enough bytes in flight.
         const size_t items_off = plan.workspace_bytes - prefill_items_bytes(p);
+        const vkv_decode_params d = prefill_as_decode(p, true);
         const int rc = launch_prefill_mfma(p, static_cast<char*>(workspace) + items_off,
                                            static_cast<int32_t*>(workspace) + kPrefillClaimSlot, st);
         if (rc) return rc;
-        const vkv_decode_params d = prefill_as_decode(p, true);
         return launch_rows(&d, plan, workspace, nullptr, nullptr, p->query_start_loc, st);
     }
     // Every query row decoded like a sequence of a decode call, each with its

@@ -47,12 +47,12 @@ int launch_prefill(const vkv_prefill_params* p, const DecodePlan& plan, void* wo
 vkv_decode_params prefill_as_decode(const vkv_prefill_params* p, bool per_sequence);
 bool prefill_mfma_supported(const vkv_prefill_params* p);
 size_t prefill_items_bytes(const vkv_prefill_params* p);
-// inline_claim: a zeroed int the merge kernel of the same call resets (the
-// fp16 kernel's claim counter when it builds its own work list), or nullptr.
+// inline_claim: two zeroed ints (the fp16 kernel's claim and done counters
+// when it builds its own work list; the kernel leaves them zero), or nullptr.
 int launch_prefill_mfma(const vkv_prefill_params* p, void* item_space, int32_t* inline_claim, hipStream_t st);
 // Decode workspace header ints (the claim counters use 0, 32, 64, ...).
 constexpr int kChosenPartitionSlot = 1;  // partition size the partition kernel chose
-constexpr int kPrefillClaimSlot = 2;     // claim counter of the fp16 prefill kernel's in-kernel list
+constexpr int kPrefillClaimSlot = 2;     // claim and done counters (ints 2, 3) of the fp16 prefill kernel's list
 
 struct PlaneSet {
     char* base[4];

@@ -78,7 +78,8 @@ struct PrefillArgs {
     float scale_log2;
     // fp16 kernel, calls of at most kInlineBlocks row blocks: every workgroup
     // orders the blocks itself (no list kernel); inline_claim is the claim
-    // counter (zero at entry, reset by the merge kernel that follows)
+    // counter and inline_claim[1] counts the workgroups that are done (both
+    // zero at entry; the last workgroup out returns them to zero)
     int32_t inline_list;
     int32_t* inline_claim;
     int32_t rows_per_item;
@@ -993,6 +994,13 @@ __device__ __forceinline__ void wide_items(const PrefillArgs& a, const WideBuffe
         }
         prefill_block_wide<D, FP8>(a, item.x, item.y / a.num_kv_heads, item.y % a.num_kv_heads, buf);
         if (threadIdx.x == 0) claimed = atomicAdd(claim, 1);
+    }
+    // Every claim of this workgroup has returned (its value decided the exit);
+    // the last workgroup to arrive here resets the inline counters for the
+    // next call.  (The list kernel zeroes its counters itself.)
+    if (a.inline_list && threadIdx.x == 0 && atomicAdd(a.inline_claim + 1, 1) == int(gridDim.x) - 1) {
+        a.inline_claim[0] = 0;
+        a.inline_claim[1] = 0;
     }
 }
 
