@@ -747,7 +747,7 @@ def suite_c4(dev, steps, warmup):
     b = torch.from_numpy(free).long().to(dev)
     swap_exact = all(torch.equal(pl[l][b], pl[l][a]) for pl in planes for l in range(L))
     swap_bytes = nsw * hb
-    beside = _decode_beside_swap(dev, planes, host, nsw, out_pairs, swap_bytes)
+    beside = _decode_beside_swap(dev, planes, host, nsw, out_pairs, in_pairs, swap_bytes)
     from oracle import oracle
     Ls, Ps = 4, 256
     sub_ids = np.unique(np.concatenate([cfg.copy_pairs[:Ps, 0], cfg.copy_pairs[:Ps, 1]]))
@@ -771,11 +771,10 @@ def suite_c4(dev, steps, warmup):
                              "sample": f"oracle copy_blocks of {Ps} pairs x {Ls} layers x K,V, {reps} calls"}}
 
 
-def _decode_beside_swap(dev, planes, host, nsw, out_pairs, swap_bytes, reps=40):
-    """C2's decode on the default stream alone, then while a swap-out of the C4
-    blocks runs on a side stream: decode us per call both ways, and the swap's
-    rate while the decodes run (HIP events on each stream)."""
-    import numpy as np
+def _decode_beside_swap(dev, planes, host, nsw, out_pairs, in_pairs, swap_bytes, reps=40):
+    """C2's decode on the default stream alone, then while a swap of the C4
+    blocks runs on a side stream (out, then in): decode us per call each way,
+    and each swap's rate while the decodes run (HIP events on each stream)."""
     import torch
     import vllm_kv_amd as vkv
     from vllm_kv_amd import workloads
@@ -798,25 +797,26 @@ def _decode_beside_swap(dev, planes, host, nsw, out_pairs, swap_bytes, reps=40):
     for _ in range(5):
         decode()
     torch.cuda.synchronize()
-    solo = _events_ms(decode, reps, main)[0]
-    s0 = torch.cuda.Event(enable_timing=True)
-    s1 = torch.cuda.Event(enable_timing=True)
-    d0 = torch.cuda.Event(enable_timing=True)
-    d1 = torch.cuda.Event(enable_timing=True)
-    s0.record(side)
-    vkv.swap_blocks(planes, host, nsw, out_pairs, 0, stream=side)
-    s1.record(side)
-    d0.record(main)
-    for _ in range(reps):
-        decode()
-    d1.record(main)
-    torch.cuda.synchronize()
-    busy = d0.elapsed_time(d1) / reps
-    swap_ms = s0.elapsed_time(s1)
-    return {"decode_us_alone": round(solo * 1e3, 2), "decode_us_beside_swap": round(busy * 1e3, 2),
-            "decodes_inside_swap": bool(d1.elapsed_time(s1) > 0),
-            "swap_out_gbs_beside_decode": round(swap_bytes / (swap_ms * 1e-3) / 1e9, 1),
-            "workload": f"C2 decode x {reps} on the default stream; swap-out of {nsw} C4 blocks on a side stream"}
+    res = {"decode_us_alone": round(_events_ms(decode, reps, main)[0] * 1e3, 2)}
+    for name, pairs, direction in (("out", out_pairs, 0), ("in", in_pairs, 1)):
+        s0 = torch.cuda.Event(enable_timing=True)
+        s1 = torch.cuda.Event(enable_timing=True)
+        d0 = torch.cuda.Event(enable_timing=True)
+        d1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        s0.record(side)
+        vkv.swap_blocks(planes, host, nsw, pairs, direction, stream=side)
+        s1.record(side)
+        d0.record(main)
+        for _ in range(reps):
+            decode()
+        d1.record(main)
+        torch.cuda.synchronize()
+        res[f"decode_us_beside_swap_{name}"] = round(d0.elapsed_time(d1) / reps * 1e3, 2)
+        res[f"decodes_inside_swap_{name}"] = bool(d1.elapsed_time(s1) > 0)
+        res[f"swap_{name}_gbs_beside_decode"] = round(swap_bytes / (s0.elapsed_time(s1) * 1e-3) / 1e9, 1)
+    res["workload"] = f"C2 decode x {reps} on the default stream; swap of {nsw} C4 blocks on a side stream"
+    return res
 
 
 SUITES = {"stream": suite_stream, "c1": suite_c1, "append": suite_append, "rope": suite_rope, "step": suite_step,

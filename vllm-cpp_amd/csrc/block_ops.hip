@@ -151,20 +151,24 @@ int grid_for_units(int64_t units, int64_t cap) {
 // 256-CU part).
 constexpr int64_t kCopyWorkgroups = int64_t(256) * 16;
 
-// Swap: bound by the host link (~55 GB/s), which a few workgroups with 16 KiB
-// in flight each keep busy; the rest of the chip stays free for the decode
-// that a side-stream swap runs beside.  VKV_SWAP_WORKGROUPS overrides it
-// (tuning).
-#ifndef VKV_SWAP_WORKGROUPS_DEFAULT
-#define VKV_SWAP_WORKGROUPS_DEFAULT 64
-#endif
-int64_t swap_workgroups() {
+// Swap: bound by the host link (~55 GB/s), which a few workgroups keep busy;
+// the rest of the chip stays free for the decode a side-stream swap runs
+// beside.  Writes to host memory (out) reach 49 GB/s with 8 workgroups, with
+// C2's decode beside them 6 % slower; reads of host memory (in) wait longer
+// per request and need more in flight (8: 19 GB/s, 16: 38 GB/s, 24-32:
+// 54-57 GB/s).  More workgroups than these slow a decode beside the swap far
+// more than they speed the swap (16 writing workgroups: decode 1.6x slower).
+// VKV_SWAP_WORKGROUPS overrides both (tuning).
+constexpr int64_t kSwapOutWorkgroups = 8;
+constexpr int64_t kSwapInWorkgroups = 24;
+int64_t swap_workgroups(int32_t direction) {
     static const int64_t v = [] {
         const char* e = std::getenv("VKV_SWAP_WORKGROUPS");
         const long n = e ? std::atol(e) : 0;
-        return n > 0 ? int64_t(n) : int64_t(VKV_SWAP_WORKGROUPS_DEFAULT);
+        return n > 0 ? int64_t(n) : int64_t(0);
     }();
-    return v;
+    if (v > 0) return v;
+    return direction == 0 ? kSwapOutWorkgroups : kSwapInWorkgroups;
 }
 
 }  // namespace
@@ -189,7 +193,7 @@ int launch_swap_blocks(const PlaneSet& planes, int32_t num_layers, int32_t num_d
     a.num_host_blocks = num_host_blocks;
     a.direction = direction;
     if (a.total_units == 0) return 0;
-    hipLaunchKernelGGL(swap_blocks_kernel, dim3(grid_for_units(a.total_units, swap_workgroups())), dim3(kThreads), 0,
+    hipLaunchKernelGGL(swap_blocks_kernel, dim3(grid_for_units(a.total_units, swap_workgroups(direction))), dim3(kThreads), 0,
                        st, a);
     return 0;
 }
