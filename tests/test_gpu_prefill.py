@@ -71,6 +71,9 @@ def _threads():
     # groups 5 and 6: 256-row work items end inside a token's heads
     (10, 2, 128, 16, [77, 1, 300, 52], [3, 40, 129, 0]),
     (24, 4, 64, 32, [129, 7, 1, 250], [600, 0, 33, 64]),
+    # groups above 8 (a token brings G rows to a work item): 16 and 32
+    (32, 2, 128, 16, [300, 1, 40], [100, 50, 0]),
+    (32, 1, 64, 16, [200, 2], [30, 0]),
 ])
 def test_prefill_vs_oracle(vkv, oracle, cuda, kvt, H, Hkv, D, bs, q_lens, prior):
     import torch
@@ -413,3 +416,36 @@ def test_prefill_max_context_len_clamp(vkv, oracle, cuda, io):
                       to_dev(qsl, cuda), max(q_lens), scale, max_context_len=max_ctx)
     torch.cuda.synchronize()
     assert_close(to_np(out).astype(np.float32), ref, *tol, f"prefill clamped to {max_ctx} keys ({io})")
+
+
+def test_prefill_group16_list_kernel(vkv, oracle, cuda):
+    """Group 16 in a call large enough for the separate list kernel (more than
+    512 row blocks): each sequence brings ceil(q G / 256) row blocks per kv
+    head, twice what one per 32 query tokens would allow, and the work list
+    must hold them all.  Every row of three sequences against the oracle."""
+    import torch
+    from vllm_kv_amd import workloads
+    rng = np.random.default_rng(29)
+    H, Hkv, D, bs, S, qn_ = 16, 1, 128, 16, 24, 360
+    q_lens = np.full(S, qn_, np.int32)
+    prior = rng.integers(0, 200, S).astype(np.int32)
+    ctx = prior + q_lens
+    lay = workloads.make_layout(ctx, bs, rng, slack=0.1)
+    qsl = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    Tq = int(qsl[-1])
+    assert Tq * (H // Hkv) // 256 > 512  # the list-kernel path
+    k, v = workloads.fill_pool_numpy(rng, lay.num_blocks, bs, Hkv, D, 0.5)
+    q = (rng.standard_normal((Tq, H, D), dtype=np.float32) * 0.5).astype(np.float16)
+    scale = float(1.0 / np.sqrt(np.float32(D)))
+    out = torch.zeros((Tq, H, D), dtype=torch.float16, device=cuda)
+    vkv.paged_prefill(out, to_dev(q, cuda), to_dev(k, cuda), to_dev(v, cuda), to_dev(lay.block_tables, cuda),
+                      to_dev(ctx, cuda), to_dev(qsl, cuda), qn_, scale)
+    torch.cuda.synchronize()
+    got = to_np(out).astype(np.float32)
+    seqs = [0, 11, S - 1]
+    rows = np.concatenate([np.arange(qsl[s], qsl[s + 1]) for s in seqs])
+    sub_qsl = np.concatenate([[0], np.cumsum([qsl[s + 1] - qsl[s] for s in seqs])]).astype(np.int32)
+    ref = oracle.paged_prefill(q[rows].astype(np.float32), k.view(np.uint16), v.view(np.uint16),
+                               np.ascontiguousarray(lay.block_tables[seqs]), np.ascontiguousarray(ctx[seqs]), sub_qsl,
+                               scale, nthreads=_threads())
+    assert_close(got[rows], ref, F16_ATOL, F16_RTOL, "group-16 prefill through the list kernel")

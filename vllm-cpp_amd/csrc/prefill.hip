@@ -1141,9 +1141,28 @@ bool prefill_mfma_supported(const vkv_prefill_params* p) {
            p->num_heads / p->num_kv_heads <= kMaxHeadGroups * kMaxWaves;
 }
 
+namespace {
+
+// fp16 caches and FP8 caches at D = 128 run on the direct-load kernels, whose
+// items are Wide<D>::ROWS (token, head) rows; FP8 at D = 64 on
+// prefill_mfma_kernel, whose items are kBQ query tokens (of every head).
+bool wide_path(const vkv_prefill_params* p) { return p->kv_dtype == VKV_DTYPE_F16 || p->head_dim == 128; }
+int rows_per_item(const vkv_prefill_params* p) {
+    if (!wide_path(p)) return kBQ;
+    return p->head_dim == 128 ? Wide<128>::ROWS : Wide<64>::ROWS;
+}
+// Row blocks (work items per kv head) of a sequence, at most: with a group of
+// G heads a token brings G rows to the direct-load kernels.
+int64_t max_row_blocks(const vkv_prefill_params* p) {
+    const int64_t row_mult = wide_path(p) ? p->num_heads / p->num_kv_heads : 1;
+    const int rows = rows_per_item(p);
+    return (int64_t(p->max_query_len) * row_mult + rows - 1) / rows;
+}
+
+}  // namespace
+
 size_t prefill_items_bytes(const vkv_prefill_params* p) {
-    const int64_t qblocks = (p->max_query_len + kBQ - 1) / kBQ;
-    return 256 + size_t(int64_t(p->num_seqs) * qblocks * p->num_kv_heads) * sizeof(int2);
+    return 256 + size_t(int64_t(p->num_seqs) * max_row_blocks(p) * p->num_kv_heads) * sizeof(int2);
 }
 
 int launch_prefill_mfma(const vkv_prefill_params* p, void* item_space, int32_t* inline_claim, hipStream_t st) {
@@ -1164,7 +1183,7 @@ int launch_prefill_mfma(const vkv_prefill_params* p, void* item_space, int32_t* 
     // fp16 caches and FP8 caches at D = 128: prefill_wide_kernel /
     // prefill_wide8_kernel, Wide<D>::ROWS (token, head) rows per item; FP8 at
     // D = 64: prefill_mfma_kernel, up to kMaxWaves heads x kBQ tokens per item
-    const bool wide = p->kv_dtype == VKV_DTYPE_F16 || p->head_dim == 128;
+    const bool wide = wide_path(p);
     const int head_groups = wide ? 1 : (a.group + kMaxWaves - 1) / kMaxWaves;
     a.heads_per_wg = (a.group + head_groups - 1) / head_groups;
     a.bs_log2 = ilog2i(p->block_size);
@@ -1175,8 +1194,8 @@ int launch_prefill_mfma(const vkv_prefill_params* p, void* item_space, int32_t* 
     if (p->max_context_len > 0 && p->max_context_len < tt) tt = p->max_context_len;
     a.table_tokens = int32_t(tt > 0x7FFFFFFF ? 0x7FFFFFFF : tt);
     const int row_mult = wide ? a.group : 1;
-    const int rows_per_item = wide ? (p->head_dim == 128 ? Wide<128>::ROWS : Wide<64>::ROWS) : kBQ;
-    a.qblocks = int((int64_t(p->max_query_len) * row_mult + rows_per_item - 1) / rows_per_item);
+    const int rpi = rows_per_item(p);
+    a.qblocks = int(max_row_blocks(p));
     a.num_seqs = p->num_seqs;
     a.scale_log2 = p->scale * 1.4426950408889634f;
     int32_t* count = static_cast<int32_t*>(item_space);
@@ -1186,19 +1205,19 @@ int launch_prefill_mfma(const vkv_prefill_params* p, void* item_space, int32_t* 
     // bins: every possible tile count (items past kMaxLevels - 1 tiles share the last)
     const int64_t max_tiles = (int64_t(a.table_tokens) + kBK - 1) / kBK;
     const int nbins = int(max_tiles + 1 < kMaxLevels ? max_tiles + 1 : kMaxLevels);
-    a.rows_per_item = rows_per_item;
+    a.rows_per_item = rpi;
     a.nbins = nbins;
     // Row blocks, at most: a sequence of q >= 2 tokens has ceil(q G / R) <=
     // q G / R + 1 of them, and there are at most min(S, T / 2) such sequences
     // (T query tokens).  Small calls order them in the kernel itself.
     const int64_t T = p->num_query_tokens;
     const int64_t nseq2 = p->num_seqs < T / 2 ? p->num_seqs : T / 2;
-    const int64_t bound = T * row_mult / rows_per_item + nseq2;
+    const int64_t bound = T * row_mult / rpi + nseq2;
     a.inline_list = wide && inline_claim != nullptr && bound <= kInlineBlocks;
     a.inline_claim = inline_claim;
     if (!a.inline_list)
         hipLaunchKernelGGL(prefill_items_kernel, dim3(1), dim3(256), 0, st, p->query_start_loc, p->context_lens,
-                           p->num_seqs, p->num_kv_heads, row_mult, rows_per_item, a.qblocks, a.table_tokens, nbins,
+                           p->num_seqs, p->num_kv_heads, row_mult, rpi, a.qblocks, a.table_tokens, nbins,
                            items, count);
     // Persistent grid, never more workgroups than there can be items: one per
     // CU for the wide kernel (its LDS and registers fill a CU); two per CU for
