@@ -56,6 +56,8 @@ class AttentionMetadata {
     int32_t num_seqs() const { return num_seqs_; }
     int32_t num_tokens() const { return num_tokens_; }
     int32_t max_query_len() const { return max_query_len_; }
+    // sequences with exactly one new token (decode rows of a mixed step)
+    int32_t single_token_seqs() const { return single_token_seqs_; }
     int32_t max_blocks_per_seq() const { return max_blocks_per_seq_; }
     int32_t block_size() const { return block_size_; }
 
@@ -74,7 +76,7 @@ class AttentionMetadata {
     bool pending_[2] = {false, false};
     int cur_ = 0;
     int32_t* dev_ = nullptr;
-    int32_t num_seqs_ = 0, num_tokens_ = 0, max_query_len_ = 0;
+    int32_t num_seqs_ = 0, num_tokens_ = 0, max_query_len_ = 0, single_token_seqs_ = 0;
 };
 
 // Attention of one layer for a whole step.  q/out: [num_tokens][num_heads][head_dim],

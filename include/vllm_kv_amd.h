@@ -272,7 +272,12 @@ int vkv_paged_decode_noalloc(const vkv_decode_params* p, vkv_stream_t stream);
  * q_len 1 ones through split-K decode; other combinations decode every row
  * with its causal context.  max_context_len > 0 clamps every row's key count
  * as decode does (the reference's max_context_len, paged_attention.cu:20);
- * 0 leaves only the table clamp.  Workspace: as for decode, a caller buffer of
+ * 0 leaves only the table clamp.  multi_token_only = 1 is the caller's
+ * promise that no sequence has exactly one query token (known on the host,
+ * e.g. a step of prompt chunks only): the split-K decode pass that serves
+ * such sequences (two kernels) is then not launched, and a sequence of one
+ * query token would get no output row; 0 (the default) launches it, and it
+ * finds the single-token sequences on the device.  Workspace: as for decode, a caller buffer of
  * vkv_paged_prefill_workspace_size() bytes (first 1024 bytes zeroed before
  * its first use) or, with workspace == NULL, the library's buffer of the
  * stream.
@@ -301,6 +306,7 @@ typedef struct vkv_prefill_params {
     int32_t io_dtype;
     int32_t kv_dtype;
     int32_t max_context_len;    /* > 0: clamp of every row's keys; 0: none */
+    int32_t multi_token_only;   /* 1: no sequence has q_len 1 (see above); 0: not known */
     void* workspace;            /* optional, see above */
     size_t workspace_bytes;
 } vkv_prefill_params;

@@ -25,7 +25,7 @@ def test_library_exports_every_declared_symbol(vkv):
     lib = vkv.load()
     for name in declared_functions():
         assert hasattr(lib, name), name
-    assert lib.vkv_abi_version() == 2
+    assert lib.vkv_abi_version() == 3
 
 
 def test_struct_sizes_match_header_layout(vkv):
@@ -34,8 +34,9 @@ def test_struct_sizes_match_header_layout(vkv):
     assert ctypes.sizeof(vkv.DecodeParams) == 8 * 8 + 8 + 14 * 4 + 8 + 8
     assert ctypes.sizeof(vkv.BlockPlane) == 24
     assert ctypes.sizeof(vkv.RopeAppendParams) == 3 * 8 + 3 * 8 + 2 * 8 + 2 * 4 + 5 * 8 + 8 * 4
-    # 9 pointers, query_stride, 13 int32/float (padded to 8), workspace pointer and size
-    assert ctypes.sizeof(vkv.PrefillParams) == 9 * 8 + 8 + 13 * 4 + 4 + 8 + 8
+    # 9 pointers, query_stride, 14 int32/float, workspace pointer and size
+    assert ctypes.sizeof(vkv.PrefillParams) == 9 * 8 + 8 + 14 * 4 + 8 + 8
+    assert vkv.PrefillParams.multi_token_only.offset == 132
     assert vkv.PrefillParams.workspace.offset == 136
 
 
@@ -184,6 +185,7 @@ def test_prefill_argument_errors_and_workspace(vkv):
     assert lib.vkv_paged_prefill(ctypes.byref(_prefill_params(vkv, query_start_loc=0)), None) == -1
     assert lib.vkv_paged_prefill(ctypes.byref(_prefill_params(vkv, max_query_len=0)), None) == -2
     assert lib.vkv_paged_prefill(ctypes.byref(_prefill_params(vkv, max_context_len=-1)), None) == -2
+    assert lib.vkv_paged_prefill(ctypes.byref(_prefill_params(vkv, multi_token_only=2)), None) == -2
     assert lib.vkv_paged_prefill(ctypes.byref(_prefill_params(vkv, num_query_tokens=0)), None) == 0
     need = lib.vkv_paged_prefill_workspace_size(ctypes.byref(_prefill_params(vkv)))
     # at least the 1 KiB header and the partials of the 3 sequences' decode rows

@@ -449,3 +449,35 @@ def test_prefill_group16_list_kernel(vkv, oracle, cuda):
                                np.ascontiguousarray(lay.block_tables[seqs]), np.ascontiguousarray(ctx[seqs]), sub_qsl,
                                scale, nthreads=_threads())
     assert_close(got[rows], ref, F16_ATOL, F16_RTOL, "group-16 prefill through the list kernel")
+
+
+@pytest.mark.parametrize("kvt", ["f16", "fp8"])
+def test_prefill_multi_token_only(vkv, oracle, cuda, kvt):
+    """multi_token_only = 1 (no sequence has one query token) skips the decode
+    pass: on such a batch the output equals the default call's bit for bit and
+    the oracle's; a mixed call on the same workspace afterwards is still right
+    (the skipped pass leaves no counter behind)."""
+    import torch
+    H, Hkv, D, bs = 28, 4, 128, 16
+    lay, ctx, qsl, q, k, v, scale = _case(H, Hkv, D, bs, [40, 3, 77, 2], [100, 0, 513, 31], 200)
+    (kc, vc, ks, vs), (hk, hv, hks, hvs) = _cache(vkv, cuda, kvt, k, v)
+    args = (to_dev(q, cuda), kc, vc, to_dev(lay.block_tables, cuda), to_dev(ctx, cuda), to_dev(qsl, cuda), 77, scale)
+    out_a = torch.full((q.shape[0], H, D), float("nan"), dtype=torch.float16, device=cuda)
+    out_b = torch.full_like(out_a, float("nan"))
+    vkv.paged_prefill(out_a, *args, key_scales=ks, value_scales=vs)
+    vkv.paged_prefill(out_b, *args, key_scales=ks, value_scales=vs, multi_token_only=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out_a.view(torch.int16), out_b.view(torch.int16))
+    ref = oracle.paged_prefill(q.astype(np.float32), hk, hv, lay.block_tables, ctx, qsl, scale,
+                               key_scales=hks, value_scales=hvs, nthreads=_threads())
+    assert_close(to_np(out_b).astype(np.float32), ref, F16_ATOL, F16_RTOL, f"multi-token-only prefill ({kvt})")
+    # then a mixed call (single-token sequences among them) on the same library workspace
+    lay2, ctx2, qsl2, q2, k2, v2, _ = _case(H, Hkv, D, bs, [1, 30, 1, 1], [300, 7, 0, 900], 200)
+    (kc2, vc2, ks2, vs2), (hk2, hv2, hks2, hvs2) = _cache(vkv, cuda, kvt, k2, v2)
+    out_c = torch.full((q2.shape[0], H, D), float("nan"), dtype=torch.float16, device=cuda)
+    vkv.paged_prefill(out_c, to_dev(q2, cuda), kc2, vc2, to_dev(lay2.block_tables, cuda), to_dev(ctx2, cuda),
+                      to_dev(qsl2, cuda), 30, scale, key_scales=ks2, value_scales=vs2)
+    torch.cuda.synchronize()
+    ref2 = oracle.paged_prefill(q2.astype(np.float32), hk2, hv2, lay2.block_tables, ctx2, qsl2, scale,
+                                key_scales=hks2, value_scales=hvs2, nthreads=_threads())
+    assert_close(to_np(out_c).astype(np.float32), ref2, F16_ATOL, F16_RTOL, f"mixed prefill after ({kvt})")

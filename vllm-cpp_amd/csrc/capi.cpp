@@ -161,6 +161,8 @@ int check_prefill(const vkv_prefill_params* p) {
     if (!p->query_start_loc) return fail(VKV_ERR_NULL, "query_start_loc is NULL");
     if (p->max_query_len < 1) return fail(VKV_ERR_SHAPE, "max_query_len must be >= 1");
     if (p->max_context_len < 0) return fail(VKV_ERR_SHAPE, "max_context_len < 0");
+    if (p->multi_token_only != 0 && p->multi_token_only != 1)
+        return fail(VKV_ERR_SHAPE, "multi_token_only must be 0 or 1");
     // Shape/dtype rules are those of decode; the decode rows are the
     // sequences (mixed matrix-core path) or the query tokens (row path).
     const vkv_decode_params d = vkv::prefill_as_decode(p, vkv::prefill_mfma_supported(p));
@@ -286,7 +288,7 @@ extern "C" {
 
 const char* vkv_last_error(void) { return g_last_error; }
 
-int vkv_abi_version(void) { return 2; }
+int vkv_abi_version(void) { return 3; }
 
 int vkv_reshape_and_cache(const vkv_append_params* p, vkv_stream_t stream) {
     int rc = check_append(p);

@@ -1121,7 +1121,9 @@ int launch_prefill(const vkv_prefill_params* p, const DecodePlan& plan, void* wo
         const vkv_decode_params d = prefill_as_decode(p, true);
         const int rc = launch_prefill_mfma(p, static_cast<char*>(workspace) + items_off,
                                            static_cast<int32_t*>(workspace) + kPrefillClaimSlot, st);
-        if (rc) return rc;
+        // (the caller's promise of no single-token sequence spares the decode
+        // pass: its kernels cost ~9 us even when they find no row)
+        if (rc || p->multi_token_only) return rc;
         return launch_rows(&d, plan, workspace, nullptr, nullptr, p->query_start_loc, st);
     }
     // Every query row decoded like a sequence of a decode call, each with its

@@ -76,7 +76,7 @@ void AttentionMetadata::build(const std::vector<StepSequence>& seqs, hipStream_t
     int32_t* tables = h + off_tables_;
     int32_t* context = h + off_context_;
     int32_t* qsl = h + off_qsl_;
-    int32_t t = 0, max_q = 0;
+    int32_t t = 0, max_q = 0, singles = 0;
     qsl[0] = 0;
     for (int32_t s = 0; s < S; ++s) {
         const StepSequence& q = seqs[size_t(s)];
@@ -96,6 +96,7 @@ void AttentionMetadata::build(const std::vector<StepSequence>& seqs, hipStream_t
         context[s] = q.context_len + q.num_new_tokens;
         qsl[s + 1] = t;
         max_q = std::max(max_q, q.num_new_tokens);
+        singles += q.num_new_tokens == 1 ? 1 : 0;
     }
     // One copy of the whole image (unused tails included: one transfer beats several).
     VLLM_HIP_CHECK(hipMemcpyAsync(dev_, h, words_ * sizeof(int32_t), hipMemcpyHostToDevice, stream));
@@ -105,6 +106,7 @@ void AttentionMetadata::build(const std::vector<StepSequence>& seqs, hipStream_t
     num_seqs_ = S;
     num_tokens_ = t;
     max_query_len_ = max_q;
+    single_token_seqs_ = singles;
 }
 
 PagedAttentionLayer::PagedAttentionLayer(int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
@@ -187,8 +189,8 @@ void PagedAttentionLayer::forward(void* out, void* q, void* k, const void* v, KV
         d.accumulate = 0;  // the reference zeroes, then adds (:128-129)
         VLLM_KV_CHECK(vkv_paged_decode(&d, st));
     } else {
-        // Prefill contexts stay within max_context_len by the scheduler's
-        // capacity checks; the reference clamps decode contexts the same way.
+        // Every row's keys are clamped as in decode (the reference's
+        // max_context_len); a step without decode rows skips their pass.
         vkv_prefill_params p{};
         p.output = out;
         p.query = q;
@@ -211,6 +213,8 @@ void PagedAttentionLayer::forward(void* out, void* q, void* k, const void* v, KV
         p.scale = scale;
         p.io_dtype = int32_t(io_dtype);
         p.kv_dtype = int32_t(cache.dtype());
+        p.max_context_len = max_ctx;
+        p.multi_token_only = md.single_token_seqs() == 0 ? 1 : 0;
         VLLM_KV_CHECK(vkv_paged_prefill(&p, st));
     }
 }

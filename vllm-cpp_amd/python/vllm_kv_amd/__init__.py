@@ -109,7 +109,7 @@ class PrefillParams(ctypes.Structure):
         ("block_size", ctypes.c_int32), ("max_blocks_per_seq", ctypes.c_int32),
         ("num_blocks", ctypes.c_int32), ("scale", ctypes.c_float),
         ("io_dtype", ctypes.c_int32), ("kv_dtype", ctypes.c_int32),
-        ("max_context_len", ctypes.c_int32),
+        ("max_context_len", ctypes.c_int32), ("multi_token_only", ctypes.c_int32),
         ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
     ]
 
@@ -334,7 +334,7 @@ def decode_workspace_size(out, query, key_cache, value_cache, block_tables, cont
 
 def prefill_params(out, query, key_cache, value_cache, block_tables, context_lens, query_start_loc,
                    max_query_len, scale, key_scales=None, value_scales=None, max_context_len=0,
-                   workspace=None) -> PrefillParams:
+                   workspace=None, multi_token_only=False) -> PrefillParams:
     Tq, H, D = out.shape
     N, bs, Hkv, _ = key_cache.shape
     return PrefillParams(
@@ -346,19 +346,22 @@ def prefill_params(out, query, key_cache, value_cache, block_tables, context_len
         num_heads=H, num_kv_heads=Hkv, head_dim=D, block_size=bs,
         max_blocks_per_seq=block_tables.shape[1], num_blocks=N, scale=scale,
         io_dtype=_dtype_code(out), kv_dtype=_dtype_code(key_cache), max_context_len=max_context_len,
-        workspace=_ptr(workspace),
+        multi_token_only=1 if multi_token_only else 0, workspace=_ptr(workspace),
         workspace_bytes=0 if workspace is None else workspace.numel() * workspace.element_size())
 
 
 def paged_prefill(out, query, key_cache, value_cache, block_tables, context_lens, query_start_loc,
                   max_query_len, scale, key_scales=None, value_scales=None, max_context_len=0,
-                  workspace=None, stream=None) -> None:
+                  workspace=None, stream=None, multi_token_only=False) -> None:
     """out/query [Tq, H, D]; query_start_loc int32 [S+1]; context_lens counts the step's tokens.
-    max_context_len > 0 clamps every row's keys; workspace (optional) as for paged_decode."""
+    max_context_len > 0 clamps every row's keys; workspace (optional) as for paged_decode;
+    multi_token_only: the caller's promise that no sequence has exactly one query token
+    (skips the decode pass that serves those)."""
     _require_cuda(out, query, key_cache, value_cache, block_tables, context_lens, query_start_loc,
                   key_scales, value_scales, workspace)
     p = prefill_params(out, query, key_cache, value_cache, block_tables, context_lens, query_start_loc,
-                       max_query_len, scale, key_scales, value_scales, max_context_len, workspace)
+                       max_query_len, scale, key_scales, value_scales, max_context_len, workspace,
+                       multi_token_only)
     check(load().vkv_paged_prefill(ctypes.byref(p), _stream(stream)))
 
 
