@@ -124,7 +124,9 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=10)
+    # ~0.2 s of untimed steps: an idle GPU's clocks take that long to rise
+    # (C2 decode measured 103.9 us after 10 warmup steps, 103.0 us after 2000)
+    ap.add_argument("--warmup", type=int, default=2000)
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle timing")
     ap.add_argument("--partition-size", type=int, default=0,
                     help="decode split-K partition in tokens (0: the library's default)")
@@ -248,6 +250,21 @@ def main():
 # --suite: the other rows of the path, one JSON line each (not the headline).
 
 
+def _warm(fn, warmup, min_ms=200.0):
+    """`warmup` untimed calls, then more until min_ms of wall time has passed:
+    an idle GPU's clocks take a while to rise, and a short kernel timed right
+    away runs slow."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < min_ms:
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
+
+
 def _events_ms(fn, n, stream, groups=5):
     """Median, p10 and p90 over `groups` samples of the mean time of n
     back-to-back calls (HIP events on the launch stream), in ms."""
@@ -323,9 +340,7 @@ def suite_c3(dev, steps, warmup):
     def attn():
         vkv.paged_prefill(out, q, kc, vc, bt, cl, qsl, mql, cfg.scale, stream=stream)
 
-    for _ in range(warmup):
-        append()
-        attn()
+    _warm(lambda: (append(), attn()), warmup)
     torch.cuda.synchronize()
     t_app = _events_ms(append, steps, stream)
     t_att = _events_ms(attn, steps, stream)
@@ -368,11 +383,10 @@ def suite_c3_prefill_only(dev, steps, warmup):
     stream = torch.cuda.current_stream()
 
     def attn():
-        vkv.paged_prefill(out, q, kc, vc, bt, cl, qsl, int(ql.max()), cfg.scale, stream=stream)
+        vkv.paged_prefill(out, q, kc, vc, bt, cl, qsl, int(ql.max()), cfg.scale, stream=stream,
+                          multi_token_only=True)
 
-    for _ in range(warmup):
-        attn()
-    torch.cuda.synchronize()
+    _warm(attn, warmup)
     t = _events_ms(attn, steps, stream)
     keys = sum(int(cfg.prior_lens[s]) * int(ql[s]) + int(ql[s]) * (int(ql[s]) + 1) // 2 for s in range(npf))
     flops = 4.0 * D * H * keys
@@ -387,11 +401,9 @@ def suite_c3_prefill_only(dev, steps, warmup):
 
     def attn8():
         vkv.paged_prefill(out, q, k8, v8, bt, cl, qsl, int(ql.max()), cfg.scale, key_scales=ks8, value_scales=vs8,
-                          stream=stream)
+                          stream=stream, multi_token_only=True)
 
-    for _ in range(warmup):
-        attn8()
-    torch.cuda.synchronize()
+    _warm(attn8, warmup)
     t8 = _events_ms(attn8, steps, stream)
     tf8 = flops / (t8[0] * 1e-3) / 1e12
     # CPU: the oracle's prefill (one decode per query row, as the reference) of sequence 0
@@ -408,7 +420,8 @@ def suite_c3_prefill_only(dev, steps, warmup):
                                           cfg.scale, nthreads=thr)
     sec, reps = _cpu_time(fn_cpu)
     keys0 = int(cfg.prior_lens[0]) * int(ql[0]) + int(ql[0]) * (int(ql[0]) + 1) // 2
-    return {"row": "C3 prefill sequences alone", "workload": "the 8 x 512-token chunks of C3 (prior U[0,2048])",
+    return {"row": "C3 prefill sequences alone", "workload": "the 8 x 512-token chunks of C3 (prior U[0,2048]), "
+                                                          "one vkv_paged_prefill call with multi_token_only = 1",
             "us_median": round(t[0] * 1e3, 2), "us_p10_p90": [round(t[1] * 1e3, 2), round(t[2] * 1e3, 2)],
             "gflop": round(flops / 1e9, 2), "tflops": round(tf, 1),
             "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": 2500.0, "unit": "TFLOP/s",
@@ -446,9 +459,7 @@ def suite_c1(dev, steps, warmup):
         vkv.reshape_and_cache(nk, nv, kc, vc, slots, stream=stream)
         vkv.paged_decode(out, q, kc, vc, bt, cl, cfg.scale, stream=stream)
 
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
+    _warm(step, warmup)
     t = _events_ms(step, steps, stream)
     kvb = cfg.kv_bytes(2)
     from oracle import oracle
@@ -509,9 +520,7 @@ def suite_c5(dev, steps, warmup):
     def decode():
         vkv.paged_decode(out, q, kc, vc, bt, cl, cfg.scale, key_scales=ks, value_scales=vs, stream=stream)
 
-    for _ in range(warmup):
-        append()
-        decode()
+    _warm(lambda: (append(), decode()), warmup)
     torch.cuda.synchronize()
     ta = _events_ms(append, steps, stream)
     td = _events_ms(decode, steps, stream)
@@ -576,9 +585,7 @@ def suite_append(dev, steps, warmup):
             def fn():
                 vkv.reshape_and_cache(k, v, kc, vc, perm, ks, vs, stream=stream)
 
-            for _ in range(warmup):
-                fn()
-            torch.cuda.synchronize()
+            _warm(fn, warmup)
             t = _events_ms(fn, steps, stream)
             nbytes = T * Hkv * D * 2 * 2 + wbytes + T * 4
             gbs = nbytes / (t[0] * 1e-3) / 1e9
@@ -651,9 +658,7 @@ def suite_rope(dev, steps, warmup):
                 vkv.rope_reshape_and_cache(q, k, None, cs, positions=pos, stream=stream)
                 vkv.reshape_and_cache(k, v, kc, vc, perm, ks, vs, stream=stream)
 
-            for _ in range(warmup):
-                fused()
-                unfused()
+            _warm(lambda: (fused(), unfused()), warmup)
             torch.cuda.synchronize()
             tf = _events_ms(fused, steps, stream)
             tu = _events_ms(unfused, steps, stream)
@@ -694,8 +699,7 @@ def suite_stream(dev, steps, warmup):
     src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
     stream = torch.cuda.current_stream()
-    for _ in range(warmup):
-        dst.copy_(src)
+    _warm(lambda: dst.copy_(src), warmup)
     t = _events_ms(lambda: dst.copy_(src), steps, stream)
     gbs = 2 * (1 << 30) / (t[0] * 1e-3) / 1e9
     return {"row": "copy ceiling", "workload": "torch copy_ of 1 GiB on the device", "us_median": round(t[0] * 1e3, 1),
