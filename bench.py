@@ -462,6 +462,24 @@ def suite_c1(dev, steps, warmup):
     _warm(step, warmup)
     t = _events_ms(step, steps, stream)
     kvb = cfg.kv_bytes(2)
+    # The same step captured once in a HIP graph and replayed (the launch-bound
+    # case graphs are for): the capture stream's library workspace is sized by
+    # an eager call on it first (a workspace cannot grow under capture).
+    ref_out = out.clone()
+    cs = torch.cuda.Stream()
+    cs.wait_stream(stream)
+    with torch.cuda.stream(cs):
+        vkv.reshape_and_cache(nk, nv, kc, vc, slots, stream=cs)
+        vkv.paged_decode(out, q, kc, vc, bt, cl, cfg.scale, stream=cs)
+    cs.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=cs):
+        vkv.reshape_and_cache(nk, nv, kc, vc, slots, stream=cs)
+        vkv.paged_decode(out, q, kc, vc, bt, cl, cfg.scale, stream=cs)
+    out.fill_(float("nan"))
+    _warm(graph.replay, warmup)
+    tg = _events_ms(graph.replay, steps, stream)
+    graph_equal = bool(torch.equal(out.view(torch.int16), ref_out.view(torch.int16)))
     from oracle import oracle
     hk, hv = kc.cpu().numpy().view(np.uint16), vc.cpu().numpy().view(np.uint16)
     hnk, hnv = nk.cpu().numpy().view(np.uint16), nv.cpu().numpy().view(np.uint16)
@@ -477,6 +495,7 @@ def suite_c1(dev, steps, warmup):
             "kv_bytes": kvb, "step_us_median": round(t[0] * 1e3, 2),
             "step_us_p10_p90": [round(t[1] * 1e3, 2), round(t[2] * 1e3, 2)],
             "note": "launch-bound: three kernels (append, partition, merge) for 0.6 MB of KV",
+            "graph_step_us_median": round(tg[0] * 1e3, 2), "graph_output_equals_eager": graph_equal,
             "cpu_baseline": {"us_per_step": round(sec * 1e6, 1), "cores": 1, "kind": "port",
                              "sample": f"oracle append + decode of the whole step, {reps} steps"}}
 
