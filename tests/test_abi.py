@@ -25,7 +25,7 @@ def test_library_exports_every_declared_symbol(vkv):
     lib = vkv.load()
     for name in declared_functions():
         assert hasattr(lib, name), name
-    assert lib.vkv_abi_version() == 3
+    assert lib.vkv_abi_version() == vkv.ABI_VERSION == 3
 
 
 def test_struct_sizes_match_header_layout(vkv):

@@ -21,6 +21,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 PKG_ROOT = os.path.dirname(os.path.dirname(_HERE))          # vllm-cpp_amd/
 LIB_PATH = os.path.join(PKG_ROOT, "lib", "libvllm_kv_amd.so")
 
+ABI_VERSION = 3  # vkv_abi_version() of the library this binding's structs match
 DTYPE_F32, DTYPE_F16, DTYPE_FP8 = 0, 1, 2
 SWAP_OUT, SWAP_IN = 0, 1
 
@@ -140,6 +141,9 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib = ctypes.CDLL(path)
     lib.vkv_last_error.restype = ctypes.c_char_p
     lib.vkv_abi_version.restype = ctypes.c_int
+    if lib.vkv_abi_version() != ABI_VERSION:
+        raise RuntimeError(f"{path} has ABI version {lib.vkv_abi_version()}, this binding's structs are "
+                           f"version {ABI_VERSION}: rebuild it (make -C vllm-cpp_amd)")
     for name, ptype in (("vkv_reshape_and_cache", AppendParams), ("vkv_paged_decode", DecodeParams),
                         ("vkv_paged_decode_noalloc", DecodeParams),
                         ("vkv_paged_prefill", PrefillParams),
