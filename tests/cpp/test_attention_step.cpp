@@ -139,6 +139,7 @@ struct Harness {
         const int T = qsl.back();
         md.build(ss, nullptr);
         CHECK_EQ(md.num_tokens(), T);
+        CHECK_EQ(md.single_token_seqs(), int32_t(std::count(nnew.begin(), nnew.end(), 1)));
         CHECK_EQ(md.max_query_len(), *std::max_element(nnew.begin(), nnew.end()));
         std::vector<int32_t> slots(T), pos(T), cl(S);
         for (int s = 0, t = 0; s < S; ++s) {
@@ -221,7 +222,10 @@ void run_scenario(const Geometry& g, uint32_t seed) {
         CHECK(!tables[s].empty());
     }
     std::vector<std::vector<int32_t>*> tp = {&tables[0], &tables[1], &tables[2], &tables[3]};
-    const std::vector<std::vector<int>> steps = {{5, 33, 1, 18}, {1, 1, 1, 1}, {1, 1, 1, 1}, {1, 7, 1, 1}};
+    // prompts (one of them a single token), decodes, a step where every
+    // sequence has >= 2 new tokens (the prefill call then skips its decode
+    // pass), a mixed step
+    const std::vector<std::vector<int>> steps = {{5, 33, 1, 18}, {1, 1, 1, 1}, {3, 2, 2, 4}, {1, 1, 1, 1}, {1, 7, 1, 1}};
     for (size_t st = 0; st < steps.size(); ++st) {
         for (int s = 0; s < 4; ++s) CHECK(h.bm.ensure_sequence_capacity(tables[s], size_t(ctx[s] + steps[st][s])));
         h.step(tp, ctx, steps[st], "step");
