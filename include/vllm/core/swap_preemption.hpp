@@ -38,7 +38,8 @@ class SwapPreemption {
     // host_pool: hipHostMalloc memory of at least
     // bm.num_total_cpu_blocks() * cache.host_block_bytes() bytes, holding CPU
     // block c at c * host_block_bytes().  Allocates a small device buffer for
-    // the pair lists (one per instance).
+    // the pair lists and a pinned host buffer they are uploaded from (one each
+    // per instance).
     SwapPreemption(BlockManager& bm, KVCache& cache, void* host_pool);
     ~SwapPreemption();
     SwapPreemption(const SwapPreemption&) = delete;
@@ -67,6 +68,11 @@ class SwapPreemption {
     void* host_pool_;
     int32_t* dev_pairs_ = nullptr;  // capacity: 2 * max(GPU blocks, CPU blocks) ids
     size_t dev_pairs_cap_ = 0;
+    // Pinned staging of the pair list: the upload is asynchronous, so the
+    // buffer is rewritten only after the previous upload's event completed.
+    int32_t* host_pairs_ = nullptr;
+    hipEvent_t uploaded_ = nullptr;
+    bool upload_pending_ = false;
 };
 
 }  // namespace vllm

@@ -14,9 +14,16 @@ SwapPreemption::SwapPreemption(BlockManager& bm, KVCache& cache, void* host_pool
     if (!host_pool) throw std::invalid_argument("SwapPreemption needs a host pool");
     dev_pairs_cap_ = 2 * std::max<size_t>(std::max(bm.num_total_gpu_blocks(), bm.num_total_cpu_blocks()), 1);
     VLLM_HIP_CHECK(hipMalloc(&dev_pairs_, dev_pairs_cap_ * sizeof(int32_t)));
+    VLLM_HIP_CHECK(hipHostMalloc(reinterpret_cast<void**>(&host_pairs_), dev_pairs_cap_ * sizeof(int32_t)));
+    VLLM_HIP_CHECK(hipEventCreateWithFlags(&uploaded_, hipEventDisableTiming));
 }
 
-SwapPreemption::~SwapPreemption() { (void)hipFree(dev_pairs_); }
+SwapPreemption::~SwapPreemption() {
+    if (upload_pending_) (void)hipEventSynchronize(uploaded_);
+    (void)hipEventDestroy(uploaded_);
+    (void)hipHostFree(host_pairs_);
+    (void)hipFree(dev_pairs_);
+}
 
 int SwapPreemption::pick_victim(const std::vector<SwappableSequence*>& running, const SwappableSequence* except) {
     for (size_t i = running.size(); i > 0; --i) {
@@ -30,10 +37,15 @@ int SwapPreemption::pick_victim(const std::vector<SwappableSequence*>& running, 
 void SwapPreemption::enqueue_swap(const std::vector<int32_t>& pairs, int32_t direction, hipStream_t stream) {
     const size_t n = pairs.size() / 2;
     if (n == 0) return;
-    // The copy from pageable memory is staged before hipMemcpyAsync returns;
-    // the swap kernel after it on the same stream reads the uploaded list.
+    if (pairs.size() > dev_pairs_cap_) throw std::length_error("SwapPreemption: more pairs than the pool has blocks");
+    // The pinned staging buffer may still feed the previous upload.
+    if (upload_pending_) VLLM_HIP_CHECK(hipEventSynchronize(uploaded_));
+    std::copy(pairs.begin(), pairs.end(), host_pairs_);
     VLLM_HIP_CHECK(
-        hipMemcpyAsync(dev_pairs_, pairs.data(), pairs.size() * sizeof(int32_t), hipMemcpyHostToDevice, stream));
+        hipMemcpyAsync(dev_pairs_, host_pairs_, pairs.size() * sizeof(int32_t), hipMemcpyHostToDevice, stream));
+    VLLM_HIP_CHECK(hipEventRecord(uploaded_, stream));
+    upload_pending_ = true;
+    // the swap kernel after the upload on the same stream reads the list
     cache_.swap_blocks(host_pool_, int32_t(bm_.num_total_cpu_blocks()), dev_pairs_, int32_t(n), direction, stream);
 }
 
