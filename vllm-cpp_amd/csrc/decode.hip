@@ -1031,7 +1031,7 @@ int launch_rows(const vkv_decode_params* p, const DecodePlan& plan, void* worksp
         int64_t item_wgs = (max_items + kWavesPerBlock - 1) / kWavesPerBlock;
         if (item_wgs > (int64_t(1) << 30)) item_wgs = int64_t(1) << 30;
         const int grid_x = int(item_wgs < 1 ? 1 : item_wgs);
-        const size_t lds = (size_t(n) + 1) * sizeof(int);
+        const size_t lds = (size_t(n) + 1) * sizeof(int) + lpt_lds_bytes(n);
         int rc;
         if (!fixed) {
             rc = launch_decode_generic(c, p->kv_dtype, int64_t(n) * plan.max_parts, lds, st);

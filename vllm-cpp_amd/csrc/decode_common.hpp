@@ -202,6 +202,22 @@ __device__ inline int choose_partition(const DecodeArgs& a, const int (&cnt)[kMa
     return (items0 <= W || items0 > 2 * W) ? a.P : best;
 }
 
+// Longest-first order of the pairs of a call whose items take more than one
+// round of the resident waves (rows <= kLptMaxRows, so that the host's LDS
+// holds the lists below): waves that finish claim the next items, and with
+// the rows' short final partitions spread through a row-major list the last
+// round ends with long items started late while other waves sit idle (C5's
+// batch ran 5 % below the bandwidth of the same batch with every context a
+// multiple of the partition).  So the full partitions of every row come
+// first (row-major), then each row's short final partition, longest first,
+// in kLptBins length classes (rows in order within a class).  Every
+// workgroup derives the same order from the context lengths.
+constexpr int kLptMaxRows = 512;
+constexpr int kLptBins = 64;
+// Extra dynamic LDS of a launch of n rows for that order (the row prefix of
+// (n + 1) ints comes first).
+inline size_t lpt_lds_bytes(int n) { return n <= kLptMaxRows ? size_t(2) * size_t(n) * sizeof(int) : 0; }
+
 // The item loop of the persistent partition kernels.  Items are numbered
 // densely, pair-major: pair = (row, partition), items_per_pair items each
 // (kv heads, or kv heads x query-head chunks), so no wave is launched for a
@@ -281,6 +297,89 @@ __device__ __forceinline__ void run_partitions(const DecodeArgs& a, const int it
     const int num_pairs = prefix[nrows];
     const int num_items = num_pairs * items_per_pair;
 
+    // Longest-first order (above).  prefix becomes the exclusive prefix of the
+    // rows' full partitions (the last one counts when it is full); the short
+    // final partitions follow in shortlist, their row's partition index being
+    // its full count.
+    const bool lpt = nrows <= kLptMaxRows && num_items > a.wave_slots;
+    int num_full = 0;
+    int* shortlist = prefix + (nrows + 1);  // [nrows]: rows of the short final partitions, longest first
+    int* bins = shortlist + nrows;          // [nrows]: length class of a row's short final partition, -1 none
+    if (lpt) {
+        int full_r[kLptMaxRows / 256 + 1];  // this thread's rows r = tid + 256 j
+#pragma unroll
+        for (int j = 0; j * 256 < kLptMaxRows; ++j) {
+            const int r = int(threadIdx.x) + 256 * j;
+            full_r[j] = 0;
+            if (r < nrows) {
+                const int np = prefix[r + 1] - prefix[r];
+                const int ctx = np > 0 ? row_context(a, r) : 0;
+                const int last = ctx - (np - 1) * P;  // tokens of the final partition
+                const bool short_last = np > 0 && last < P;
+                full_r[j] = short_last ? np - 1 : np;
+                bins[r] = short_last ? int((int64_t(last) * kLptBins) / P) : -1;
+            }
+        }
+        __syncthreads();  // every thread has read the partition prefix
+        // the full counts into prefix (exclusive, by a block scan of the
+        // per-thread tiles of contiguous rows)
+        const int per2 = (nrows + int(blockDim.x) - 1) / int(blockDim.x);
+#pragma unroll
+        for (int j = 0; j * 256 < kLptMaxRows; ++j) {
+            const int r = int(threadIdx.x) + 256 * j;
+            if (r < nrows) shortlist[r] = full_r[j];  // (shortlist as scratch for the counts)
+        }
+        __syncthreads();
+        const int t0 = int(threadIdx.x) * per2;
+        int tile = 0;
+        for (int i = 0; i < per2; ++i)
+            if (t0 + i < nrows) tile += shortlist[t0 + i];
+        int incl = tile;
+#pragma unroll
+        for (int o = 1; o < kWave; o <<= 1) {
+            const int y = __shfl_up(incl, o, kWave);
+            if (lane >= o) incl += y;
+        }
+        if (lane == kWave - 1) wave_total[threadIdx.x / kWave] = incl;
+        __syncthreads();
+        int before = 0;
+        for (int w = 0; w < int(threadIdx.x) / kWave; ++w) before += wave_total[w];
+        int run = before + incl - tile;
+        for (int i = 0; i < per2; ++i) {
+            if (t0 + i < nrows) {
+                const int c = shortlist[t0 + i];
+                prefix[t0 + i] = run;
+                run += c;
+            }
+        }
+        if (threadIdx.x == blockDim.x - 1) prefix[nrows] = before + incl;
+        __syncthreads();  // prefix complete; the counts in shortlist are no longer needed
+        num_full = prefix[nrows];
+        // short final partitions by class, longest class first: thread t takes
+        // class kLptBins - 1 - t / 4 over the quarter t % 4 of the rows; the
+        // (class, quarter) counts in thread order give each its offset
+        const int cls = kLptBins - 1 - int(threadIdx.x) / 4;
+        const int qlen = (nrows + 3) / 4;
+        const int q0 = (int(threadIdx.x) & 3) * qlen;
+        const int q1 = q0 + qlen < nrows ? q0 + qlen : nrows;
+        int cnt = 0;
+        for (int r = q0; r < q1; ++r) cnt += bins[r] == cls ? 1 : 0;
+        int ci2 = cnt;
+#pragma unroll
+        for (int o = 1; o < kWave; o <<= 1) {
+            const int y = __shfl_up(ci2, o, kWave);
+            if (lane >= o) ci2 += y;
+        }
+        __syncthreads();  // every wave has read wave_total above
+        if (lane == kWave - 1) wave_total[threadIdx.x / kWave] = ci2;
+        __syncthreads();
+        int off = ci2 - cnt;
+        for (int w = 0; w < int(threadIdx.x) / kWave; ++w) off += wave_total[w];
+        for (int r = q0; r < q1; ++r)
+            if (bins[r] == cls) shortlist[off++] = r;
+        __syncthreads();
+    }
+
     // Item groups of 4 consecutive items go to a workgroup, one item per
     // wave.  Round 0 is static: workgroup b takes group b.  Later groups
     // g >= gridDim.x are dealt in 8 interleaved sequences g = gridDim.x + 8k +
@@ -300,13 +399,19 @@ __device__ __forceinline__ void run_partitions(const DecodeArgs& a, const int it
         if (it < num_items) {
             const int pair = it / items_per_pair;
             const int sub = it - pair * items_per_pair;
-            int lo = 0, hi = nrows - 1;  // row = last r with prefix[r] <= pair
-            while (lo < hi) {
-                const int mid = (lo + hi + 1) >> 1;
-                if (prefix[mid] <= pair) lo = mid;
-                else hi = mid - 1;
+            if (lpt && pair >= num_full) {
+                // a short final partition: its index is the row's full count
+                const int row = shortlist[pair - num_full];
+                item(P, row, prefix[row + 1] - prefix[row], sub);
+            } else {
+                int lo = 0, hi = nrows - 1;  // row = last r with prefix[r] <= pair
+                while (lo < hi) {
+                    const int mid = (lo + hi + 1) >> 1;
+                    if (prefix[mid] <= pair) lo = mid;
+                    else hi = mid - 1;
+                }
+                item(P, lo, pair - prefix[lo], sub);
             }
-            item(P, lo, pair - prefix[lo], sub);
         }
         if (g0 >= num_groups) break;  // the grid covers every group: nothing to claim
         __syncthreads();
