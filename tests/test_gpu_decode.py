@@ -604,3 +604,42 @@ def test_decode_config5_all_rows(vkv, oracle, cuda):
                               lay.context_lens, cfg.scale, key_scales=to_np(ks), value_scales=to_np(vs),
                               nthreads=_threads())
     assert_close(to_np(out).astype(np.float32), ref, F16_ATOL, F16_RTOL, "C5, all 256 sequences")
+
+
+@pytest.mark.parametrize("mix", ["mixed", "exact"])
+def test_decode_multi_round_claim_order(vkv, oracle, cuda, mix):
+    """A call whose items take several rounds of the resident waves, with at
+    most 512 rows, claims its items longest first: full partitions, then the
+    rows' short final partitions by length class.  480 sequences (H32/Hkv8/D128
+    fp16, bs16) whose contexts mix empty rows, exact multiples of the 768-token
+    partition (no short partition), single short partitions and long rows
+    ("mixed"), or are all exact multiples ("exact": no short partitions at all);
+    every sequence and head against the oracle."""
+    import torch
+    from vllm_kv_amd import workloads
+    rng = np.random.default_rng(77 if mix == "mixed" else 78)
+    S, H, Hkv, D, bs = 480, 32, 8, 128, 16
+    if mix == "mixed":
+        kind = rng.integers(0, 4, S)
+        ctx = np.where(kind == 0, 0,
+              np.where(kind == 1, 768 * rng.integers(1, 5, S),
+              np.where(kind == 2, rng.integers(1, 768, S), rng.integers(769, 4000, S)))).astype(np.int32)
+    else:
+        ctx = (768 * rng.integers(1, 4, S)).astype(np.int32)
+    lay = workloads.make_layout(ctx, bs, rng, slack=0.05)
+    N = lay.num_blocks
+    g = torch.Generator(device=cuda).manual_seed(5)
+    kc = (torch.randn((N, bs, Hkv, D), generator=g, device=cuda) * 0.5).half()
+    vc = (torch.randn((N, bs, Hkv, D), generator=g, device=cuda) * 0.5).half()
+    q = (torch.randn((S, H, D), generator=g, device=cuda) * 0.5).half()
+    scale = float(1.0 / np.sqrt(D))
+    out = torch.full((S, H, D), float("nan"), dtype=torch.float16, device=cuda)
+    vkv.paged_decode(out, q, kc, vc, to_dev(lay.block_tables, cuda), to_dev(ctx, cuda), scale)
+    torch.cuda.synchronize()
+    items = int(((ctx.astype(np.int64) + 767) // 768).sum()) * Hkv
+    assert items > 3 * 1024, "the call must take more than one round of resident waves"
+    ref = oracle.paged_decode(to_np(q).astype(np.float32), to_np(kc).view(np.uint16), to_np(vc).view(np.uint16),
+                              lay.block_tables, ctx, scale, nthreads=_threads())
+    got = to_np(out).astype(np.float32)
+    # (empty rows: zero, as the reference's zeroed output would hold)
+    assert_close(got, ref, F16_ATOL, F16_RTOL, f"multi-round claim order ({mix})")
