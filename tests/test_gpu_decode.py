@@ -243,7 +243,12 @@ def _fp8_case(rng, ctx, H, Hkv, D, bs):
 
 
 @pytest.mark.parametrize("H,Hkv,D,bs,ctx", [(32, 8, 128, 16, [1, 130, 600, 2000]), (14, 2, 64, 16, [5, 257]),
-                                            (28, 4, 128, 32, [33, 900])])
+                                            (28, 4, 128, 32, [33, 900]),
+                                            # kv-head pairs at groups 1-3 and with two kv heads, and an odd
+                                            # kv-head count (single kv heads per item)
+                                            (8, 8, 128, 16, [17, 800, 3]), (16, 8, 128, 16, [1, 1500]),
+                                            (12, 4, 128, 16, [40, 777, 16]), (8, 2, 128, 64, [65, 2100]),
+                                            (12, 3, 128, 16, [300, 31])])
 def test_decode_fp8(vkv, oracle, cuda, H, Hkv, D, bs, ctx):
     import torch
     rng = np.random.default_rng(4 + D)
