@@ -114,24 +114,22 @@ __device__ __forceinline__ u32x4 load8(const char* p, const float* scale) {
 }
 
 // Eight fp16 values for LDS: fp16 bytes as they are, FP8 codes dequantised with
-// the token's scale (code * scale in fp32, rounded to fp16).
+// the token's scale (code * scale in fp32, rounded to fp16).  The codes widen
+// exactly to fp32 two at a time (gfx950's v_cvt_pk_f32_fp8, OCP e4m3fn).
 template <int KVT>
 __device__ __forceinline__ u32x4 to_half8(u32x4 raw) {
     if constexpr (KVT == kF16) {
         return raw;
     } else {
-        const u32x2 w = {raw[0], raw[1]};
-        const float sc = as_f32(raw[2]) * kFp8HalfScale;
+        typedef float float2_t __attribute__((ext_vector_type(2)));
+        const float sc = as_f32(raw[2]);
         u32x4 r;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            uint32_t lo, hi;  // (b0, b2), (b1, b3)
-            fp8x4_to_half2x2_scaled(w[i], lo, hi);
-            const half2_t a = as_half2(lo), b = as_half2(hi);
-            const half2_t x0 = {static_cast<_Float16>(static_cast<float>(a[0]) * sc),
-                                static_cast<_Float16>(static_cast<float>(b[0]) * sc)};
-            const half2_t x1 = {static_cast<_Float16>(static_cast<float>(a[1]) * sc),
-                                static_cast<_Float16>(static_cast<float>(b[1]) * sc)};
+            const float2_t lo = __builtin_amdgcn_cvt_pk_f32_fp8(int(raw[i]), false);  // b0, b1
+            const float2_t hi = __builtin_amdgcn_cvt_pk_f32_fp8(int(raw[i]), true);   // b2, b3
+            const half2_t x0 = {static_cast<_Float16>(lo[0] * sc), static_cast<_Float16>(lo[1] * sc)};
+            const half2_t x1 = {static_cast<_Float16>(hi[0] * sc), static_cast<_Float16>(hi[1] * sc)};
             r[2 * i] = __builtin_bit_cast(uint32_t, x0);
             r[2 * i + 1] = __builtin_bit_cast(uint32_t, x1);
         }
