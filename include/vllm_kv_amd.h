@@ -197,7 +197,7 @@ int vkv_rope_cos_sin_host(float theta, int32_t head_dim, int32_t max_position, f
  * Long contexts are split into partitions of partition_size tokens that are
  * reduced by a second kernel; that needs vkv_paged_decode_workspace_size()
  * bytes of device workspace.  With partition_size 0 the kernels choose the
- * size per call from the device-side context lengths (5/6 to 2 times the
+ * size per call from the device-side context lengths (3/4 to 2 times the
  * default; the workspace size covers the smallest), so results may differ in
  * the last bits from an explicit size.
  *

@@ -78,9 +78,9 @@ def test_workspace_size_formula(vkv):
     lib = vkv.load()
     p = _decode_params(vkv, num_seqs=64, max_context_len=4112, max_blocks_per_seq=257)
     # 1 KiB of claim counters, then partials of (D + 2) floats per (seq, head, partition).  The
-    # default size is 768 tokens, but the kernels may pick a size per call from 5/6 of that
-    # (640 tokens, a multiple of the 16-token block) upwards: ceil(4112/640) = 7 partitions
-    assert lib.vkv_paged_decode_workspace_size(ctypes.byref(p)) == 1024 + 64 * 32 * 7 * (128 + 2) * 4
+    # default size is 768 tokens, but the kernels may pick a size per call from 3/4 of that
+    # (576 tokens, a multiple of the 16-token block) upwards: ceil(4112/576) = 8 partitions
+    assert lib.vkv_paged_decode_workspace_size(ctypes.byref(p)) == 1024 + 64 * 32 * 8 * (128 + 2) * 4
     p.partition_size = 512  # ceil(4112/512) = 9
     assert lib.vkv_paged_decode_workspace_size(ctypes.byref(p)) == 1024 + 64 * 32 * 9 * (128 + 2) * 4
 

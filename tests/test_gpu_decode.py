@@ -556,8 +556,8 @@ def test_decode_default_partition_choice(vkv, oracle, cuda):
     vkv.paged_decode(out, q, kc, vc, bt, cl, scale, workspace=ws)
     torch.cuda.synchronize()
     chosen = int(ws[1].item())
-    # candidates: 5/6, 1, 5/4, 3/2, 5/3 and 2 x 768 tokens, in 32-token blocks
-    assert chosen in (640, 768, 960, 1152, 1280, 1536), chosen
+    # candidates: 3/4, 7/8, 1, 5/4, 5/3 and 2 x 768 tokens, in 32-token blocks
+    assert chosen in (576, 672, 768, 960, 1280, 1536), chosen
     out2 = torch.zeros_like(out)
     vkv.paged_decode(out2, q, kc, vc, bt, cl, scale, partition_size=chosen)
     torch.cuda.synchronize()
@@ -573,6 +573,44 @@ def test_decode_default_partition_choice(vkv, oracle, cuda):
         ref = oracle.paged_decode(qn[s:s + 1], kk, vv, np.arange(nblk, dtype=np.int32)[None, :],
                                   np.array([n], np.int32), scale)
         assert_close(got[s:s + 1], ref, F16_ATOL, F16_RTOL, f"row {s} (partition {chosen})")
+
+
+def test_decode_partition_choice_below_default(vkv, cuda):
+    """C2's batch (64 rows, 8 kv heads, contexts U[513, 4097]) gives 1 784
+    items at the default 768 tokens: two waves on the busiest SIMDs of a
+    256-CU device.  672 tokens keep two (1 968 items, computed from the
+    context lengths here) with shorter partitions, so the kernels pick it and
+    record it; the output equals an explicit call at that size bit for bit."""
+    import torch
+    from vllm_kv_amd import workloads
+    cfg = workloads.config2()
+    lay = cfg.layout
+    H, Hkv, D, bs = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim, cfg.block_size
+    cl_np = np.asarray(lay.context_lens, np.int64)
+    assert int(((cl_np + 767) // 768).sum()) * Hkv == 1784
+    assert int(((cl_np + 671) // 672).sum()) * Hkv == 1968
+    bt = to_dev(lay.block_tables, cuda)
+    cl = to_dev(lay.context_lens, cuda)
+    S = bt.shape[0]
+    g = torch.Generator(device=cuda).manual_seed(22)
+    shape = (lay.num_blocks, bs, Hkv, D)
+    kc = (torch.randn(shape, generator=g, device=cuda) * 0.5).half()
+    vc = (torch.randn(shape, generator=g, device=cuda) * 0.5).half()
+    q = (torch.randn((S, H, D), generator=g, device=cuda) * 0.5).half()
+    scale = float(1.0 / np.sqrt(np.float32(D)))
+    out = torch.zeros((S, H, D), dtype=torch.float16, device=cuda)
+    need = vkv.decode_workspace_size(out, q, kc, vc, bt, cl, scale)
+    ws = torch.zeros(need // 4 + 4, dtype=torch.int32, device=cuda)
+    vkv.paged_decode(out, q, kc, vc, bt, cl, scale, workspace=ws)
+    torch.cuda.synchronize()
+    chosen = int(ws[1].item())
+    if torch.cuda.get_device_properties(cuda).multi_processor_count == 256:
+        assert chosen == 672, chosen
+    assert chosen in (576, 672, 768, 960, 1280, 1536), chosen
+    out2 = torch.zeros_like(out)
+    vkv.paged_decode(out2, q, kc, vc, bt, cl, scale, partition_size=chosen)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), out2.view(torch.int16)), chosen
 
 
 def test_decode_config5_all_rows(vkv, oracle, cuda):

@@ -86,6 +86,22 @@ __device__ __forceinline__ float group_max(float x) {
     return x;
 }
 
+// Inclusive prefix sum of v over the wave's 64 lanes in lane order, in
+// registers (no LDS round trip per step): a Hillis-Steele scan inside each
+// 16-lane row by DPP row_shr:1, 2, 4, 8 (lanes shifted in from outside the row
+// read 0), then row_bcast:15 adds lane 15 of rows 0 and 2 into rows 1 and 3,
+// and row_bcast:31 adds lane 31 (the total of rows 0-1) into rows 2 and 3.
+// Lane 63 ends with the wave total.
+__device__ __forceinline__ int wave_incl_scan(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, true);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, true);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, true);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, true);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);
+    return v;
+}
+
 // Sum over lanes that share (lane % STRIDE), i.e. across the 64/STRIDE groups
 // of STRIDE consecutive lanes.  STRIDE is a power of two.
 template <int STRIDE>

@@ -71,10 +71,17 @@ constexpr int64_t kMinItems = 2048;
 // Small batches stop splitting before a row could have more partitions than this.
 constexpr int64_t kMaxSplitParts = 64;
 // Per-call partition choice (library default only).  Candidates relative to
-// the default size P0 (block multiples, at most 64 blocks): 5/6, 1, 5/4, 3/2,
-// 5/3, 2 x P0.  Calls over more rows than kAdaptMaxRows keep P0.
-constexpr int kCandNum[kMaxPartitionCandidates] = {5, 1, 5, 3, 5, 2};
-constexpr int kCandDen[kMaxPartitionCandidates] = {6, 1, 4, 2, 3, 1};
+// the default size P0 (block multiples, at most 64 blocks): 3/4, 7/8, 1, 5/4,
+// 5/3, 2 x P0 (at P0 = 768 and 16-token blocks: 576, 672, 768, 960, 1 280,
+// 1 536).  The sizes below P0 let a batch whose items almost fill a whole
+// number of waves per SIMD take shorter partitions that keep that number.
+// Six, because the counts per candidate take registers in the kernels'
+// prologue: with ten, the compiler reloaded a kernel argument and added a
+// load wait inside the partition kernels' token loop (C5's batch: 354 us
+// against 343 us at the same partition size).  Calls over more rows than
+// kAdaptMaxRows keep P0.
+constexpr int kCandNum[kMaxPartitionCandidates] = {3, 7, 1, 5, 5, 2};
+constexpr int kCandDen[kMaxPartitionCandidates] = {4, 8, 1, 4, 3, 1};
 constexpr int kAdaptMaxRows = 4096;
 
 // One work item: partition `part` of row s (a sequence, or a prefill query
@@ -823,13 +830,14 @@ void launch_g(DecodeArgs& args, int grid_x, int grid_y, int grid_z, size_t lds, 
         const int64_t wgs = int64_t(cus) * per_cu;
         const int gx = int(wgs < grid_x ? wgs : grid_x);
         args.wave_slots = (gx > 0 ? gx : 1) * kWavesPerBlock;
-        // When even the longest possible contexts give at most one round of
-        // default-size items, the default stands and the kernels (this one
-        // and the merge, which reads these args) skip the choice.
+        args.level_waves = (gx > 0 ? (gx < cus ? gx : cus) : 1) * kWavesPerBlock;
+        // When even the longest possible contexts give at most one wave of
+        // default-size items per SIMD, the default stands and the kernels
+        // (this one and the merge, which reads these args) skip the choice.
         if (args.num_cands > 1) {
             const int64_t worst = int64_t(args.num_rows) * ((int64_t(args.max_ctx) + args.P - 1) / args.P) *
                                   args.num_kv_heads;
-            if (worst <= args.wave_slots) args.num_cands = 1;
+            if (worst <= args.level_waves) args.num_cands = 1;
         }
         hipLaunchKernelGGL(kernel, dim3(gx > 0 ? gx : 1, grid_y, grid_z), dim3(kWave * kWavesPerBlock), lds, st, args);
     };
@@ -993,6 +1001,7 @@ int launch_rows(const vkv_decode_params* p, const DecodePlan& plan, void* worksp
     a.num_cands = plan.num_candidates;
     for (int i = 0; i < kMaxPartitionCandidates; ++i) a.cands[i] = plan.candidates[i];
     a.wave_slots = 0;  // set per variant at launch
+    a.level_waves = 0;
     a.scale_log2 = p->scale * kLog2e;
     a.accumulate = p->accumulate;
 

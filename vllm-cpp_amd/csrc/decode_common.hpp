@@ -71,6 +71,7 @@ struct DecodeArgs {
     int32_t num_cands;
     int32_t cands[kMaxPartitionCandidates];
     int32_t wave_slots;       // waves of this launch resident at once (estimate)
+    int32_t level_waves;      // waves of one workgroup per CU (one wave per SIMD)
     // generic variant (any head_dim / group size / block size) only
     int32_t head_dim;
     int32_t block_size;
@@ -156,31 +157,38 @@ __device__ __forceinline__ void unpack_lane(const uint32_t* w, float* v) {
 // Partition size of a call that left it to the library.  Every workgroup
 // evaluates the same candidates over the rows' context lengths (each thread
 // brings its row tile's partition count per candidate), so all reach the same
-// size.  Items run in rounds of wave_slots resident waves.  A call whose
-// default-size items fit in one round keeps the default: it is
-// bandwidth-bound, and longer partitions only lengthen each wave's chain
-// (C2's batch: 105 us at 768 tokens, 116 us at 1 024).  Between one and two
-// rounds a second round that is only partly filled costs nearly a whole one,
-// so the candidate with the least rounds x (P + kItemOverheadTokens) wins
-// (ties: the smaller size): C3's decode rows fill 1.6 rounds at 768 tokens
-// (227 us) and one at 1 280 (the choice, 207 us).  Beyond two rounds the
-// default stays: waves that claim items as they finish fill the last round
-// with the short final partitions of the rows, and C5's batch (3.3 rounds at
-// 768) measured 361 us at 768 against 365 us at 640, the size this estimate
-// would take.
+// size.  One workgroup per CU puts one wave on each SIMD (level_waves waves),
+// so n items stack ceil(n / level_waves) waves on the busiest SIMDs, and a
+// SIMD's waves share its issue slots and memory pipeline: the call takes
+// about ceil(items / level_waves) x (P + kItemOverheadTokens), the cost the
+// candidates compete on (ties: the smaller size).  Items beyond the
+// wave_slots resident waves wait for a wave to finish, which the same count
+// covers.  C2's batch (8 kv heads, 64 rows; 1 024 waves per level) measured
+// 97.8 us at 656 tokens (2 016 items, cost 2 x 784), 98.4 at 672, 99.5 at
+// 688, 102.2 at 448 (2 840 items, 3 x 576), 102.8 at 768 (1 784 items,
+// 2 x 896), 106.4 at 512, 110.5 at 544, 113.5 at 576 and 117.7 at 608
+// (2 160 items, 3 x 736): time rises with the cost throughout, except that a
+// nearly empty extra level costs less (107.5 us at 640: 2 064 items); among
+// the candidates it takes 672 (1 968 items, 2 x 800).  C3's
+// decode rows (two waves per SIMD resident) take 1 280 tokens (2 x 1 408;
+// 207 us, against 227 us at 768 with 3 216 items).  Two cases keep the
+// default: default-size items of at most one level (small batches, which the
+// host already split finer), and beyond two rounds of resident waves, where
+// waves that claim items as they finish fill the last round with the short
+// final partitions of the rows (C5's batch, 3.3 rounds at 768 tokens:
+// 361 us at 768 against 365 us at 640).
 __device__ inline int choose_partition(const DecodeArgs& a, const int (&cnt)[kMaxPartitionCandidates]) {
     __shared__ int sums[kWavesPerBlock][kMaxPartitionCandidates];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
 #pragma unroll
     for (int c = 0; c < kMaxPartitionCandidates; ++c) {
-        int v = cnt[c];
-#pragma unroll
-        for (int o = kWave / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+        const int v = __builtin_amdgcn_readlane(wave_incl_scan(cnt[c]), kWave - 1);
         if (lane == 0) sums[wave][c] = v;
     }
     __syncthreads();
     const unsigned W = a.wave_slots > 0 ? unsigned(a.wave_slots) : 1u;
+    const unsigned L = a.level_waves > 0 ? unsigned(a.level_waves) : 1u;
     const unsigned cap = 0x7FFFFFFFu / unsigned(a.num_kv_heads);
     unsigned items0 = 0;
     uint64_t best_cost = ~uint64_t(0);
@@ -193,13 +201,13 @@ __device__ inline int choose_partition(const DecodeArgs& a, const int (&cnt)[kMa
         for (int w = 0; w < kWavesPerBlock; ++w) pairs += unsigned(sums[w][c]);
         const unsigned items = (pairs < cap ? pairs : cap) * unsigned(a.num_kv_heads);
         if (a.cands[c] == a.P) items0 = items;
-        const uint64_t cost = uint64_t((items + W - 1) / W) * unsigned(a.cands[c] + kItemOverheadTokens);
+        const uint64_t cost = uint64_t((items + L - 1) / L) * unsigned(a.cands[c] + kItemOverheadTokens);
         if (cost < best_cost) {
             best_cost = cost;
             best = a.cands[c];
         }
     }
-    return (items0 <= W || items0 > 2 * W) ? a.P : best;
+    return (items0 <= L || items0 > 2 * W) ? a.P : best;
 }
 
 // Longest-first order of the pairs of a call whose items take more than one
@@ -235,7 +243,7 @@ __device__ __forceinline__ void run_partitions(const DecodeArgs& a, const int it
 
     // Partitions per row and their exclusive prefix, scanned by the whole
     // workgroup: each thread sums a contiguous tile of rows, the 256 tile sums
-    // are scanned with wave shuffles plus one LDS step, then each thread writes
+    // are scanned with DPP wave scans plus one LDS step, then each thread writes
     // its tile's prefix entries.  A call that leaves the partition size to the
     // library counts its tile for every candidate size in the same pass and
     // picks the size first (power-of-two block sizes only).
@@ -274,12 +282,7 @@ __device__ __forceinline__ void run_partitions(const DecodeArgs& a, const int it
         for (int i = 0; i < per; ++i)
             if (r0 + i < nrows) local += parts_of(r0 + i);
     }
-    int incl = local;
-#pragma unroll
-    for (int o = 1; o < kWave; o <<= 1) {
-        const int y = __shfl_up(incl, o, kWave);
-        if (lane >= o) incl += y;
-    }
+    const int incl = wave_incl_scan(local);
     const int wave = threadIdx.x / kWave;
     if (lane == kWave - 1) wave_total[wave] = incl;
     __syncthreads();
@@ -334,12 +337,7 @@ __device__ __forceinline__ void run_partitions(const DecodeArgs& a, const int it
         int tile = 0;
         for (int i = 0; i < per2; ++i)
             if (t0 + i < nrows) tile += shortlist[t0 + i];
-        int incl = tile;
-#pragma unroll
-        for (int o = 1; o < kWave; o <<= 1) {
-            const int y = __shfl_up(incl, o, kWave);
-            if (lane >= o) incl += y;
-        }
+        const int incl = wave_incl_scan(tile);
         if (lane == kWave - 1) wave_total[threadIdx.x / kWave] = incl;
         __syncthreads();
         int before = 0;
@@ -364,12 +362,7 @@ __device__ __forceinline__ void run_partitions(const DecodeArgs& a, const int it
         const int q1 = q0 + qlen < nrows ? q0 + qlen : nrows;
         int cnt = 0;
         for (int r = q0; r < q1; ++r) cnt += bins[r] == cls ? 1 : 0;
-        int ci2 = cnt;
-#pragma unroll
-        for (int o = 1; o < kWave; o <<= 1) {
-            const int y = __shfl_up(ci2, o, kWave);
-            if (lane >= o) ci2 += y;
-        }
+        const int ci2 = wave_incl_scan(cnt);
         __syncthreads();  // every wave has read wave_total above
         if (lane == kWave - 1) wave_total[threadIdx.x / kWave] = ci2;
         __syncthreads();

@@ -289,6 +289,8 @@ void launch_variant(DecodeArgs& a, int64_t max_pairs, size_t lds, hipStream_t st
     const int64_t wgs = int64_t(device_cu_count()) * per_cu;
     const int64_t gx = groups < wgs ? groups : wgs;
     a.wave_slots = int(gx > 0 ? gx : 1) * kWavesPerBlock;
+    const int64_t cus = device_cu_count();
+    a.level_waves = int(gx > 0 ? (gx < cus ? gx : cus) : 1) * kWavesPerBlock;
     hipLaunchKernelGGL((decode_generic_kernel<KVT, DP, GC>), dim3(unsigned(gx > 0 ? gx : 1)),
                        dim3(kWave * kWavesPerBlock), lds, st, a);
 }

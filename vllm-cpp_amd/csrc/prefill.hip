@@ -926,12 +926,7 @@ __device__ int inline_row_blocks(const PrefillArgs& a, int2* lblk) {
             prior = a.cl[s] - q;
             n = seq_row_blocks(q, a.group, a.rows_per_item, a.qblocks);
         }
-        int incl = n;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int y = __shfl_up(incl, o, 64);
-            if (lane >= o) incl += y;
-        }
+        const int incl = wave_incl_scan(n);
         if (lane == 63) wave_tot[wave] = incl;
         __syncthreads();
         int before = carry;
@@ -1052,7 +1047,7 @@ constexpr int kMaxLevels = 4096;
 constexpr int kMaxHeadGroups = 63;  // claim counters after the item count (256-byte header)
 
 // Exclusive prefix sum of arr[0, n) in LDS by 256 threads (each a contiguous
-// tile, tiles combined with wave shuffles and one LDS step); returns the total.
+// tile, tiles combined with DPP wave scans and one LDS step); returns the total.
 __device__ int block_exclusive_scan(int* arr, int n, int* wave_tot) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int per = (n + 255) / 256;
@@ -1060,12 +1055,7 @@ __device__ int block_exclusive_scan(int* arr, int n, int* wave_tot) {
     int local = 0;
     for (int i = 0; i < per; ++i)
         if (b + i < n) local += arr[b + i];
-    int incl = local;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int y = __shfl_up(incl, o, 64);
-        if (lane >= o) incl += y;
-    }
+    const int incl = wave_incl_scan(local);
     if (lane == 63) wave_tot[wave] = incl;
     __syncthreads();
     int before = 0;
