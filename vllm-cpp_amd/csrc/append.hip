@@ -55,9 +55,9 @@ __device__ __forceinline__ u32x4 f32x8_to_f16x8(u32x4 a, u32x4 b) {
 constexpr int kAppendUnrollSmall = 2;
 constexpr int kAppendUnrollLarge = 8;
 template <int SRC_PER_DST, int UNROLL>
-__global__ __launch_bounds__(256) void append_rows_kernel(AppendArgs a) {
-    const int64_t stride = int64_t(gridDim.x) * blockDim.x;
-    for (int64_t i0 = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i0 < a.total; i0 += stride * UNROLL) {
+__global__ __launch_bounds__(kBlockThreads) void append_rows_kernel(AppendArgs a) {
+    const int64_t stride = int64_t(gridDim.x) * kBlockThreads;
+    for (int64_t i0 = int64_t(blockIdx.x) * kBlockThreads + threadIdx.x; i0 < a.total; i0 += stride * UNROLL) {
         int64_t slot[UNROLL], t[UNROLL], c[UNROLL];
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u) {
@@ -116,11 +116,11 @@ __device__ __forceinline__ float quotient(float x, float s, float rinv) {
 // unless the input holds inf or NaN; a wave that meets one encodes with the
 // software rule (f32_to_fp8_sat: NaN -> 0x7F, saturation) instead.
 template <typename SRC, int LPT>
-__global__ __launch_bounds__(256) void append_fp8_kernel(AppendArgs a) {
+__global__ __launch_bounds__(kBlockThreads) void append_fp8_kernel(AppendArgs a) {
     constexpr int SRC_BYTES = 16 * int(sizeof(SRC));
-    const int64_t stride = int64_t(gridDim.x) * blockDim.x;
+    const int64_t stride = int64_t(gridDim.x) * kBlockThreads;
     const int64_t per_token = int64_t(a.num_kv_heads) * LPT;
-    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < a.total; i += stride) {
+    for (int64_t i = int64_t(blockIdx.x) * kBlockThreads + threadIdx.x; i < a.total; i += stride) {
         const int64_t t = i / per_token;
         const int64_t r = i - t * per_token;  // head * LPT + sub
         const int64_t slot = a.slot_mapping[t];
@@ -203,10 +203,10 @@ __global__ __launch_bounds__(256) void append_fp8_kernel(AppendArgs a) {
 // fp16 RNE) and FP8 rule (wave amax, scale = amax / 448, exact quotient,
 // software e4m3fn encoder) as the vector kernels, so results are identical.
 template <typename SRC, int DST>
-__global__ __launch_bounds__(256) void append_elems_kernel(AppendArgs a, int head_dim) {
+__global__ __launch_bounds__(kBlockThreads) void append_elems_kernel(AppendArgs a, int head_dim) {
     const int lane = threadIdx.x & (kWave - 1);
-    const int64_t wave = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) / kWave;
-    const int64_t waves = int64_t(gridDim.x) * blockDim.x / kWave;
+    const int64_t wave = (int64_t(blockIdx.x) * kBlockThreads + threadIdx.x) / kWave;
+    const int64_t waves = int64_t(gridDim.x) * kBlockThreads / kWave;
     const int64_t pairs = a.total;  // (token, kv head) pairs
     for (int64_t i = wave; i < pairs; i += waves) {
         const int64_t t = i / a.num_kv_heads;
@@ -259,11 +259,11 @@ template <typename SRC>
 int launch_fp8(const AppendArgs& a, int lpt, hipStream_t st) {
     const int g = grid_for(a.total);
     switch (lpt) {
-        case 1: hipLaunchKernelGGL((append_fp8_kernel<SRC, 1>), dim3(g), dim3(256), 0, st, a); break;
-        case 2: hipLaunchKernelGGL((append_fp8_kernel<SRC, 2>), dim3(g), dim3(256), 0, st, a); break;
-        case 4: hipLaunchKernelGGL((append_fp8_kernel<SRC, 4>), dim3(g), dim3(256), 0, st, a); break;
-        case 8: hipLaunchKernelGGL((append_fp8_kernel<SRC, 8>), dim3(g), dim3(256), 0, st, a); break;
-        case 16: hipLaunchKernelGGL((append_fp8_kernel<SRC, 16>), dim3(g), dim3(256), 0, st, a); break;
+        case 1: hipLaunchKernelGGL((append_fp8_kernel<SRC, 1>), dim3(g), dim3(kBlockThreads), 0, st, a); break;
+        case 2: hipLaunchKernelGGL((append_fp8_kernel<SRC, 2>), dim3(g), dim3(kBlockThreads), 0, st, a); break;
+        case 4: hipLaunchKernelGGL((append_fp8_kernel<SRC, 4>), dim3(g), dim3(kBlockThreads), 0, st, a); break;
+        case 8: hipLaunchKernelGGL((append_fp8_kernel<SRC, 8>), dim3(g), dim3(kBlockThreads), 0, st, a); break;
+        case 16: hipLaunchKernelGGL((append_fp8_kernel<SRC, 16>), dim3(g), dim3(kBlockThreads), 0, st, a); break;
         default: return -1;
     }
     return 0;
@@ -304,14 +304,14 @@ int launch_append(const vkv_append_params* p, hipStream_t st) {
         const int D = p->head_dim;
         if (p->src_dtype == VKV_DTYPE_F32) {
             switch (p->cache_dtype) {
-                case VKV_DTYPE_F32: hipLaunchKernelGGL((append_elems_kernel<float, kF32>), dim3(g), dim3(256), 0, st, a, D); break;
-                case VKV_DTYPE_F16: hipLaunchKernelGGL((append_elems_kernel<float, kF16>), dim3(g), dim3(256), 0, st, a, D); break;
-                default: hipLaunchKernelGGL((append_elems_kernel<float, kFp8>), dim3(g), dim3(256), 0, st, a, D); break;
+                case VKV_DTYPE_F32: hipLaunchKernelGGL((append_elems_kernel<float, kF32>), dim3(g), dim3(kBlockThreads), 0, st, a, D); break;
+                case VKV_DTYPE_F16: hipLaunchKernelGGL((append_elems_kernel<float, kF16>), dim3(g), dim3(kBlockThreads), 0, st, a, D); break;
+                default: hipLaunchKernelGGL((append_elems_kernel<float, kFp8>), dim3(g), dim3(kBlockThreads), 0, st, a, D); break;
             }
         } else {
             switch (p->cache_dtype) {
-                case VKV_DTYPE_F16: hipLaunchKernelGGL((append_elems_kernel<_Float16, kF16>), dim3(g), dim3(256), 0, st, a, D); break;
-                case VKV_DTYPE_FP8_E4M3: hipLaunchKernelGGL((append_elems_kernel<_Float16, kFp8>), dim3(g), dim3(256), 0, st, a, D); break;
+                case VKV_DTYPE_F16: hipLaunchKernelGGL((append_elems_kernel<_Float16, kF16>), dim3(g), dim3(kBlockThreads), 0, st, a, D); break;
+                case VKV_DTYPE_FP8_E4M3: hipLaunchKernelGGL((append_elems_kernel<_Float16, kFp8>), dim3(g), dim3(kBlockThreads), 0, st, a, D); break;
                 default: return -1;
             }
         }
@@ -328,11 +328,11 @@ int launch_append(const vkv_append_params* p, hipStream_t st) {
     const int g = grid_for(a.total);
     const bool deep = a.total >= int64_t(g) * 256 * kAppendUnrollLarge;
     if (src_eb == dst_eb) {
-        if (deep) hipLaunchKernelGGL((append_rows_kernel<1, kAppendUnrollLarge>), dim3(g), dim3(256), 0, st, a);
-        else hipLaunchKernelGGL((append_rows_kernel<1, kAppendUnrollSmall>), dim3(g), dim3(256), 0, st, a);
+        if (deep) hipLaunchKernelGGL((append_rows_kernel<1, kAppendUnrollLarge>), dim3(g), dim3(kBlockThreads), 0, st, a);
+        else hipLaunchKernelGGL((append_rows_kernel<1, kAppendUnrollSmall>), dim3(g), dim3(kBlockThreads), 0, st, a);
     } else {
-        if (deep) hipLaunchKernelGGL((append_rows_kernel<2, kAppendUnrollLarge>), dim3(g), dim3(256), 0, st, a);
-        else hipLaunchKernelGGL((append_rows_kernel<2, kAppendUnrollSmall>), dim3(g), dim3(256), 0, st, a);
+        if (deep) hipLaunchKernelGGL((append_rows_kernel<2, kAppendUnrollLarge>), dim3(g), dim3(kBlockThreads), 0, st, a);
+        else hipLaunchKernelGGL((append_rows_kernel<2, kAppendUnrollSmall>), dim3(g), dim3(kBlockThreads), 0, st, a);
     }
     return 0;
 }

@@ -15,6 +15,12 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float float2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kWave = 64;
+// Threads per workgroup of the fixed-size launches (append, RoPE + append,
+// decode partitions, prefill row map).  Those kernels use this constant, not
+// blockDim.x: HIP reads blockDim.x from the dispatch's hidden arguments with
+// two dependent memory loads (block count, then group size), which every
+// workgroup would await before its first load of real data.
+constexpr int kBlockThreads = 256;
 
 enum KvType : int { kF32 = 0, kF16 = 1, kFp8 = 2 };
 

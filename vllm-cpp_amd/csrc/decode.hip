@@ -839,7 +839,7 @@ void launch_g(DecodeArgs& args, int grid_x, int grid_y, int grid_z, size_t lds, 
                                   args.num_kv_heads;
             if (worst <= args.level_waves) args.num_cands = 1;
         }
-        hipLaunchKernelGGL(kernel, dim3(gx > 0 ? gx : 1, grid_y, grid_z), dim3(kWave * kWavesPerBlock), lds, st, args);
+        hipLaunchKernelGGL(kernel, dim3(gx > 0 ? gx : 1, grid_y, grid_z), dim3(kBlockThreads), lds, st, args);
     };
     if (kMfmaShape && args.bs_log2 >= 4 && args.mfma_enabled) run(decode_partition_kernel<IO, KVT, D, G, kMfmaShape>, 1);
     else run(decode_partition_kernel<IO, KVT, D, G, false>, 0);
@@ -949,10 +949,10 @@ DecodePlan plan_decode(const vkv_decode_params* p) {
 
 // Query row r of a prefill step: its sequence and the number of keys it sees
 // (the reference's prefill is one decode per position, src/core/engine.cpp:157-164).
-__global__ __launch_bounds__(256) void prefill_rows_kernel(const int32_t* qsl, const int32_t* cl, int32_t num_seqs,
+__global__ __launch_bounds__(kBlockThreads) void prefill_rows_kernel(const int32_t* qsl, const int32_t* cl, int32_t num_seqs,
                                                            int32_t rows, int32_t max_ctx, int32_t* row_seq,
                                                            int32_t* row_ctx) {
-    const int r = blockIdx.x * blockDim.x + threadIdx.x;
+    const int r = blockIdx.x * kBlockThreads + threadIdx.x;
     if (r >= rows) return;
     int lo = 0, hi = num_seqs - 1;  // last s with qsl[s] <= r
     while (lo < hi) {
@@ -1153,7 +1153,8 @@ int launch_prefill(const vkv_prefill_params* p, const DecodePlan& plan, void* wo
     int64_t max_keys = int64_t(p->max_blocks_per_seq) * p->block_size;
     if (p->max_context_len > 0 && p->max_context_len < max_keys) max_keys = p->max_context_len;
     const int32_t max_ctx = int32_t(max_keys > 0x7FFFFFFF ? 0x7FFFFFFF : max_keys);
-    hipLaunchKernelGGL(prefill_rows_kernel, dim3((p->num_query_tokens + 255) / 256), dim3(256), 0, st,
+    hipLaunchKernelGGL(prefill_rows_kernel, dim3((p->num_query_tokens + kBlockThreads - 1) / kBlockThreads),
+                       dim3(kBlockThreads), 0, st,
                        p->query_start_loc, p->context_lens, p->num_seqs, p->num_query_tokens, max_ctx, row_seq,
                        row_ctx);
     return launch_rows(&d, plan, workspace, row_seq, row_ctx, nullptr, st);

@@ -16,6 +16,7 @@ namespace vkv {
 namespace dec {
 
 constexpr int kWavesPerBlock = 4;
+static_assert(kWave * kWavesPerBlock == kBlockThreads, "partition kernels launch kBlockThreads threads");
 // Workspace layout: a 1 KiB header holding the work-claim counters (zero
 // between calls: the merge kernel resets them) followed by the partials.
 constexpr size_t kWorkspaceHeader = 1024;
@@ -253,7 +254,7 @@ __device__ __forceinline__ void run_partitions(const DecodeArgs& a, const int it
         const int ctx = row_context(a, r);
         return ctx > 0 ? (ctx + P - 1) / P : 0;
     };
-    const int per = (nrows + int(blockDim.x) - 1) / int(blockDim.x);
+    const int per = (nrows + kBlockThreads - 1) / kBlockThreads;
     const int r0 = int(threadIdx.x) * per;
     int local = 0;
     if (a.num_cands > 1) {
@@ -295,7 +296,7 @@ __device__ __forceinline__ void run_partitions(const DecodeArgs& a, const int it
             run += parts_of(r0 + i);
         }
     }
-    if (threadIdx.x == blockDim.x - 1) prefix[nrows] = before + incl;
+    if (threadIdx.x == kBlockThreads - 1) prefix[nrows] = before + incl;
     __syncthreads();
     const int num_pairs = prefix[nrows];
     const int num_items = num_pairs * items_per_pair;
@@ -326,7 +327,7 @@ __device__ __forceinline__ void run_partitions(const DecodeArgs& a, const int it
         __syncthreads();  // every thread has read the partition prefix
         // the full counts into prefix (exclusive, by a block scan of the
         // per-thread tiles of contiguous rows)
-        const int per2 = (nrows + int(blockDim.x) - 1) / int(blockDim.x);
+        const int per2 = (nrows + kBlockThreads - 1) / kBlockThreads;
 #pragma unroll
         for (int j = 0; j * 256 < kLptMaxRows; ++j) {
             const int r = int(threadIdx.x) + 256 * j;
@@ -350,7 +351,7 @@ __device__ __forceinline__ void run_partitions(const DecodeArgs& a, const int it
                 run += c;
             }
         }
-        if (threadIdx.x == blockDim.x - 1) prefix[nrows] = before + incl;
+        if (threadIdx.x == kBlockThreads - 1) prefix[nrows] = before + incl;
         __syncthreads();  // prefix complete; the counts in shortlist are no longer needed
         num_full = prefix[nrows];
         // short final partitions by class, longest class first: thread t takes

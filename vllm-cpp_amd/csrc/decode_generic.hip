@@ -292,7 +292,7 @@ void launch_variant(DecodeArgs& a, int64_t max_pairs, size_t lds, hipStream_t st
     const int64_t cus = device_cu_count();
     a.level_waves = int(gx > 0 ? (gx < cus ? gx : cus) : 1) * kWavesPerBlock;
     hipLaunchKernelGGL((decode_generic_kernel<KVT, DP, GC>), dim3(unsigned(gx > 0 ? gx : 1)),
-                       dim3(kWave * kWavesPerBlock), lds, st, a);
+                       dim3(kBlockThreads), lds, st, a);
 }
 
 template <int KVT, int DP>

@@ -106,13 +106,13 @@ __device__ __forceinline__ void store8(char* p, const float (&x)[8]) {
 }
 
 template <typename SRC, int CT, int LPH>
-__global__ __launch_bounds__(256) void rope_append_kernel(RopeArgs a) {
+__global__ __launch_bounds__(kBlockThreads) void rope_append_kernel(RopeArgs a) {
     constexpr int D = LPH * 16;
     constexpr int HALF = D / 2;
     constexpr int SEB = int(sizeof(SRC));
-    const int64_t stride = int64_t(gridDim.x) * blockDim.x;
+    const int64_t stride = int64_t(gridDim.x) * kBlockThreads;
     const int64_t per_token = int64_t(a.heads_per_token) * LPH;
-    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < a.total; i += stride) {
+    for (int64_t i = int64_t(blockIdx.x) * kBlockThreads + threadIdx.x; i < a.total; i += stride) {
         const int64_t t = i / per_token;
         const int u = int(i - t * per_token);
         const int head = u / LPH;
@@ -199,9 +199,9 @@ template <typename SRC, int CT>
 int launch_rope_t(const RopeArgs& a, int lph, hipStream_t st) {
     const int g = rope_grid(a.total);
     switch (lph) {
-        case 4: hipLaunchKernelGGL((rope_append_kernel<SRC, CT, 4>), dim3(g), dim3(256), 0, st, a); break;
-        case 8: hipLaunchKernelGGL((rope_append_kernel<SRC, CT, 8>), dim3(g), dim3(256), 0, st, a); break;
-        case 16: hipLaunchKernelGGL((rope_append_kernel<SRC, CT, 16>), dim3(g), dim3(256), 0, st, a); break;
+        case 4: hipLaunchKernelGGL((rope_append_kernel<SRC, CT, 4>), dim3(g), dim3(kBlockThreads), 0, st, a); break;
+        case 8: hipLaunchKernelGGL((rope_append_kernel<SRC, CT, 8>), dim3(g), dim3(kBlockThreads), 0, st, a); break;
+        case 16: hipLaunchKernelGGL((rope_append_kernel<SRC, CT, 16>), dim3(g), dim3(kBlockThreads), 0, st, a); break;
         default: return -1;
     }
     return 0;
