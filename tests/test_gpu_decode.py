@@ -556,7 +556,13 @@ def test_decode_default_partition_choice(vkv, oracle, cuda):
     vkv.paged_decode(out, q, kc, vc, bt, cl, scale, workspace=ws)
     torch.cuda.synchronize()
     chosen = int(ws[1].item())
-    # candidates: 3/4, 7/8, 1, 5/4, 5/3 and 2 x 768 tokens, in 32-token blocks
+    # candidates: 3/4, 7/8, 1, 5/4, 5/3 and 2 x 768 tokens, in 32-token blocks.  On a
+    # 256-CU device (1 024 waves per level, 2 048 resident at this group size) 768
+    # tokens give 3 216 items (4 levels) and 1 280 tokens 2 044 (2 levels), the least
+    # levels x (P + 128) of the six.
+    assert int(((cl.cpu().numpy().astype(np.int64) + 1279) // 1280).sum()) * Hkv == 2044
+    if torch.cuda.get_device_properties(cuda).multi_processor_count == 256:
+        assert chosen == 1280, chosen
     assert chosen in (576, 672, 768, 960, 1280, 1536), chosen
     out2 = torch.zeros_like(out)
     vkv.paged_decode(out2, q, kc, vc, bt, cl, scale, partition_size=chosen)
