@@ -68,6 +68,32 @@ __device__ __forceinline__ float dpp_mov(float x) {
                                                                 0xF, 0xF, true));
 }
 
+// x combined with the value of lane l ^ O.  O = 16 and 32 use gfx950's
+// permlane swaps on the VALU (16-lane rows, or wave halves, change places;
+// swapping a value with itself leaves the two partners' values, one in each
+// result), other distances an LDS permute.  Both operations are commutative,
+// so every lane gets the same bits whichever result holds its own value.
+template <int O>
+__device__ __forceinline__ float xor_add(float x) {
+    if constexpr (O == 16 || O == 32) {
+        const auto a = O == 16 ? __builtin_amdgcn_permlane16_swap(as_u32(x), as_u32(x), false, false)
+                               : __builtin_amdgcn_permlane32_swap(as_u32(x), as_u32(x), false, false);
+        return as_f32(a[0]) + as_f32(a[1]);
+    } else {
+        return x + __shfl_xor(x, O, 64);
+    }
+}
+template <int O>
+__device__ __forceinline__ float xor_max(float x) {
+    if constexpr (O == 16 || O == 32) {
+        const auto a = O == 16 ? __builtin_amdgcn_permlane16_swap(as_u32(x), as_u32(x), false, false)
+                               : __builtin_amdgcn_permlane32_swap(as_u32(x), as_u32(x), false, false);
+        return fmaxf(as_f32(a[0]), as_f32(a[1]));
+    } else {
+        return fmaxf(x, __shfl_xor(x, O, 64));
+    }
+}
+
 // Sum over aligned groups of N lanes (N a power of two <= 64); every lane of a
 // group receives the group sum.
 template <int N>
@@ -76,8 +102,8 @@ __device__ __forceinline__ float group_sum(float x) {
     if constexpr (N >= 4) x += dpp_mov<0x4E>(x);
     if constexpr (N >= 8) x += dpp_mov<0x141>(x);
     if constexpr (N >= 16) x += dpp_mov<0x140>(x);
-    if constexpr (N >= 32) x += __shfl_xor(x, 16, 64);
-    if constexpr (N >= 64) x += __shfl_xor(x, 32, 64);
+    if constexpr (N >= 32) x = xor_add<16>(x);
+    if constexpr (N >= 64) x = xor_add<32>(x);
     return x;
 }
 
@@ -87,8 +113,8 @@ __device__ __forceinline__ float group_max(float x) {
     if constexpr (N >= 4) x = fmaxf(x, dpp_mov<0x4E>(x));
     if constexpr (N >= 8) x = fmaxf(x, dpp_mov<0x141>(x));
     if constexpr (N >= 16) x = fmaxf(x, dpp_mov<0x140>(x));
-    if constexpr (N >= 32) x = fmaxf(x, __shfl_xor(x, 16, 64));
-    if constexpr (N >= 64) x = fmaxf(x, __shfl_xor(x, 32, 64));
+    if constexpr (N >= 32) x = xor_max<16>(x);
+    if constexpr (N >= 64) x = xor_max<32>(x);
     return x;
 }
 
@@ -112,16 +138,14 @@ __device__ __forceinline__ int wave_incl_scan(int v) {
 // of STRIDE consecutive lanes.  STRIDE is a power of two.
 template <int STRIDE>
 __device__ __forceinline__ float cross_group_sum(float x) {
-#pragma unroll
-    for (int o = STRIDE; o < kWave; o <<= 1) x += __shfl_xor(x, o, 64);
-    return x;
+    if constexpr (STRIDE < kWave) return cross_group_sum<2 * STRIDE>(xor_add<STRIDE>(x));
+    else return x;
 }
 
 template <int STRIDE>
 __device__ __forceinline__ float cross_group_max(float x) {
-#pragma unroll
-    for (int o = STRIDE; o < kWave; o <<= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
-    return x;
+    if constexpr (STRIDE < kWave) return cross_group_max<2 * STRIDE>(xor_max<STRIDE>(x));
+    else return x;
 }
 
 // Orders this wave's earlier LDS writes before its later LDS reads of other

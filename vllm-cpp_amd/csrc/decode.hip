@@ -565,8 +565,10 @@ __device__ __forceinline__ void decode_item_mfma(const DecodeArgs& a, const int 
 
         // running max per head: lanes sharing col hold the same value after the exchange
         float cm = fmaxf(fmaxf(r[0], r[1]), fmaxf(r[2], r[3]));
-        cm = fmaxf(cm, __shfl_xor(cm, 16, kWave));
-        cm = fmaxf(cm, __shfl_xor(cm, 32, kWave));
+        // (FP8 chunks keep the exchange on the LDS permute: their VALU is the
+        // busier pipe, and the VALU swaps measured C5 1 % slower)
+        if constexpr (FP8) cm = fmaxf(cm, __shfl_xor(cm, 16, kWave)), cm = fmaxf(cm, __shfl_xor(cm, 32, kWave));
+        else cm = xor_max<32>(xor_max<16>(cm));
         const bool grow = cm > m;
         if (__builtin_amdgcn_ballot_w64(grow && col < G)) {
             const float alpha = grow ? __builtin_amdgcn_exp2f((m - cm) * sc) : 1.0f;
@@ -676,8 +678,7 @@ __device__ __forceinline__ void decode_item_mfma(const DecodeArgs& a, const int 
     }
 
     // head sums: lanes sharing col; accumulators: lanes sharing col (token groups)
-    l += __shfl_xor(l, 16, kWave);
-    l += __shfl_xor(l, 32, kWave);
+    l = xor_add<32>(xor_add<16>(l));
 #pragma unroll
     for (int h = 0; h < G; ++h)
 #pragma unroll
