@@ -619,6 +619,85 @@ def test_decode_partition_choice_below_default(vkv, cuda):
     assert torch.equal(out.view(torch.int16), out2.view(torch.int16)), chosen
 
 
+# (rows, context range, kv dtype, the size a 256-CU device picks)
+_CHOICE_BATCHES = [
+    (64, 1000, 2600, "f16", 576), (64, 512, 4096, "f16", 768), (48, 2000, 4096, "f16", 672),
+    (96, 300, 2000, "f16", 576), (64, 2600, 4096, "f16", 960), (64, 2800, 4096, "f16", 1024),
+    (64, 1000, 2600, "fp8", 576), (48, 2000, 4096, "fp8", 672), (64, 2600, 4096, "fp8", 960),
+]
+
+
+@pytest.mark.parametrize("idx", range(len(_CHOICE_BATCHES)))
+def test_decode_partition_choice_batches(vkv, oracle, cuda, idx):
+    """Batches of 48-96 rows (8 kv heads, G = 4, D = 128, 16-token blocks, the
+    matrix-core kernels; enough rows that the default stays 768 tokens) whose
+    default-size items lie beyond one level of
+    waves and within two rounds, so the kernels pick a size among 576, 672,
+    768, 960 and 1 024 tokens.  The one they record must give an output bit-identical to
+    an explicit call at that size (the merge read the same size).  On a
+    256-CU device it must be the least ceil(items / 1 024) x (P + 128), with
+    the items counted here from the context lengths.  Two rows are checked
+    against the oracle."""
+    import torch
+    from vllm_kv_amd import workloads
+    S, lo, hi, kv, want = _CHOICE_BATCHES[idx]
+    H, Hkv, D, bs = 32, 8, 128, 16
+    rng = np.random.default_rng(100 + [b[:3] for b in _CHOICE_BATCHES].index((S, lo, hi)))
+    ctx = rng.integers(lo, hi + 1, size=S).astype(np.int32)
+    lay = workloads.make_layout(ctx, bs, rng, slack=0.05)
+    cl_np = lay.context_lens.astype(np.int64)
+    cands = (576, 672, 768, 960, 1024)
+    items = {c: int(((cl_np + c - 1) // c).sum()) * Hkv for c in cands}
+    assert 1024 < items[768] <= 4096  # beyond one level, within two rounds of a 256-CU device
+    assert min(cands, key=lambda c: (-(-items[c] // 1024) * (c + 128), c)) == want
+    g = torch.Generator(device=cuda).manual_seed(idx)
+    shape = (lay.num_blocks, bs, Hkv, D)
+    ks = vs = None
+    if kv == "fp8":
+        kc = torch.empty(shape, dtype=torch.uint8, device=cuda)
+        vc = torch.empty_like(kc)
+        ks = torch.empty(shape[:3], dtype=torch.float32, device=cuda)
+        vs = torch.empty_like(ks)
+        x = torch.randn((2, lay.num_blocks * bs, Hkv, D), generator=g, device=cuda).half()
+        vkv.reshape_and_cache(x[0], x[1], kc, vc, torch.arange(lay.num_blocks * bs, dtype=torch.int32,
+                                                                device=cuda), ks, vs)
+        del x
+    else:
+        kc = (torch.randn(shape, generator=g, device=cuda) * 0.5).half()
+        vc = (torch.randn(shape, generator=g, device=cuda) * 0.5).half()
+    q = (torch.randn((S, H, D), generator=g, device=cuda) * 0.5).half()
+    bt = to_dev(lay.block_tables, cuda)
+    cl = to_dev(lay.context_lens, cuda)
+    scale = float(1.0 / np.sqrt(np.float32(D)))
+    out = torch.zeros((S, H, D), dtype=torch.float16, device=cuda)
+    need = vkv.decode_workspace_size(out, q, kc, vc, bt, cl, scale, key_scales=ks, value_scales=vs)
+    ws = torch.zeros(need // 4 + 4, dtype=torch.int32, device=cuda)
+    vkv.paged_decode(out, q, kc, vc, bt, cl, scale, key_scales=ks, value_scales=vs, workspace=ws)
+    torch.cuda.synchronize()
+    chosen = int(ws[1].item())
+    assert chosen in cands, chosen
+    if torch.cuda.get_device_properties(cuda).multi_processor_count == 256:
+        assert chosen == want, (chosen, want)
+    out2 = torch.zeros_like(out)
+    vkv.paged_decode(out2, q, kc, vc, bt, cl, scale, key_scales=ks, value_scales=vs, partition_size=chosen)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), out2.view(torch.int16)), chosen
+    got = to_np(out).astype(np.float32)
+    qn = to_np(q).astype(np.float32)
+    for s_ in (0, S - 1):
+        n = int(lay.context_lens[s_])
+        nblk = (n + bs - 1) // bs
+        ids = torch.from_numpy(lay.block_tables[s_, :nblk]).long().to(cuda)
+        tab = np.arange(nblk, dtype=np.int32)[None, :]
+        if kv == "fp8":
+            ref = oracle.paged_decode(qn[s_:s_ + 1], to_np(kc[ids]), to_np(vc[ids]), tab, np.array([n], np.int32),
+                                      scale, key_scales=to_np(ks[ids]), value_scales=to_np(vs[ids]))
+        else:
+            ref = oracle.paged_decode(qn[s_:s_ + 1], to_np(kc[ids]).view(np.uint16), to_np(vc[ids]).view(np.uint16),
+                                      tab, np.array([n], np.int32), scale)
+        assert_close(got[s_:s_ + 1], ref, F16_ATOL, F16_RTOL, f"row {s_} (partition {chosen}, {kv})")
+
+
 def test_decode_config5_all_rows(vkv, oracle, cuda):
     """Full C5 (Llama-3-8B shape, FP8 e4m3 cache with per-(token, head) scales, B=256,
     lognormal contexts up to 22.6k tokens): the pool, N(0,1) with 1 % of the values
