@@ -120,13 +120,11 @@ __global__ __launch_bounds__(kBlockThreads) void rope_append_kernel(RopeArgs a) 
         // kind 0 = query head, 1 = key head, 2 = value head (uniform over a head's lanes)
         const int kind = head < a.num_heads ? 0 : (head < a.num_heads + a.num_kv_heads ? 1 : 2);
         const int hh = kind == 0 ? head : (kind == 1 ? head - a.num_heads : head - a.num_heads - a.num_kv_heads);
+        // The slot id, the source row and the position are read together
+        // (the slot check waits for all three, not the loads for the check).
         int64_t slot = -1;
-        if constexpr (CT != kRopeOnly) {
-            if (kind != 0) {
-                slot = a.slot_mapping[t];
-                if (slot < 0 || slot >= a.num_slots) continue;  // padding token: nothing to store
-            }
-        }
+        if constexpr (CT != kRopeOnly)
+            if (kind != 0) slot = a.slot_mapping[t];
         char* src = kind == 0 ? a.q + t * a.q_stride_bytes
                               : (kind == 1 ? a.k + t * a.k_stride_bytes
                                            : const_cast<char*>(a.v) + t * a.v_stride_bytes);
@@ -134,8 +132,11 @@ __global__ __launch_bounds__(kBlockThreads) void rope_append_kernel(RopeArgs a) 
         float x0[8], x1[8];
         load8<SRC>(src + d0 * SEB, x0);
         load8<SRC>(src + (HALF + d0) * SEB, x1);
+        const int pos_in = a.positions ? a.positions[t] : a.start_pos + int(t);
+        if constexpr (CT != kRopeOnly)
+            if (kind != 0 && (slot < 0 || slot >= a.num_slots)) continue;  // padding token: nothing to store
         if (kind != 2) {
-            int pos = a.positions ? a.positions[t] : a.start_pos + int(t);
+            int pos = pos_in;
             pos = pos < 0 ? 0 : (pos >= a.max_position ? a.max_position - 1 : pos);
             const float* tb = a.cos_sin + int64_t(pos) * D + 2 * d0;
             const u32x4 c0 = load16(tb), c1 = load16(tb + 4), c2 = load16(tb + 8), c3 = load16(tb + 12);
