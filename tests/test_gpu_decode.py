@@ -584,7 +584,7 @@ def test_decode_default_partition_choice(vkv, oracle, cuda):
 def test_decode_partition_choice_below_default(vkv, cuda):
     """C2's batch (64 rows, 8 kv heads, contexts U[513, 4097]) gives 1 784
     items at the default 768 tokens: two waves on the busiest SIMDs of a
-    256-CU device.  672 tokens keep two (1 968 items, computed from the
+    256-CU device.  656 tokens keep two (2 016 items, computed from the
     context lengths here) with shorter partitions, so the kernels pick it and
     record it; the output equals an explicit call at that size bit for bit."""
     import torch
@@ -594,7 +594,7 @@ def test_decode_partition_choice_below_default(vkv, cuda):
     H, Hkv, D, bs = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim, cfg.block_size
     cl_np = np.asarray(lay.context_lens, np.int64)
     assert int(((cl_np + 767) // 768).sum()) * Hkv == 1784
-    assert int(((cl_np + 671) // 672).sum()) * Hkv == 1968
+    assert int(((cl_np + 655) // 656).sum()) * Hkv == 2016
     bt = to_dev(lay.block_tables, cuda)
     cl = to_dev(lay.context_lens, cuda)
     S = bt.shape[0]
@@ -611,8 +611,9 @@ def test_decode_partition_choice_below_default(vkv, cuda):
     torch.cuda.synchronize()
     chosen = int(ws[1].item())
     if torch.cuda.get_device_properties(cuda).multi_processor_count == 256:
-        assert chosen == 672, chosen
-    assert chosen in (576, 672, 768, 960, 1280, 1536), chosen
+        assert chosen == 656, chosen
+    # 3/4, 7/8, 1, 5/4 x 768 and 64 blocks (5/3 and 2 x 768 capped), and 55/64 x 768 in the freed slot
+    assert chosen in (576, 656, 672, 768, 960, 1024), chosen
     out2 = torch.zeros_like(out)
     vkv.paged_decode(out2, q, kc, vc, bt, cl, scale, partition_size=chosen)
     torch.cuda.synchronize()
@@ -621,9 +622,9 @@ def test_decode_partition_choice_below_default(vkv, cuda):
 
 # (rows, context range, kv dtype, the size a 256-CU device picks)
 _CHOICE_BATCHES = [
-    (64, 1000, 2600, "f16", 576), (64, 512, 4096, "f16", 768), (48, 2000, 4096, "f16", 672),
+    (64, 1000, 2600, "f16", 576), (64, 512, 4096, "f16", 768), (48, 2000, 4096, "f16", 656),
     (96, 300, 2000, "f16", 576), (64, 2600, 4096, "f16", 960), (64, 2800, 4096, "f16", 1024),
-    (64, 1000, 2600, "fp8", 576), (48, 2000, 4096, "fp8", 672), (64, 2600, 4096, "fp8", 960),
+    (64, 1000, 2600, "fp8", 576), (48, 2000, 4096, "fp8", 656), (64, 2600, 4096, "fp8", 960),
 ]
 
 
@@ -631,10 +632,10 @@ _CHOICE_BATCHES = [
 def test_decode_partition_choice_batches(vkv, oracle, cuda, idx):
     """Batches of 48-96 rows (8 kv heads, G = 4, D = 128, 16-token blocks, the
     matrix-core kernels; enough rows that the default stays 768 tokens) whose
-    default-size items lie beyond one level of
-    waves and within two rounds, so the kernels pick a size among 576, 672,
-    768, 960 and 1 024 tokens.  The one they record must give an output bit-identical to
-    an explicit call at that size (the merge read the same size).  On a
+    default-size items lie beyond one level of waves and within two rounds,
+    so the kernels pick a size among 576, 656, 672, 768, 960 and 1 024
+    tokens.  The one they record must give an output bit-identical to an
+    explicit call at that size (the merge read the same size).  On a
     256-CU device it must be the least ceil(items / 1 024) x (P + 128), with
     the items counted here from the context lengths.  Two rows are checked
     against the oracle."""
@@ -646,7 +647,7 @@ def test_decode_partition_choice_batches(vkv, oracle, cuda, idx):
     ctx = rng.integers(lo, hi + 1, size=S).astype(np.int32)
     lay = workloads.make_layout(ctx, bs, rng, slack=0.05)
     cl_np = lay.context_lens.astype(np.int64)
-    cands = (576, 672, 768, 960, 1024)
+    cands = (576, 656, 672, 768, 960, 1024)
     items = {c: int(((cl_np + c - 1) // c).sum()) * Hkv for c in cands}
     assert 1024 < items[768] <= 4096  # beyond one level, within two rounds of a 256-CU device
     assert min(cands, key=lambda c: (-(-items[c] // 1024) * (c + 128), c)) == want

@@ -72,8 +72,9 @@ constexpr int64_t kMinItems = 2048;
 constexpr int64_t kMaxSplitParts = 64;
 // Per-call partition choice (library default only).  Candidates relative to
 // the default size P0 (block multiples, at most 64 blocks): 3/4, 7/8, 1, 5/4,
-// 5/3, 2 x P0 (at P0 = 768 and 16-token blocks: 576, 672, 768, 960, 1 280,
-// 1 536).  The sizes below P0 let a batch whose items almost fill a whole
+// 5/3, 2 x P0 (at P0 = 768: 576, 672, 768, 960, 1 280 and 1 536 tokens with
+// 32-token blocks; with 16-token blocks the last two are both 1 024).  The
+// sizes below P0 let a batch whose items almost fill a whole
 // number of waves per SIMD take shorter partitions that keep that number.
 // Six, because the counts per candidate take registers in the kernels'
 // prologue: with ten, the compiler reloaded a kernel argument and added a
@@ -82,6 +83,14 @@ constexpr int64_t kMaxSplitParts = 64;
 // kAdaptMaxRows keep P0.
 constexpr int kCandNum[kMaxPartitionCandidates] = {3, 7, 1, 5, 5, 2};
 constexpr int kCandDen[kMaxPartitionCandidates] = {4, 8, 1, 4, 3, 1};
+// When the 64-block cap merges candidates (at 16-token blocks and P0 = 768,
+// 5/3 and 2 x P0 are both 1 024), the freed slots take these, in order: 55/64,
+// 15/16, 13/16 x P0 (656, 720, 624 tokens there).  C2's batch then takes 656
+// (2 016 items, still two waves per SIMD): 97.1 us explicit against 98.0 at
+// 672.
+constexpr int kFillCandidates = 3;
+constexpr int kFillNum[kFillCandidates] = {55, 15, 13};
+constexpr int kFillDen[kFillCandidates] = {64, 16, 16};
 constexpr int kAdaptMaxRows = 4096;
 
 // One work item: partition `part` of row s (a sequence, or a prefill query
@@ -931,11 +940,24 @@ DecodePlan plan_decode(const vkv_decode_params* p) {
                                           p->value_cache);
     if (p->partition_size <= 0 && p->num_seqs <= kAdaptMaxRows && fixed) {
         // the kernels pick the size per call among these (ascending)
+        auto block_multiple = [&](int num, int den) {
+            const int c = (P * num / den) / bs * bs;
+            return c < bs ? bs : (c > 64 * bs ? 64 * bs : c);
+        };
         int n = 0;
         for (int i = 0; i < kMaxPartitionCandidates; ++i) {
-            int c = (P * kCandNum[i] / kCandDen[i]) / bs * bs;
-            c = c < bs ? bs : (c > 64 * bs ? 64 * bs : c);
+            const int c = block_multiple(kCandNum[i], kCandDen[i]);
             if (n == 0 || c != plan.candidates[n - 1]) plan.candidates[n++] = c;
+        }
+        // Slots freed by the 64-block cap take finer sizes just below the default.
+        for (int i = 0; i < kFillCandidates && n < kMaxPartitionCandidates; ++i) {
+            const int c = block_multiple(kFillNum[i], kFillDen[i]);
+            int at = 0;
+            while (at < n && plan.candidates[at] < c) ++at;
+            if (at < n && plan.candidates[at] == c) continue;
+            for (int j = n; j > at; --j) plan.candidates[j] = plan.candidates[j - 1];
+            plan.candidates[at] = c;
+            ++n;
         }
         for (int i = n; i < kMaxPartitionCandidates; ++i) plan.candidates[i] = plan.candidates[n - 1];
         plan.num_candidates = n;

@@ -170,7 +170,7 @@ __device__ __forceinline__ void unpack_lane(const uint32_t* w, float* v) {
 // 2 x 896), 106.4 at 512, 110.5 at 544, 113.5 at 576 and 117.7 at 608
 // (2 160 items, 3 x 736): time rises with the cost throughout, except that a
 // nearly empty extra level costs less (107.5 us at 640: 2 064 items); among
-// the candidates it takes 672 (1 968 items, 2 x 800).  C3's decode rows (two
+// the candidates it takes 656 (2 016 items, 2 x 784).  C3's decode rows (two
 // waves per SIMD resident) take 1 280 tokens (2 044 items, 2 x 1 408), the
 // fastest of a sweep: 198.8 us, against 200.7 at 1 152, 210.0 at 768, 212.2
 // at 1 536, 223.3 at 960 and 238.0 at 2 048.  Two cases keep the
