@@ -26,6 +26,8 @@ for _p in (os.path.join(ROOT, "vllm-cpp_amd", "python"), ROOT):
         sys.path.insert(0, _p)
 
 HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E bandwidth
+WARM_MS = 300.0        # minimum wall time of untimed steps before the timed ones
+DECODE_GROUPS, DECODE_CALLS = 11, 20
 
 
 def log(msg):
@@ -124,9 +126,8 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
-    # ~0.2 s of untimed steps: an idle GPU's clocks take that long to rise
-    # (C2 decode measured 103.9 us after 10 warmup steps, 103.0 us after 2000)
-    ap.add_argument("--warmup", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=10,
+                    help="untimed steps before the timed ones (then more until %.0f ms have passed)" % WARM_MS)
     ap.add_argument("--no-cpu-baseline", action="store_true", help="skip the CPU oracle timing")
     ap.add_argument("--partition-size", type=int, default=0,
                     help="decode split-K partition in tokens (0: the library's default)")
@@ -194,16 +195,23 @@ def main():
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / n  # ms
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    log(f"[bench] warmup done: {args.warmup} steps, pool {lay.num_blocks} blocks "
-        f"({2 * kc.numel() * 2 / 1e9:.2f} GB K+V)")
+    # `warmup` steps, then more until WARM_MS of wall time has passed: an idle
+    # GPU's clocks take ~0.2 s to rise, and a run warmed by 5 steps alone timed
+    # the decode ~4 % slow.
+    t_w = time.perf_counter()
+    warm_steps = _warm(step, args.warmup, min_ms=WARM_MS)
+    warm_ms = (time.perf_counter() - t_w) * 1e3
+    log(f"[bench] warmup done: {warm_steps} steps in {warm_ms:.0f} ms ({args.warmup} asked), pool "
+        f"{lay.num_blocks} blocks ({2 * kc.numel() * 2 / 1e9:.2f} GB K+V)")
     ms_step = timed(step, args.steps)
     log(f"[bench] timed {args.steps} steps: {ms_step * 1e3:.1f} us/step")
-    ms_decode = timed(decode, args.steps)
-    ms_append = timed(append, args.steps)
-    log(f"[bench] decode {ms_decode * 1e3:.1f} us, append {ms_append * 1e3:.1f} us")
+    # the decode call alone: median, p10 and p90 over DECODE_GROUPS samples,
+    # each the mean of DECODE_CALLS back-to-back calls
+    dec = _events_ms(decode, DECODE_GROUPS * DECODE_CALLS, stream, groups=DECODE_GROUPS)
+    ms_decode = dec[0]
+    ms_append = _events_ms(append, DECODE_GROUPS * DECODE_CALLS, stream, groups=DECODE_GROUPS)[0]
+    log(f"[bench] decode {ms_decode * 1e3:.1f} us (p10 {dec[1] * 1e3:.1f}, p90 {dec[2] * 1e3:.1f}), "
+        f"append {ms_append * 1e3:.1f} us")
 
     kv_bytes = cfg.kv_bytes(2)
     traffic, traffic_note = measured_traffic()
@@ -230,6 +238,11 @@ def main():
         "decode_tokens_per_s": round(S / (ms_step * 1e-3), 1),
         "decode_tokens_per_s_32_layers": round(S / (32 * ms_step * 1e-3), 1),
         "decode_us": round(ms_decode * 1e3, 2),
+        "decode_us_p10_p90": [round(dec[1] * 1e3, 2), round(dec[2] * 1e3, 2)],
+        "decode_timing": f"median of {DECODE_GROUPS} samples, each the mean of {DECODE_CALLS} back-to-back "
+                         "calls timed with HIP events on the launch stream",
+        "warm_steps": warm_steps,
+        "warm_ms": round(warm_ms, 1),
         "append_us": round(ms_append * 1e3, 2),
         "append_gbs": round(append_bytes / (ms_append * 1e-3) / 1e9, 2),
         "kv_bytes_per_call": kv_bytes,
@@ -255,14 +268,18 @@ def _warm(fn, warmup, min_ms=200.0):
     an idle GPU's clocks take a while to rise, and a short kernel timed right
     away runs slow."""
     import torch
+    n = 0
     for _ in range(warmup):
         fn()
+        n += 1
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     while (time.perf_counter() - t0) * 1e3 < min_ms:
         for _ in range(10):
             fn()
+        n += 10
         torch.cuda.synchronize()
+    return n
 
 
 def _events_ms(fn, n, stream, groups=5):

@@ -10,8 +10,19 @@
 // the victim's blocks go to host memory (BlockManager::swap_out, then
 // vkv_swap_blocks on the caller's stream) and come back into fresh GPU blocks
 // on re-admission (BlockManager::swap_in, vkv_swap_blocks): no token is
-// recomputed.  Single-threaded, like BlockManager; all swaps of one instance
-// are ordered on the streams the caller passes (use one stream, or order them).
+// recomputed.  Single-threaded, like BlockManager.
+//
+// Stream ordering.  The block ids a swap gives up return to BlockManager's
+// free lists when the swap is enqueued, before its kernel has copied them:
+// preempt_one frees the victim's GPU blocks while the swap-out still reads
+// them, swap_in frees its CPU blocks while the swap-in still reads them.  So:
+//   - swaps of one instance are ordered among themselves by the instance (each
+//     swap's stream waits for the previous swap, whatever streams they use);
+//   - every other write into the KV cache (append, copy_blocks, a prefill's
+//     cache writes) that runs on a stream other than the swap's must be
+//     ordered after it: call wait_swaps(that_stream) after preempt_one /
+//     swap_in and before enqueuing the write.  Running all KV writes on the
+//     swap's stream orders them too.
 #pragma once
 
 #include <hip/hip_runtime_api.h>
@@ -60,6 +71,10 @@ class SwapPreemption {
     // False, with nothing changed, when the GPU pool lacks free blocks.
     bool swap_in(SwappableSequence& seq, hipStream_t stream);
 
+    // Makes `stream` wait (on the device, no host sync) until every swap this
+    // instance has enqueued so far has finished; a no-op before the first one.
+    void wait_swaps(hipStream_t stream);
+
   private:
     void enqueue_swap(const std::vector<int32_t>& pairs, int32_t direction, hipStream_t stream);
 
@@ -73,6 +88,9 @@ class SwapPreemption {
     int32_t* host_pairs_ = nullptr;
     hipEvent_t uploaded_ = nullptr;
     bool upload_pending_ = false;
+    // Recorded after each swap kernel: the next swap and wait_swaps wait on it.
+    hipEvent_t swapped_ = nullptr;
+    bool swap_enqueued_ = false;
 };
 
 }  // namespace vllm

@@ -206,11 +206,13 @@ int vkv_rope_cos_sin_host(float theta, int32_t head_dim, int32_t max_position, f
  * int 1, the partition size the call chose), and calls that may run
  * concurrently need distinct workspaces.  workspace == NULL uses a buffer the
  * library keeps per (device, stream): calls on different streams never share
- * it.  It grows with hipMalloc when a call needs more (an outgrown buffer is
- * kept, not freed, so graphs captured before stay valid); a call that would
- * grow it while its stream is being captured fails with VKV_ERR_WORKSPACE
- * instead, so capture after one eager call of the largest size, or pass a
- * workspace.  Calls over many sequences are split into consecutive ranges of
+ * it (hipStreamPerThread: per (device, thread)).  It grows with hipMalloc
+ * when a call needs more (an outgrown buffer is kept, not freed, so graphs
+ * captured before stay valid); a call that would grow it while its stream is
+ * being captured fails with VKV_ERR_WORKSPACE instead, so capture after one
+ * eager call of the largest size, or pass a workspace.  The buffers live
+ * until vkv_release_workspace(stream), which a caller runs before it destroys
+ * the stream.  Calls over many sequences are split into consecutive ranges of
  * rows inside the library (same results).
  * ------------------------------------------------------------------------- */
 typedef struct vkv_decode_params {
@@ -242,6 +244,17 @@ typedef struct vkv_decode_params {
 
 size_t vkv_paged_decode_workspace_size(const vkv_decode_params* p);
 int vkv_paged_decode(const vkv_decode_params* p, vkv_stream_t stream);
+
+/* Frees the workspace buffers the library keeps for `stream` on the current
+ * device (the ones decode and prefill calls with workspace == NULL use), after
+ * synchronising the stream; for hipStreamPerThread, the calling thread's.  No
+ * counterpart in the reference, whose kernels use no workspace.  Call it
+ * before destroying a stream the library was called on with workspace ==
+ * NULL: a stream created later at the same handle value would otherwise
+ * inherit the buffers, and they would stay allocated until the process ends.
+ * Graphs captured from such calls on that stream must not be replayed after
+ * it.  VKV_OK (nothing to do) for a stream without buffers. */
+int vkv_release_workspace(vkv_stream_t stream);
 
 /* Paged decode that allocates nothing.  No counterpart in the reference: it is
  * for callers that cannot allocate device memory (code under HIP graph

@@ -160,6 +160,54 @@ void oracle_rope(void* query, void* key, int64_t query_stride, int64_t key_strid
 
 /* ---------------------------------------------------------------- append */
 
+/* One (token, kv head) vector of head_dim source elements at element offset
+ * s0 -> head_dim e4m3 codes; returns the vector's scale (amax / 448, 1 for an
+ * all-zero vector).  Each code is the nearest e4m3 value of x / scale. */
+static float quantise_row_fp8(const void* src, int64_t s0, int32_t head_dim, int32_t src_dtype, uint8_t* codes) {
+    float amax = 0.0f;
+    for (int d = 0; d < head_dim; ++d) {
+        float a = fabsf(load_elem(src, s0 + d, src_dtype));
+        if (a > amax) amax = a;
+    }
+    float sc = oracle_fp8_scale(amax);
+    for (int d = 0; d < head_dim; ++d) codes[d] = oracle_fp8_encode(load_elem(src, s0 + d, src_dtype) / sc);
+    return sc;
+}
+
+typedef struct quant_job {
+    const void* src;
+    uint8_t* codes;
+    float* scales;
+    int32_t head_dim, src_dtype;
+    int64_t begin, end;
+} quant_job;
+
+static void* quant_worker(void* p) {
+    const quant_job* j = (const quant_job*)p;
+    for (int64_t r = j->begin; r < j->end; ++r)
+        j->scales[r] = quantise_row_fp8(j->src, r * j->head_dim, j->head_dim, j->src_dtype,
+                                        j->codes + r * j->head_dim);
+    return NULL;
+}
+
+void oracle_fp8_quantise_rows(const void* src, int64_t num_rows, int32_t head_dim, int32_t src_dtype,
+                              uint8_t* codes, float* scales, int32_t nthreads) {
+    pthread_once(&g_tables_once, fill_tables);
+    if (nthreads < 1) nthreads = 1;
+    if (nthreads > 256) nthreads = 256;
+    if ((int64_t)nthreads > num_rows) nthreads = (int32_t)(num_rows > 0 ? num_rows : 1);
+    quant_job jobs[256];
+    pthread_t th[256];
+    for (int i = 0; i < nthreads; ++i) {
+        jobs[i] = (quant_job){src, codes, scales, head_dim, src_dtype, num_rows * i / nthreads,
+                              num_rows * (i + 1) / nthreads};
+        if (nthreads > 1) pthread_create(&th[i], NULL, quant_worker, &jobs[i]);
+    }
+    if (nthreads == 1) quant_worker(&jobs[0]);
+    else
+        for (int i = 0; i < nthreads; ++i) pthread_join(th[i], NULL);
+}
+
 void oracle_reshape_and_cache(const void* key, const void* value, int64_t key_stride,
                               int64_t value_stride, void* key_cache, void* value_cache,
                               float* key_scales, float* value_scales,
@@ -192,15 +240,8 @@ void oracle_reshape_and_cache(const void* key, const void* value, int64_t key_st
                     for (int d = 0; d < head_dim; ++d)
                         ((uint16_t*)dst)[d0 + d] = oracle_f32_to_f16(load_elem(src, s0 + d, src_dtype));
                 } else { /* FP8 */
-                    float amax = 0.0f;
-                    for (int d = 0; d < head_dim; ++d) {
-                        float a = fabsf(load_elem(src, s0 + d, src_dtype));
-                        if (a > amax) amax = a;
-                    }
-                    float sc = oracle_fp8_scale(amax);
-                    scales[slot * num_kv_heads + h] = sc;
-                    for (int d = 0; d < head_dim; ++d)
-                        ((uint8_t*)dst)[d0 + d] = oracle_fp8_encode(load_elem(src, s0 + d, src_dtype) / sc);
+                    scales[slot * num_kv_heads + h] =
+                        quantise_row_fp8(src, s0, head_dim, src_dtype, (uint8_t*)dst + d0);
                 }
             }
         }

@@ -55,6 +55,14 @@ void oracle_reshape_and_cache(const void* key, const void* value, int64_t key_st
                               int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
                               int32_t num_blocks, int32_t src_dtype, int32_t cache_dtype);
 
+/* The FP8 quantisation of oracle_reshape_and_cache on a dense array of rows:
+ * row r of head_dim source elements (src_dtype) -> codes[r * head_dim ..] and
+ * scales[r], by the same per-row code (amax / 448 scale, nearest e4m3 code of
+ * x / scale), on nthreads threads (rows are independent).  Pinned by
+ * tests/test_oracle.py against oracle_reshape_and_cache and torch's e4m3. */
+void oracle_fp8_quantise_rows(const void* src, int64_t num_rows, int32_t head_dim, int32_t src_dtype,
+                              uint8_t* codes, float* scales, int32_t nthreads);
+
 /* RoPE in place.  Restates src/kernels/rotary_embedding.cu:13-34 (pairs d and
  * d + D/2, interleaved [pos][D/2][cos, sin] table rows of head_dim floats,
  * q heads h < num_heads, k heads h < num_kv_heads) with pos = positions[t]

@@ -38,6 +38,8 @@ def load() -> ctypes.CDLL:
         i32, i64, f32 = ctypes.c_int32, ctypes.c_int64, ctypes.c_float
         lib.oracle_reshape_and_cache.argtypes = [P, P, i64, i64, P, P, P, P, P, i32, i32, i32, i32, i32, i32, i32]
         lib.oracle_reshape_and_cache.restype = None
+        lib.oracle_fp8_quantise_rows.argtypes = [P, i64, i32, i32, P, P, i32]
+        lib.oracle_fp8_quantise_rows.restype = None
         lib.oracle_paged_decode.argtypes = [P, P, P, P, P, P, P, P, i32, i32, i32, i32, i32, i32, i32, f32, i32, i32]
         lib.oracle_paged_decode.restype = None
         lib.oracle_paged_prefill.argtypes = [P, P, P, P, P, P, P, P, P, i32, i32, i32, i32, i32, i32, f32, i32, i32]
@@ -99,6 +101,18 @@ def reshape_and_cache(key, value, key_cache, value_cache, slot_mapping, key_scal
     load().oracle_reshape_and_cache(_p(key), _p(value), 0, 0, _p(key_cache), _p(value_cache),
                                     _p(key_scales), _p(value_scales), _p(slot_mapping), T, Hkv, D, bs, N,
                                     dtype_code(key), dtype_code(key_cache))
+
+
+def fp8_quantise_rows(x, nthreads=1):
+    """x [..., D] fp32, or fp16 bits as uint16 -> (codes uint8 [..., D], scales fp32 [...]):
+    the FP8 quantisation reshape_and_cache applies per (token, kv head) vector."""
+    x = np.ascontiguousarray(x)
+    D = x.shape[-1]
+    rows = x.size // D
+    codes = np.empty(x.shape, np.uint8)
+    scales = np.empty(x.shape[:-1], np.float32)
+    load().oracle_fp8_quantise_rows(_p(x), rows, D, dtype_code(x), _p(codes), _p(scales), nthreads)
+    return codes, scales
 
 
 def rope(query, key, cos_sin, positions=None, start_pos=0):

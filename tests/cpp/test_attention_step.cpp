@@ -77,6 +77,7 @@ struct Harness {
     std::vector<std::vector<float>> hks, hvs;
     std::mt19937 gen;
     std::normal_distribution<float> nd{0.f, 0.6f};
+    hipStream_t st = nullptr;  // the stream the layer's kernels (appends included) run on
 
     Harness(const Geometry& geo, uint32_t seed, int cpu_blocks = 0)
         : g(geo),
@@ -137,7 +138,7 @@ struct Harness {
             qsl.push_back(qsl.back() + nnew[s]);
         }
         const int T = qsl.back();
-        md.build(ss, nullptr);
+        md.build(ss, st);
         CHECK_EQ(md.num_tokens(), T);
         CHECK_EQ(md.single_token_seqs(), int32_t(std::count(nnew.begin(), nnew.end(), 1)));
         CHECK_EQ(md.max_query_len(), *std::max_element(nnew.begin(), nnew.end()));
@@ -166,7 +167,7 @@ struct Harness {
             VLLM_HIP_CHECK(hipMemcpy(dq, q.data(), q.size(), hipMemcpyHostToDevice));
             VLLM_HIP_CHECK(hipMemcpy(dk, k.data(), k.size(), hipMemcpyHostToDevice));
             VLLM_HIP_CHECK(hipMemcpy(dv, v.data(), v.size(), hipMemcpyHostToDevice));
-            layer.forward(dout, dq, dk, dv, g.io, cache, md, size_t(l), nullptr);
+            layer.forward(dout, dq, dk, dv, g.io, cache, md, size_t(l), st);
             VLLM_HIP_CHECK(hipDeviceSynchronize());
 
             // oracle: the reference's rope then row copies, then one decode per query position
@@ -318,8 +319,23 @@ void run_fork_swap_scenario(const Geometry& g, uint32_t seed) {
 // A finishes B is swapped back in, its blocks' bytes equal those it had before
 // (every layer, K and V), and it decodes on.  Attention is checked against the
 // oracle at every step.
-void run_swap_preemption_scenario(const Geometry& g, uint32_t seed) {
+//
+// With side_stream, the swaps run on a side stream behind 1 GiB of unrelated
+// work (a memset), while the layer's appends and attention run on a compute
+// stream: the swap-out is still queued when A's next append is enqueued into
+// the block B gave up, so only SwapPreemption::wait_swaps(compute) keeps that
+// append from overwriting B's bytes before they are copied to the host.
+void run_swap_preemption_scenario(const Geometry& g, uint32_t seed, bool side_stream = false) {
     Harness h(g, seed, 3);
+    hipStream_t compute = nullptr, side = nullptr;
+    void* busy = nullptr;
+    const size_t busy_bytes = size_t(1) << 30;
+    if (side_stream) {
+        VLLM_HIP_CHECK(hipStreamCreateWithFlags(&compute, hipStreamNonBlocking));
+        VLLM_HIP_CHECK(hipStreamCreateWithFlags(&side, hipStreamNonBlocking));
+        VLLM_HIP_CHECK(hipMalloc(&busy, busy_bytes));
+        h.st = compute;
+    }
     CHECK_EQ(h.bm.num_total_gpu_blocks(), 3u);
     const size_t hbb = h.cache.host_block_bytes();
     void* host = nullptr;
@@ -357,7 +373,9 @@ void run_swap_preemption_scenario(const Geometry& g, uint32_t seed) {
     }
     CHECK(!h.bm.ensure_sequence_capacity(a.block_table, 33));
     CHECK_EQ(vllm::SwapPreemption::pick_victim(running, &a), 1);
-    CHECK(swap.preempt_one(running, waiting, &a, nullptr));
+    if (side_stream) VLLM_HIP_CHECK(hipMemsetAsync(busy, 0x5a, busy_bytes, side));
+    CHECK(swap.preempt_one(running, waiting, &a, side));
+    swap.wait_swaps(compute);
     CHECK(h.bm.ensure_sequence_capacity(a.block_table, 33));
     CHECK_EQ(a.block_table.size(), 3u);
     CHECK(b.swapped_out);
@@ -365,7 +383,7 @@ void run_swap_preemption_scenario(const Geometry& g, uint32_t seed) {
     CHECK_EQ(waiting.size(), 1u);
     CHECK_EQ(running.size(), 1u);
     CHECK(running[0] == &a);
-    CHECK(!swap.preempt_one(running, waiting, &a, nullptr));  // A alone: no victim
+    CHECK(!swap.preempt_one(running, waiting, &a, side));  // A alone: no victim
     h.step({&a.block_table}, {32}, {1}, "decode A in the third block");  // may overwrite B's old block
 
     // A finishes; B is re-admitted by swap-in, not replay
@@ -373,7 +391,9 @@ void run_swap_preemption_scenario(const Geometry& g, uint32_t seed) {
     a.block_table.clear();
     a.finished = true;
     running.clear();
-    CHECK(swap.swap_in(b, nullptr));
+    if (side_stream) VLLM_HIP_CHECK(hipMemsetAsync(busy, 0xa5, busy_bytes, side));
+    CHECK(swap.swap_in(b, side));
+    swap.wait_swaps(compute);
     waiting.pop_front();
     running.push_back(&b);
     CHECK(!b.swapped_out);
@@ -391,13 +411,23 @@ void run_swap_preemption_scenario(const Geometry& g, uint32_t seed) {
     CHECK(h.bm.ensure_sequence_capacity(b.block_table, 17));
     CHECK_EQ(b.block_table.size(), 2u);
     h.step({&b.block_table}, {16}, {1}, "decode B after swap-in");
+    VLLM_HIP_CHECK(hipDeviceSynchronize());
     (void)hipHostFree(host);
+    if (side_stream) {
+        (void)hipFree(busy);
+        (void)hipStreamDestroy(side);
+        (void)hipStreamDestroy(compute);
+    }
 }
 
 }  // namespace
 
 TEST_CASE(preemption_by_swap_reference_pressure_test) {
     run_swap_preemption_scenario({2, 3, 16, 14, 2, 64, vllm::KVDtype::kF16, vllm::KVDtype::kF16}, 6);
+}
+
+TEST_CASE(preemption_by_swap_on_a_side_stream) {
+    run_swap_preemption_scenario({2, 3, 16, 14, 2, 64, vllm::KVDtype::kF16, vllm::KVDtype::kF16}, 7, true);
 }
 
 TEST_CASE(attention_step_f16_qwen05b_shape) {

@@ -194,6 +194,49 @@ def test_decode_f32_reference_api_semantics(vkv, oracle, cuda):
     assert_close(got, ref, F32_ATOL, F32_RTOL, "fp32 decode")
 
 
+# scale 0 weighs every key e^0 = 1 in the reference (the mean of V); each
+# kernel family: fixed fp16 D 128 (matrix-core QK^T), fixed D 64 (VALU),
+# generic (head_dim 80, group 16), FP8 cache, fp32 reference types.
+@pytest.mark.parametrize("H,Hkv,D,bs,io,kv", [(32, 8, 128, 16, "f16", "f16"), (14, 2, 64, 16, "f16", "f16"),
+                                              (32, 2, 80, 12, "f16", "f16"), (32, 8, 128, 16, "f16", "fp8"),
+                                              (14, 2, 64, 16, "f32", "f32")])
+def test_decode_scale_zero(vkv, oracle, cuda, H, Hkv, D, bs, io, kv):
+    import torch
+    rng = np.random.default_rng(77 + D)
+    ctx = [1, 16, 300, 1100]
+    lay = _layout(rng, ctx, bs)
+    N = lay.num_blocks
+    kf = rng.standard_normal((N, bs, Hkv, D), dtype=np.float32)
+    vf = rng.standard_normal((N, bs, Hkv, D), dtype=np.float32)
+    q = (rng.standard_normal((len(ctx), H, D), dtype=np.float32) * 4).astype(np.float16).astype(np.float32)
+    ks = vs = hks = hvs = None
+    if kv == "f32":
+        hk, hv, kc, vc = kf, vf, to_dev(kf, cuda), to_dev(vf, cuda)
+    elif kv == "f16":
+        hk, hv = kf.astype(np.float16).view(np.uint16), vf.astype(np.float16).view(np.uint16)
+        kc, vc = to_dev(hk.view(np.float16), cuda), to_dev(hv.view(np.float16), cuda)
+    else:
+        kc = torch.zeros((N, bs, Hkv, D), dtype=torch.uint8, device=cuda)
+        vc = torch.zeros_like(kc)
+        ks = torch.zeros((N, bs, Hkv), dtype=torch.float32, device=cuda)
+        vs = torch.zeros_like(ks)
+        vkv.reshape_and_cache(to_dev(kf.astype(np.float16).reshape(-1, Hkv, D), cuda),
+                              to_dev(vf.astype(np.float16).reshape(-1, Hkv, D), cuda), kc, vc,
+                              to_dev(np.arange(N * bs, dtype=np.int32), cuda), ks, vs)
+        torch.cuda.synchronize()
+        hk, hv, hks, hvs = to_np(kc), to_np(vc), to_np(ks), to_np(vs)
+    ref = oracle.paged_decode(q, hk, hv, lay.block_tables, lay.context_lens, 0.0, key_scales=hks, value_scales=hvs)
+    out = torch.zeros((len(ctx), H, D), dtype=torch.float16 if io == "f16" else torch.float32, device=cuda)
+    vkv.paged_decode(out, to_dev(q.astype(np.float16) if io == "f16" else q, cuda), kc, vc,
+                     to_dev(lay.block_tables, cuda), to_dev(lay.context_lens, cuda), 0.0, key_scales=ks,
+                     value_scales=vs)
+    torch.cuda.synchronize()
+    got = to_np(out).astype(np.float32)
+    assert np.isfinite(got).all()
+    tol = (F16_ATOL, F16_RTOL) if io == "f16" else (F32_ATOL, F32_RTOL)
+    assert_close(got, ref, *tol, f"scale 0 decode {H}/{Hkv}/{D} {io}/{kv}")
+
+
 def test_decode_f32_io_f16_kv(vkv, oracle, cuda):
     rng = np.random.default_rng(21)
     ctx = [3, 200, 700]
@@ -393,6 +436,63 @@ def test_decode_concurrent_streams_library_workspace(vkv, cuda):
     for i in range(6):
         assert torch.equal(outs_a[i].view(torch.int16), solo_a.view(torch.int16)), ("stream 1", i)
         assert torch.equal(outs_b[i].view(torch.int16), solo_b.view(torch.int16)), ("stream 2", i)
+
+
+def test_decode_per_thread_stream_and_release(vkv, cuda):
+    """hipStreamPerThread names a different stream in each thread: two threads
+    decoding on it at the same time each get their own library workspace, and
+    every output equals its solo run bit for bit.  vkv_release_workspace frees
+    a stream's buffers; the next call on that stream allocates afresh and gives
+    the same result, and releasing a stream without buffers is a no-op."""
+    import threading
+    import torch
+    cfg, kc, vc, qa, _, _ = _c2_inputs(cuda)
+    _, kc_b, vc_b, qb, _, _ = _c2_inputs(cuda, seed_shift=5)
+    lay = cfg.layout
+    bt = to_dev(lay.block_tables, cuda)
+    cl = to_dev(lay.context_lens, cuda)
+    solo = [torch.zeros_like(qa), torch.zeros_like(qb)]
+    vkv.paged_decode(solo[0], qa, kc, vc, bt, cl, cfg.scale)
+    vkv.paged_decode(solo[1], qb, kc_b, vc_b, bt, cl, cfg.scale)
+    torch.cuda.synchronize()
+    outs = [[torch.full_like(qa, float("nan")) for _ in range(6)], [torch.full_like(qb, float("nan")) for _ in range(6)]]
+    args = [(qa, kc, vc), (qb, kc_b, vc_b)]
+    errors = []
+    start = threading.Barrier(2)
+
+    def worker(w):
+        try:
+            torch.cuda.set_device(cuda)
+            q_, k_, v_ = args[w]
+            start.wait()
+            for i in range(6):
+                vkv.paged_decode(outs[w][i], q_, k_, v_, bt, cl, cfg.scale, stream=vkv.STREAM_PER_THREAD)
+            torch.cuda.synchronize()
+            vkv.release_workspace(vkv.STREAM_PER_THREAD)
+        except Exception as e:  # reported below
+            errors.append(e)
+
+    torch.cuda.synchronize()  # the fills of outs run on torch's stream
+    ths = [threading.Thread(target=worker, args=(w,)) for w in range(2)]
+    for t in ths:
+        t.start()
+    for t in ths:
+        t.join()
+    assert not errors, errors
+    for w in range(2):
+        for i in range(6):
+            assert torch.equal(outs[w][i].view(torch.int16), solo[w].view(torch.int16)), ("thread", w, i)
+    s1 = torch.cuda.Stream()
+    vkv.release_workspace(s1)  # nothing allocated yet
+    again = torch.full_like(qa, float("nan"))
+    vkv.paged_decode(again, qa, kc, vc, bt, cl, cfg.scale, stream=s1)
+    vkv.release_workspace(s1)
+    again2 = torch.full_like(qa, float("nan"))
+    vkv.paged_decode(again2, qa, kc, vc, bt, cl, cfg.scale, stream=s1)
+    s1.synchronize()
+    vkv.release_workspace(s1)
+    assert torch.equal(again.view(torch.int16), solo[0].view(torch.int16))
+    assert torch.equal(again2.view(torch.int16), solo[0].view(torch.int16))
 
 
 def test_decode_library_workspace_capture_rules(vkv, cuda):
@@ -711,7 +811,7 @@ def test_decode_config5_all_rows(vkv, oracle, cuda):
     lay = cfg.layout
     S, H, Hkv, D, bs = cfg.num_seqs, cfg.num_heads, cfg.num_kv_heads, cfg.head_dim, cfg.block_size
     N = lay.num_blocks
-    g = torch.Generator(device=cuda).manual_seed(41)
+    g = torch.Generator(device=cuda).manual_seed(4)  # the pool and queries bench.py's C5 row draws
     kc = torch.empty((N, bs, Hkv, D), dtype=torch.uint8, device=cuda)
     vc = torch.empty_like(kc)
     ks = torch.empty((N, bs, Hkv), dtype=torch.float32, device=cuda)

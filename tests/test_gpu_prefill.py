@@ -104,6 +104,25 @@ def test_prefill_fp8_vs_oracle(vkv, oracle, cuda, H, Hkv, D, bs):
     assert_close(to_np(out).astype(np.float32), ref, F16_ATOL, F16_RTOL, "fp8 prefill")
 
 
+@pytest.mark.parametrize("kvt", ["f16", "fp8"])
+@pytest.mark.parametrize("H,Hkv,D,bs", [(28, 4, 128, 32), (14, 2, 64, 16)])
+def test_prefill_scale_zero(vkv, oracle, cuda, kvt, H, Hkv, D, bs):
+    """scale 0 (every key weighs e^0 = 1 in the reference: row j is the mean of
+    V over its prior + j + 1 keys) on the matrix-core kernels and the decode rows."""
+    import torch
+    lay, ctx, qsl, q, k, v, _ = _case(H, Hkv, D, bs, [70, 1, 200], [30, 90, 0], 19)
+    (kc, vc, ks, vs), (hk, hv, hks, hvs) = _cache(vkv, cuda, kvt, k, v)
+    ref = oracle.paged_prefill(q.astype(np.float32), hk, hv, lay.block_tables, ctx, qsl, 0.0,
+                               key_scales=hks, value_scales=hvs, nthreads=_threads())
+    out = torch.zeros((q.shape[0], H, D), dtype=torch.float16, device=cuda)
+    vkv.paged_prefill(out, to_dev(q, cuda), kc, vc, to_dev(lay.block_tables, cuda), to_dev(ctx, cuda),
+                      to_dev(qsl, cuda), 200, 0.0, key_scales=ks, value_scales=vs)
+    torch.cuda.synchronize()
+    got = to_np(out).astype(np.float32)
+    assert np.isfinite(got).all()
+    assert_close(got, ref, F16_ATOL, F16_RTOL, f"scale 0 prefill ({kvt} cache)")
+
+
 def test_prefill_many_items(vkv, oracle, cuda):
     """More work items than persistent workgroups (items claimed in turn), ragged lengths."""
     import torch
@@ -124,13 +143,14 @@ def test_prefill_many_items(vkv, oracle, cuda):
 
 @pytest.mark.parametrize("kvt", ["f16", "fp8"])
 def test_prefill_mixed_config3(vkv, oracle, cuda, kvt):
-    """C3's mixed call at its full size: 8 chunks of 512 query tokens (prior
-    U[0, 2048]) on the matrix-core kernels and 120 single-token sequences
-    (contexts U[1024, 8192]) through split-K decode with the partition size
-    picked on the device, over an fp16 cache and over its FP8 quantisation.
-    Every row of the chunks with the longest and the shortest prior context,
-    and every decode row, against the oracle (row j of a chunk is decode over
-    prior + j + 1 keys)."""
+    """C3's mixed call at its full size and with its stated inputs (pool and
+    queries 0.3 N(0,1) from seed 2, drawn as bench.py's C3 rows draw them):
+    8 chunks of 512 query tokens (prior U[0, 2048]) on the matrix-core kernels
+    and 120 single-token sequences (contexts U[1024, 8192]) through split-K
+    decode with the partition size picked on the device, over an fp16 cache
+    and over its FP8 quantisation.  Every one of the 4 216 query rows (4 096
+    chunk rows, 120 decode rows) against the oracle, where row j of a chunk is
+    decode over prior + j + 1 keys (src/core/engine.cpp:157-164)."""
     import torch
     from vllm_kv_amd import workloads
     cfg = workloads.config3()
@@ -138,11 +158,11 @@ def test_prefill_mixed_config3(vkv, oracle, cuda, kvt):
     H, Hkv, D, bs = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim, cfg.block_size
     qsl = cfg.query_start_loc
     Tq = int(qsl[-1])
-    g = torch.Generator(device=cuda).manual_seed(23)
+    g = torch.Generator(device=cuda).manual_seed(2)
     shape = (lay.num_blocks, bs, Hkv, D)
-    k16 = (torch.randn(shape, generator=g, device=cuda) * 0.5).half()
-    v16 = (torch.randn(shape, generator=g, device=cuda) * 0.5).half()
-    q = (torch.randn((Tq, H, D), generator=g, device=cuda) * 0.5).half()
+    k16 = (torch.randn(shape, generator=g, device=cuda) * 0.3).half()
+    v16 = (torch.randn(shape, generator=g, device=cuda) * 0.3).half()
+    q = (torch.randn((Tq, H, D), generator=g, device=cuda) * 0.3).half()
     if kvt == "f16":
         kc, vc, ks, vs = k16, v16, None, None
         hk, hv, hks, hvs = to_np(kc).view(np.uint16), to_np(vc).view(np.uint16), None, None
@@ -160,16 +180,11 @@ def test_prefill_mixed_config3(vkv, oracle, cuda, kvt):
                       to_dev(qsl, cuda), int(cfg.q_lens.max()), cfg.scale, key_scales=ks, value_scales=vs)
     torch.cuda.synchronize()
     got = to_np(out).astype(np.float32)
-    qn = to_np(q).astype(np.float32)
+    ref = oracle.paged_prefill(to_np(q).astype(np.float32), hk, hv, lay.block_tables, lay.context_lens, qsl,
+                               cfg.scale, key_scales=hks, value_scales=hvs, nthreads=_threads())
     npf = int((cfg.q_lens > 1).sum())
-    prior = cfg.prior_lens[:npf]
-    seqs = sorted({int(np.argmax(prior)), int(np.argmin(prior))}) + list(range(npf, len(cfg.q_lens)))
-    rows = np.concatenate([np.arange(qsl[s], qsl[s + 1]) for s in seqs])
-    sub_qsl = np.concatenate([[0], np.cumsum([qsl[s + 1] - qsl[s] for s in seqs])]).astype(np.int32)
-    ref = oracle.paged_prefill(qn[rows], hk, hv, np.ascontiguousarray(lay.block_tables[seqs]),
-                               np.ascontiguousarray(lay.context_lens[seqs]), sub_qsl, cfg.scale,
-                               key_scales=hks, value_scales=hvs, nthreads=_threads())
-    assert_close(got[rows], ref, F16_ATOL, F16_RTOL, f"C3 ({kvt} cache): 2 chunks and 120 decode rows")
+    assert int(qsl[npf]) == 4096 and Tq == 4216
+    assert_close(got, ref, F16_ATOL, F16_RTOL, f"C3 ({kvt} cache): all 4096 chunk rows and 120 decode rows")
 
 
 @pytest.mark.parametrize("kvt", ["f16", "fp8"])

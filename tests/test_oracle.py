@@ -241,6 +241,50 @@ def test_append_fp8_matches_torch_quantisation(oracle):
         assert np.array_equal(codes.reshape(-1, Hkv, D)[slots], q)
 
 
+@pytest.mark.parametrize("src", [np.float16, np.float32])
+def test_fp8_quantise_rows_matches_append_and_torch(oracle, src):
+    """The dense quantiser (the checker of the large FP8 append test) against
+    the append's own scatter and against torch's e4m3 cast of x / (amax / 448),
+    on C5's input distribution (N(0,1) with 1 % outliers x8, seed 4), with an
+    all-zero vector and a 448-saturating one."""
+    rng = np.random.default_rng(4)
+    T, Hkv, D = 512, 8, 128
+    x = rng.standard_normal((T, Hkv, D), dtype=np.float32)
+    x = np.where(rng.random(x.shape) < 0.01, x * 8, x).astype(src)
+    x[3, 2] = 0
+    x[7, 1, 5] = 900
+    bits = x.view(np.uint16) if src == np.float16 else x
+    codes, scales = oracle.fp8_quantise_rows(bits, nthreads=4)
+    N, bs = T // 4 + 3, 4
+    slots = rng.permutation(N * bs)[:T].astype(np.int32)
+    kc = np.zeros((N, bs, Hkv, D), np.uint8)
+    vc = np.zeros_like(kc)
+    ks = np.zeros((N, bs, Hkv), np.float32)
+    vs = np.zeros_like(ks)
+    oracle.reshape_and_cache(bits, bits, kc, vc, slots, ks, vs)
+    assert np.array_equal(kc.reshape(-1, Hkv, D)[slots], codes)
+    assert np.array_equal(ks.reshape(-1, Hkv)[slots], scales)
+    xf = x.astype(np.float32)
+    amax = np.abs(xf).max(-1)
+    sc = np.where(amax == 0, np.float32(1), amax / np.float32(448)).astype(np.float32)
+    assert np.array_equal(scales, sc)
+    assert np.array_equal(codes, torch_fp8_encode(xf / sc[..., None]))
+    assert scales[3, 2] == 1.0 and not codes[3, 2].any()
+
+
+def test_decode_scale_zero_is_mean_of_v(oracle):
+    """scale 0: every key weighs e^0 = 1 (the reference's m0 = -1e30 start makes
+    the first max 0), so each output is the mean of V over the context."""
+    rng = np.random.default_rng(12)
+    H, Hkv, D, bs = 6, 2, 32, 8
+    lay, q, k, v = _random_case(rng, H, Hkv, D, bs, [1, 9, 40])
+    out = oracle.paged_decode(q * 30, k, v, lay.block_tables, lay.context_lens, 0.0)
+    for s, n in enumerate(lay.context_lens):
+        vv = gather_tokens(v, lay.block_tables[s], int(n), bs)
+        for h in range(H):
+            np.testing.assert_allclose(out[s, h], vv[:, h // 3].mean(0), rtol=1e-6, atol=1e-6)
+
+
 def test_copy_and_swap_blocks(oracle):
     rng = np.random.default_rng(10)
     L, N = 3, 12

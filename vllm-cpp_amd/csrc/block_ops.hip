@@ -158,16 +158,14 @@ constexpr int64_t kCopyWorkgroups = int64_t(256) * 16;
 // per request and need more in flight (8: 19 GB/s, 16: 38 GB/s, 24-32:
 // 54-57 GB/s).  More workgroups than these slow a decode beside the swap far
 // more than they speed the swap (16 writing workgroups: decode 1.6x slower).
-// VKV_SWAP_WORKGROUPS overrides both (tuning).
+// Building with -DVKV_SWAP_WORKGROUPS=<n> fixes both (a tuning switch).
+#ifndef VKV_SWAP_WORKGROUPS
+#define VKV_SWAP_WORKGROUPS 0
+#endif
 constexpr int64_t kSwapOutWorkgroups = 8;
 constexpr int64_t kSwapInWorkgroups = 24;
 int64_t swap_workgroups(int32_t direction) {
-    static const int64_t v = [] {
-        const char* e = std::getenv("VKV_SWAP_WORKGROUPS");
-        const long n = e ? std::atol(e) : 0;
-        return n > 0 ? int64_t(n) : int64_t(0);
-    }();
-    if (v > 0) return v;
+    if (VKV_SWAP_WORKGROUPS > 0) return VKV_SWAP_WORKGROUPS;
     return direction == 0 ? kSwapOutWorkgroups : kSwapInWorkgroups;
 }
 

@@ -11,6 +11,7 @@
 #include <cstdio>
 #include <cstring>
 #include <mutex>
+#include <thread>
 #include <unordered_set>
 #include <vector>
 
@@ -49,32 +50,42 @@ constexpr int kMaxHeadDim = 1024;
 constexpr int kMaxBlockSize = 1 << 20;
 
 // Library-owned workspaces, one per (device, stream): calls on different
-// streams never share one, calls on one stream are ordered by it.  A buffer
-// only grows.  An outgrown buffer is retired, not freed: queued work or a
-// captured graph may still use it, and freeing would need a device-wide
-// synchronisation.  Growth doubles, so the retired buffers of a stream never
-// exceed its current one.  A stream that is being captured cannot grow its
-// buffer (that would allocate inside the capture): the call fails instead.
+// streams never share one, calls on one stream are ordered by it.  The
+// per-thread stream handle (hipStreamPerThread) names a different stream in
+// every thread, so its buffers are kept per (device, thread).  A buffer only
+// grows.  An outgrown buffer is retired, not freed: queued work or a captured
+// graph may still use it, and freeing would need a synchronisation.  Growth
+// doubles, so the retired buffers of a stream never exceed its current one.
+// A stream that is being captured cannot grow its buffer (that would allocate
+// inside the capture): the call fails instead.  vkv_release_workspace frees a
+// stream's buffers (the caller does so before destroying the stream, so that
+// a new stream created at the same address starts with none).
 struct StreamWorkspace {
     int device;
     hipStream_t stream;
+    std::thread::id thread;  // hipStreamPerThread only; default otherwise
     void* ptr;
     size_t bytes;
+    std::vector<void*> retired;
 };
 std::mutex g_ws_mutex;
 std::vector<StreamWorkspace> g_ws;
-std::vector<void*> g_ws_retired;
+
+std::thread::id stream_thread(hipStream_t stream) {
+    return stream == hipStreamPerThread ? std::this_thread::get_id() : std::thread::id();
+}
 
 int library_workspace(size_t need, hipStream_t stream, void** out) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return hip_status(e, "hipGetDevice");
+    const std::thread::id th = stream_thread(stream);
     std::lock_guard<std::mutex> lock(g_ws_mutex);
     StreamWorkspace* w = nullptr;
     for (StreamWorkspace& x : g_ws)
-        if (x.device == dev && x.stream == stream) w = &x;
+        if (x.device == dev && x.stream == stream && x.thread == th) w = &x;
     if (!w) {
-        g_ws.push_back(StreamWorkspace{dev, stream, nullptr, 0});
+        g_ws.push_back(StreamWorkspace{dev, stream, th, nullptr, 0, {}});
         w = &g_ws.back();
     }
     if (w->bytes < need) {
@@ -99,7 +110,7 @@ int library_workspace(size_t need, hipStream_t stream, void** out) {
             (void)hipFree(p);
             return hip_status(e, "hipMemsetAsync (workspace header)");
         }
-        if (w->ptr) g_ws_retired.push_back(w->ptr);
+        if (w->ptr) w->retired.push_back(w->ptr);
         w->ptr = p;
         w->bytes = sz;
     }
@@ -289,6 +300,35 @@ extern "C" {
 const char* vkv_last_error(void) { return g_last_error; }
 
 int vkv_abi_version(void) { return 3; }
+
+int vkv_release_workspace(vkv_stream_t stream_handle) {
+    const hipStream_t stream = reinterpret_cast<hipStream_t>(stream_handle);
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_status(e, "hipGetDevice");
+    const std::thread::id th = stream_thread(stream);
+    std::vector<void*> bufs;
+    {
+        std::lock_guard<std::mutex> lock(g_ws_mutex);
+        for (size_t i = 0; i < g_ws.size(); ++i) {
+            StreamWorkspace& x = g_ws[i];
+            if (x.device != dev || x.stream != stream || x.thread != th) continue;
+            bufs = std::move(x.retired);
+            if (x.ptr) bufs.push_back(x.ptr);
+            g_ws.erase(g_ws.begin() + long(i));
+            break;
+        }
+    }
+    if (bufs.empty()) return VKV_OK;
+    // the stream's queued calls may still use the buffers
+    e = hipStreamSynchronize(stream);
+    if (e != hipSuccess) return hip_status(e, "hipStreamSynchronize (vkv_release_workspace)");
+    for (void* b : bufs) {
+        e = hipFree(b);
+        if (e != hipSuccess) return hip_status(e, "hipFree (vkv_release_workspace)");
+    }
+    return VKV_OK;
+}
 
 int vkv_reshape_and_cache(const vkv_append_params* p, vkv_stream_t stream) {
     int rc = check_append(p);

@@ -223,4 +223,18 @@ __device__ __forceinline__ float fp8_scale_from_amax(float amax) {
     return amax == 0.0f ? 1.0f : amax / 448.0f;
 }
 
+// Attention logit scale in the log2 domain (scale * log2 e), as the decode
+// and prefill kernels take it.  A scale of magnitude below 2^-100 (zero
+// included) runs as +-2^-100: the reference then weights every key
+// e^(dot * 0 - 0) = 1, i.e. returns the mean of V (src/attention/
+// paged_attention.cu:47-51,75 with m0 = -1e30), and exp2((dot - max) * 2^-100)
+// rounds to exactly 1 for |dot - max| < 2^75, while the kernels' -inf running-
+// max start and masked keys still weigh 0 instead of -inf * 0 = NaN.
+inline float logit_scale_log2(float scale) {
+    constexpr float kMinLog2Scale = 0x1p-100f;
+    const float s = scale * 1.4426950408889634f;
+    if (s < kMinLog2Scale && s > -kMinLog2Scale) return s < 0.0f ? -kMinLog2Scale : kMinLog2Scale;
+    return s;  // NaN stays NaN, as in the reference
+}
+
 }  // namespace vkv

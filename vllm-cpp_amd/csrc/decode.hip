@@ -802,15 +802,12 @@ __global__ __launch_bounds__(DT ? DT : 1024) void decode_reduce_kernel(DecodeArg
     *out = static_cast<IO>(r);
 }
 
-// VKV_DECODE_MFMA=0 in the environment selects the VALU variant everywhere
-// (read once per process).
-int mfma_enabled() {
-    static const int v = [] {
-        const char* e = std::getenv("VKV_DECODE_MFMA");
-        return (e && e[0] == '0') ? 0 : 1;
-    }();
-    return v;
-}
+// Building with -DVKV_DECODE_MFMA=0 selects the VALU QK^T variant everywhere
+// (an A/B switch for measurements; the shipped library uses matrix cores).
+#ifndef VKV_DECODE_MFMA
+#define VKV_DECODE_MFMA 1
+#endif
+constexpr int mfma_enabled() { return VKV_DECODE_MFMA; }
 
 template <typename IO, int KVT, int D, int G>
 void launch_g(DecodeArgs& args, int grid_x, int grid_y, int grid_z, size_t lds, hipStream_t st) {
@@ -1025,7 +1022,7 @@ int launch_rows(const vkv_decode_params* p, const DecodePlan& plan, void* worksp
     for (int i = 0; i < kMaxPartitionCandidates; ++i) a.cands[i] = plan.candidates[i];
     a.wave_slots = 0;  // set per variant at launch
     a.level_waves = 0;
-    a.scale_log2 = p->scale * kLog2e;
+    a.scale_log2 = logit_scale_log2(p->scale);
     a.accumulate = p->accumulate;
 
     const int G = p->num_heads / p->num_kv_heads;

@@ -429,14 +429,13 @@ __device__ __forceinline__ void run_partitions(const DecodeArgs& a, const int it
     }
 }
 
-// VKV_DECODE_BLOCKS_PER_CU=<n> overrides the grid's workgroups per CU
-// (tuning; default: as many as are resident at once).
+// Building with -DVKV_DECODE_BLOCKS_PER_CU=<n> fixes the grid's workgroups per
+// CU (a tuning switch; default: as many as are resident at once).
+#ifndef VKV_DECODE_BLOCKS_PER_CU
+#define VKV_DECODE_BLOCKS_PER_CU 0
+#endif
 inline int blocks_per_cu(int fits) {
-    static const int v = [] {
-        const char* e = std::getenv("VKV_DECODE_BLOCKS_PER_CU");
-        return e ? std::atoi(e) : 0;
-    }();
-    return v > 0 ? v : fits;
+    return VKV_DECODE_BLOCKS_PER_CU > 0 ? VKV_DECODE_BLOCKS_PER_CU : fits;
 }
 
 inline int device_cu_count() {

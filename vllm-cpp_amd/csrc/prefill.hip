@@ -1185,7 +1185,7 @@ int launch_prefill_mfma(const vkv_prefill_params* p, void* item_space, int32_t* 
     const int rpi = rows_per_item(p);
     a.qblocks = int(max_row_blocks(p));
     a.num_seqs = p->num_seqs;
-    a.scale_log2 = p->scale * 1.4426950408889634f;
+    a.scale_log2 = logit_scale_log2(p->scale);
     int32_t* count = static_cast<int32_t*>(item_space);
     int2* items = reinterpret_cast<int2*>(static_cast<char*>(item_space) + 256);
     a.items = items;

@@ -16,10 +16,14 @@ SwapPreemption::SwapPreemption(BlockManager& bm, KVCache& cache, void* host_pool
     VLLM_HIP_CHECK(hipMalloc(&dev_pairs_, dev_pairs_cap_ * sizeof(int32_t)));
     VLLM_HIP_CHECK(hipHostMalloc(reinterpret_cast<void**>(&host_pairs_), dev_pairs_cap_ * sizeof(int32_t)));
     VLLM_HIP_CHECK(hipEventCreateWithFlags(&uploaded_, hipEventDisableTiming));
+    VLLM_HIP_CHECK(hipEventCreateWithFlags(&swapped_, hipEventDisableTiming));
 }
 
 SwapPreemption::~SwapPreemption() {
+    // the swap kernels read dev_pairs_: let them finish before it is freed
+    if (swap_enqueued_) (void)hipEventSynchronize(swapped_);
     if (upload_pending_) (void)hipEventSynchronize(uploaded_);
+    (void)hipEventDestroy(swapped_);
     (void)hipEventDestroy(uploaded_);
     (void)hipHostFree(host_pairs_);
     (void)hipFree(dev_pairs_);
@@ -40,6 +44,9 @@ void SwapPreemption::enqueue_swap(const std::vector<int32_t>& pairs, int32_t dir
     if (pairs.size() > dev_pairs_cap_) throw std::length_error("SwapPreemption: more pairs than the pool has blocks");
     // The pinned staging buffer may still feed the previous upload.
     if (upload_pending_) VLLM_HIP_CHECK(hipEventSynchronize(uploaded_));
+    // The previous swap (perhaps on another stream) may still read dev_pairs_
+    // and the blocks this one reuses: order this one after it.
+    if (swap_enqueued_) VLLM_HIP_CHECK(hipStreamWaitEvent(stream, swapped_, 0));
     std::copy(pairs.begin(), pairs.end(), host_pairs_);
     VLLM_HIP_CHECK(
         hipMemcpyAsync(dev_pairs_, host_pairs_, pairs.size() * sizeof(int32_t), hipMemcpyHostToDevice, stream));
@@ -47,6 +54,12 @@ void SwapPreemption::enqueue_swap(const std::vector<int32_t>& pairs, int32_t dir
     upload_pending_ = true;
     // the swap kernel after the upload on the same stream reads the list
     cache_.swap_blocks(host_pool_, int32_t(bm_.num_total_cpu_blocks()), dev_pairs_, int32_t(n), direction, stream);
+    VLLM_HIP_CHECK(hipEventRecord(swapped_, stream));
+    swap_enqueued_ = true;
+}
+
+void SwapPreemption::wait_swaps(hipStream_t stream) {
+    if (swap_enqueued_) VLLM_HIP_CHECK(hipStreamWaitEvent(stream, swapped_, 0));
 }
 
 bool SwapPreemption::preempt_one(std::vector<SwappableSequence*>& running, std::deque<SwappableSequence*>& waiting,

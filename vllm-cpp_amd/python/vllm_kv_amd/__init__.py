@@ -38,7 +38,7 @@ EXPORTED = [
     "vkv_paged_prefill",
     "vkv_copy_blocks", "vkv_check_block_pairs_host", "vkv_swap_host_block_bytes",
     "vkv_swap_blocks", "vkv_rope_reshape_and_cache", "vkv_rope_cos_sin_host",
-    "vkv_kv_block_bytes", "vkv_kv_pool_num_blocks",
+    "vkv_kv_block_bytes", "vkv_kv_pool_num_blocks", "vkv_release_workspace",
 ]
 
 
@@ -176,6 +176,8 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
                                     ctypes.c_int32, ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p,
                                     ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]
     lib.vkv_swap_blocks.restype = ctypes.c_int
+    lib.vkv_release_workspace.argtypes = [ctypes.c_void_p]
+    lib.vkv_release_workspace.restype = ctypes.c_int
     _lib = lib
     return lib
 
@@ -207,11 +209,23 @@ def _ptr(t) -> Optional[int]:
     return None if t is None else t.data_ptr()
 
 
+STREAM_PER_THREAD = 2  # the value of the hipStreamPerThread handle
+
+
 def _stream(stream) -> Optional[int]:
+    """A torch stream (None: the current one) or a raw stream handle (int)."""
+    if isinstance(stream, int):
+        return stream
     torch = _torch()
     if stream is None:
         stream = torch.cuda.current_stream()
     return stream.cuda_stream
+
+
+def release_workspace(stream=None) -> None:
+    """vkv_release_workspace: free the library's workspace buffers of `stream`
+    on the current device (after synchronising it)."""
+    check(load().vkv_release_workspace(_stream(stream)))
 
 
 def _require_cuda(*ts) -> None:
