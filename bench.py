@@ -404,7 +404,19 @@ def suite_c3_prefill_only(dev, steps, warmup):
                           multi_token_only=True)
 
     _warm(attn, warmup)
-    t = _events_ms(attn, steps, stream)
+    t_kernel_list = _events_ms(attn, steps, stream)
+    # the same call with the host-built work list (an engine builds it once per
+    # step beside its other metadata, for every layer): the headline of the row
+    words = vkv.prefill_work_list(out, q, kc, vc, bt, cl, qsl, int(ql.max()), cfg.scale, qsl_np,
+                                  lay.context_lens[:npf])
+    wl = torch.from_numpy(words).to(dev)
+
+    def attn_listed():
+        vkv.paged_prefill(out, q, kc, vc, bt, cl, qsl, int(ql.max()), cfg.scale, stream=stream,
+                          multi_token_only=True, work_list=wl)
+
+    _warm(attn_listed, warmup)
+    t = _events_ms(attn_listed, steps, stream)
     keys = sum(int(cfg.prior_lens[s]) * int(ql[s]) + int(ql[s]) * (int(ql[s]) + 1) // 2 for s in range(npf))
     flops = 4.0 * D * H * keys
     tf = flops / (t[0] * 1e-3) / 1e12
@@ -416,9 +428,12 @@ def suite_c3_prefill_only(dev, steps, warmup):
     all_slots = torch.arange(lay.num_blocks * bs, dtype=torch.int32, device=dev)
     vkv.reshape_and_cache(kc.reshape(-1, Hkv, D), vc.reshape(-1, Hkv, D), k8, v8, all_slots, ks8, vs8)
 
+    wl8 = torch.from_numpy(vkv.prefill_work_list(out, q, k8, v8, bt, cl, qsl, int(ql.max()), cfg.scale, qsl_np,
+                                                 lay.context_lens[:npf], key_scales=ks8, value_scales=vs8)).to(dev)
+
     def attn8():
         vkv.paged_prefill(out, q, k8, v8, bt, cl, qsl, int(ql.max()), cfg.scale, key_scales=ks8, value_scales=vs8,
-                          stream=stream, multi_token_only=True)
+                          stream=stream, multi_token_only=True, work_list=wl8)
 
     _warm(attn8, warmup)
     t8 = _events_ms(attn8, steps, stream)
@@ -440,6 +455,8 @@ def suite_c3_prefill_only(dev, steps, warmup):
     return {"row": "C3 prefill sequences alone", "workload": "the 8 x 512-token chunks of C3 (prior U[0,2048]), "
                                                           "one vkv_paged_prefill call with multi_token_only = 1",
             "us_median": round(t[0] * 1e3, 2), "us_p10_p90": [round(t[1] * 1e3, 2), round(t[2] * 1e3, 2)],
+            "work_list": "host-built (vkv_prefill_work_list_host), built once before the timed calls",
+            "us_median_in_kernel_list": round(t_kernel_list[0] * 1e3, 2),
             "gflop": round(flops / 1e9, 2), "tflops": round(tf, 1),
             "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": 2500.0, "unit": "TFLOP/s",
                          "frac": round(tf / 2500.0, 4)},

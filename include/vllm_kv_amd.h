@@ -322,10 +322,30 @@ typedef struct vkv_prefill_params {
     int32_t multi_token_only;   /* 1: no sequence has q_len 1 (see above); 0: not known */
     void* workspace;            /* optional, see above */
     size_t workspace_bytes;
+    const int32_t* work_list;   /* optional device copy of vkv_prefill_work_list_host()'s words for this call */
+    int32_t work_list_words;    /* its length; 0 with work_list NULL: the kernels order the work themselves */
 } vkv_prefill_params;
 
 size_t vkv_paged_prefill_workspace_size(const vkv_prefill_params* p);
 int vkv_paged_prefill(const vkv_prefill_params* p, vkv_stream_t stream);
+
+/* Host-built work list of the matrix-core prefill kernels.  No counterpart in
+ * the reference, whose prefill is one decode per token (src/core/engine.cpp:
+ * 157-164).  From host copies of the call's query_start_loc and context_lens
+ * and the shape fields of *p, it lists the call's work items (blocks of query
+ * rows of one sequence and kv head) longest first, the order in which the
+ * kernels' persistent workgroups claim them.  With the words
+ * copied to device memory and passed as p->work_list / work_list_words, the
+ * kernels skip ordering the items themselves: an engine builds it once per
+ * step beside its other metadata, for every layer of the step.  The list must
+ * come from the same lengths and shape as the call (items past the call's
+ * sequences are skipped, so a stale list gives wrong rows but reads nothing out
+ * of bounds).  Returns the number of int32 words; writes them when out is not
+ * NULL and capacity_words suffices (else returns -2); 0 when the call's shape
+ * runs without a list (everything but fp16 queries at head_dim 64/128 over fp16
+ * caches or FP8 caches at 128); -1 for a NULL argument. */
+int64_t vkv_prefill_work_list_host(const vkv_prefill_params* p, const int32_t* host_query_start_loc,
+                                   const int32_t* host_context_lens, int32_t* out, int64_t capacity_words);
 
 /* -------------------------------------------------------------------------
  * Block copy (copy-on-write on fork) and swap (HBM <-> pinned host).

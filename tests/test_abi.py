@@ -25,7 +25,7 @@ def test_library_exports_every_declared_symbol(vkv):
     lib = vkv.load()
     for name in declared_functions():
         assert hasattr(lib, name), name
-    assert lib.vkv_abi_version() == vkv.ABI_VERSION == 3
+    assert lib.vkv_abi_version() == vkv.ABI_VERSION == 4
 
 
 def test_struct_sizes_match_header_layout(vkv):
@@ -35,7 +35,8 @@ def test_struct_sizes_match_header_layout(vkv):
     assert ctypes.sizeof(vkv.BlockPlane) == 24
     assert ctypes.sizeof(vkv.RopeAppendParams) == 3 * 8 + 3 * 8 + 2 * 8 + 2 * 4 + 5 * 8 + 8 * 4
     # 9 pointers, query_stride, 14 int32/float, workspace pointer and size
-    assert ctypes.sizeof(vkv.PrefillParams) == 9 * 8 + 8 + 14 * 4 + 8 + 8
+    assert ctypes.sizeof(vkv.PrefillParams) == 9 * 8 + 8 + 14 * 4 + 8 + 8 + 8 + 8  # work_list, words + pad
+    assert vkv.PrefillParams.work_list.offset == 152
     assert vkv.PrefillParams.multi_token_only.offset == 132
     assert vkv.PrefillParams.workspace.offset == 136
 
@@ -195,3 +196,58 @@ def test_prefill_argument_errors_and_workspace(vkv):
     p = _prefill_params(vkv, workspace=8, workspace_bytes=need)
     assert lib.vkv_paged_prefill(ctypes.byref(p), None) == -5       # misaligned
     assert lib.vkv_paged_prefill_workspace_size(ctypes.byref(_prefill_params(vkv, head_dim=0))) == 0
+
+
+@pytest.mark.parametrize("shape", [(28, 4, 128, 32, 1, 1), (32, 8, 128, 16, 1, 2), (16, 2, 64, 16, 1, 1),
+                                   (32, 2, 128, 16, 1, 1)])
+def test_prefill_work_list_host(vkv, shape):
+    """vkv_prefill_work_list_host (no GPU): every work item (sequence, row block,
+    kv head) of the call exactly once, longest first; no list for shapes the
+    matrix-core kernels do not run; capacity and argument errors."""
+    import numpy as np
+    H, Hkv, D, bs, io, kv = shape
+    rng = np.random.default_rng(H + D)
+    q_lens = np.concatenate([rng.integers(2, 700, 9), [1, 1, 1]]).astype(np.int32)
+    prior = rng.integers(0, 3000, q_lens.size).astype(np.int32)
+    qsl = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    ctx = (prior + q_lens).astype(np.int32)
+    mb = int((ctx.max() + bs - 1) // bs)
+    p = _prefill_params(vkv, num_seqs=q_lens.size, num_query_tokens=int(qsl[-1]), max_query_len=int(q_lens.max()),
+                        num_heads=H, num_kv_heads=Hkv, head_dim=D, block_size=bs, max_blocks_per_seq=mb,
+                        io_dtype=io, kv_dtype=kv)
+    lib = vkv.load()
+    n = lib.vkv_prefill_work_list_host(ctypes.byref(p), qsl.ctypes.data, ctx.ctypes.data, None, 0)
+    G = H // Hkv
+    rows = 256 if D == 128 else 512
+    want = set()
+    tiles = {}
+    for s in range(q_lens.size):
+        if q_lens[s] < 2:
+            continue
+        nb = (int(q_lens[s]) * G + rows - 1) // rows
+        for b in range(nb):
+            last = min(int(q_lens[s]), ((b + 1) * rows - 1) // G + 1)
+            t = (int(prior[s]) + last + 63) // 64
+            for k in range(Hkv):
+                want.add((s, b * Hkv + k))
+                tiles[(s, b * Hkv + k)] = t
+    assert n == 32 + 2 * len(want)
+    words = np.zeros(n, np.int32)
+    assert lib.vkv_prefill_work_list_host(ctypes.byref(p), qsl.ctypes.data, ctx.ctypes.data,
+                                          words.ctypes.data, n - 1) == -2
+    assert lib.vkv_prefill_work_list_host(ctypes.byref(p), qsl.ctypes.data, ctx.ctypes.data,
+                                          words.ctypes.data, n) == n
+    assert words[0] == 1 and words[1] == 0 and words[2] == len(want)
+    items = words[32:].reshape(-1, 2)
+    got = [tuple(map(int, it)) for it in items]
+    assert sorted(got) == sorted(want) and len(got) == len(set(got))
+    t = [tiles[it] for it in got]
+    assert t == sorted(t, reverse=True)  # longest first
+    # shapes without the list: fp32 queries, FP8 at head_dim 64
+    p32 = _prefill_params(vkv, io_dtype=0, kv_dtype=0)
+    assert lib.vkv_prefill_work_list_host(ctypes.byref(p32), qsl.ctypes.data, ctx.ctypes.data, None, 0) == 0
+    p8 = _prefill_params(vkv, head_dim=64, kv_dtype=2)
+    assert lib.vkv_prefill_work_list_host(ctypes.byref(p8), qsl.ctypes.data, ctx.ctypes.data, None, 0) == 0
+    assert lib.vkv_prefill_work_list_host(ctypes.byref(p), None, ctx.ctypes.data, None, 0) == -1
+    # a negative length is refused before any launch
+    assert lib.vkv_paged_prefill(ctypes.byref(_prefill_params(vkv, work_list_words=-1)), None) == -2

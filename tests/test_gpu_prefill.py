@@ -76,17 +76,26 @@ def _threads():
     (32, 1, 64, 16, [200, 2], [30, 0]),
 ])
 def test_prefill_vs_oracle(vkv, oracle, cuda, kvt, H, Hkv, D, bs, q_lens, prior):
+    """Against the oracle, with the kernels' own work ordering and with the
+    host-built work list (vkv_prefill_work_list_host) of the same call."""
     import torch
     lay, ctx, qsl, q, k, v, scale = _case(H, Hkv, D, bs, q_lens, prior, sum(q_lens) + H)
     Tq = q.shape[0]
     (kc, vc, ks, vs), (hk, hv, hks, hvs) = _cache(vkv, cuda, kvt, k, v)
     ref = oracle.paged_prefill(q.astype(np.float32), hk, hv, lay.block_tables, ctx, qsl, scale,
                                key_scales=hks, value_scales=hvs, nthreads=_threads())
-    out = torch.zeros((Tq, H, D), dtype=torch.float16, device=cuda)
-    vkv.paged_prefill(out, to_dev(q, cuda), kc, vc, to_dev(lay.block_tables, cuda), to_dev(ctx, cuda),
-                      to_dev(qsl, cuda), int(max(q_lens)), scale, key_scales=ks, value_scales=vs)
-    torch.cuda.synchronize()
-    assert_close(to_np(out).astype(np.float32), ref, F16_ATOL, F16_RTOL, f"prefill ({kvt} cache)")
+    args = (to_dev(q, cuda), kc, vc, to_dev(lay.block_tables, cuda), to_dev(ctx, cuda), to_dev(qsl, cuda),
+            int(max(q_lens)), scale)
+    for listed in (False, True):
+        out = torch.zeros((Tq, H, D), dtype=torch.float16, device=cuda)
+        wl = None
+        if listed:
+            words = vkv.prefill_work_list(out, *args, qsl, ctx, key_scales=ks, value_scales=vs)
+            wl = to_dev(words, cuda) if words.size else None
+        vkv.paged_prefill(out, *args, key_scales=ks, value_scales=vs, work_list=wl)
+        torch.cuda.synchronize()
+        assert_close(to_np(out).astype(np.float32), ref, F16_ATOL, F16_RTOL,
+                     f"prefill ({kvt} cache, {'host' if listed else 'in-kernel'} work list)")
 
 
 @pytest.mark.parametrize("H,Hkv,D,bs", [(28, 4, 128, 32), (16, 2, 64, 16)])  # groups 7 and 8
@@ -176,8 +185,14 @@ def test_prefill_mixed_config3(vkv, oracle, cuda, kvt):
         hk, hv, hks, hvs = to_np(kc), to_np(vc), to_np(ks), to_np(vs)
     del k16, v16
     out = torch.zeros((Tq, H, D), dtype=torch.float16, device=cuda)
-    vkv.paged_prefill(out, q, kc, vc, to_dev(lay.block_tables, cuda), to_dev(lay.context_lens, cuda),
-                      to_dev(qsl, cuda), int(cfg.q_lens.max()), cfg.scale, key_scales=ks, value_scales=vs)
+    args = (q, kc, vc, to_dev(lay.block_tables, cuda), to_dev(lay.context_lens, cuda), to_dev(qsl, cuda),
+            int(cfg.q_lens.max()), cfg.scale)
+    vkv.paged_prefill(out, *args, key_scales=ks, value_scales=vs)
+    # the same call with the host-built work list
+    out2 = torch.zeros_like(out)
+    words = vkv.prefill_work_list(out2, *args, qsl, lay.context_lens, key_scales=ks, value_scales=vs)
+    assert words.size > 0
+    vkv.paged_prefill(out2, *args, key_scales=ks, value_scales=vs, work_list=to_dev(words, cuda))
     torch.cuda.synchronize()
     got = to_np(out).astype(np.float32)
     ref = oracle.paged_prefill(to_np(q).astype(np.float32), hk, hv, lay.block_tables, lay.context_lens, qsl,
@@ -185,6 +200,8 @@ def test_prefill_mixed_config3(vkv, oracle, cuda, kvt):
     npf = int((cfg.q_lens > 1).sum())
     assert int(qsl[npf]) == 4096 and Tq == 4216
     assert_close(got, ref, F16_ATOL, F16_RTOL, f"C3 ({kvt} cache): all 4096 chunk rows and 120 decode rows")
+    # the work list changes the order of the items, not a single result bit
+    assert torch.equal(out.view(torch.int16), out2.view(torch.int16))
 
 
 @pytest.mark.parametrize("kvt", ["f16", "fp8"])

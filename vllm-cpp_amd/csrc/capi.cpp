@@ -174,6 +174,10 @@ int check_prefill(const vkv_prefill_params* p) {
     if (p->max_context_len < 0) return fail(VKV_ERR_SHAPE, "max_context_len < 0");
     if (p->multi_token_only != 0 && p->multi_token_only != 1)
         return fail(VKV_ERR_SHAPE, "multi_token_only must be 0 or 1");
+    if (p->work_list_words < 0 || (p->work_list_words > 0 && !p->work_list))
+        return fail(VKV_ERR_SHAPE, "work_list_words must be >= 0, with a work_list when > 0");
+    if (p->work_list && (reinterpret_cast<uintptr_t>(p->work_list) & 7u))
+        return fail(VKV_ERR_ALIGN, "work_list must be 8-byte aligned");
     // Shape/dtype rules are those of decode; the decode rows are the
     // sequences (mixed matrix-core path) or the query tokens (row path).
     const vkv_decode_params d = vkv::prefill_as_decode(p, vkv::prefill_mfma_supported(p));
@@ -299,7 +303,12 @@ extern "C" {
 
 const char* vkv_last_error(void) { return g_last_error; }
 
-int vkv_abi_version(void) { return 3; }
+int vkv_abi_version(void) { return 4; }
+
+int64_t vkv_prefill_work_list_host(const vkv_prefill_params* p, const int32_t* host_query_start_loc,
+                                   const int32_t* host_context_lens, int32_t* out, int64_t capacity_words) {
+    return vkv::prefill_work_list_host(p, host_query_start_loc, host_context_lens, out, capacity_words);
+}
 
 int vkv_release_workspace(vkv_stream_t stream_handle) {
     const hipStream_t stream = reinterpret_cast<hipStream_t>(stream_handle);

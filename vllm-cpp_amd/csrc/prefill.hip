@@ -33,10 +33,18 @@
 // by 16 bytes to spread the banks), dequantised on the way (code x per-token
 // scale, fp32 -> fp16).  Block ids of the sequence are cached in LDS, 1024 at
 // a time.
+#include <algorithm>
 #include <type_traits>
+#include <vector>
 
 #include "common.hpp"
 #include "launch.hpp"
+
+// Building with -DVKV_PREFILL_W64=0 runs fp16 caches at head_dim 128 on the
+// 8-wave kernel instead of the one-wave-per-SIMD kernel (an A/B switch).
+#ifndef VKV_PREFILL_W64
+#define VKV_PREFILL_W64 1
+#endif
 
 namespace vkv {
 namespace {
@@ -84,6 +92,11 @@ struct PrefillArgs {
     int32_t* inline_claim;
     int32_t rows_per_item;
     int32_t nbins;
+    // host-built work list (vkv_prefill_work_list_host), or nullptr; its claim
+    // counters live in list_claim (the workspace header ints, zero between calls)
+    const int32_t* work_list;
+    int32_t work_list_items;  // items the list's words can hold (bounds every index read from it)
+    int32_t* list_claim;
 };
 
 template <int D, int KVT>
@@ -908,17 +921,21 @@ __device__ __forceinline__ void prefill_block_wide(const PrefillArgs& a, const i
 // keys are distinct, so every workgroup computes the same order; the ranking
 // is quadratic, which at kInlineBlocks blocks is a few hundred LDS reads per
 // thread.  Returns the number of blocks; lblk holds them in order.
-constexpr int kInlineBlocks = 64 * kWideWaves;  // one per thread
+constexpr int kInlineBlocks = 512;
+template <int NT>
 __device__ int inline_row_blocks(const PrefillArgs& a, int2* lblk) {
+    constexpr int NW = NT / 64;
+    constexpr int PER = kInlineBlocks / NT;  // blocks ranked per thread
+    static_assert(kInlineBlocks % NT == 0, "blocks must split evenly over the threads");
     __shared__ int key[kInlineBlocks];
-    __shared__ int wave_tot[kWideWaves];
+    __shared__ int wave_tot[NW];
     __shared__ int carry;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     if (tid == 0) carry = 0;
     __syncthreads();
     // number the blocks: sequences in chunks of one per thread, block counts
     // scanned across the workgroup
-    for (int s0 = 0; s0 < a.num_seqs; s0 += kInlineBlocks) {
+    for (int s0 = 0; s0 < a.num_seqs; s0 += NT) {
         const int s = s0 + tid;
         int q = 0, prior = 0, n = 0;
         if (s < a.num_seqs) {
@@ -941,36 +958,93 @@ __device__ int inline_row_blocks(const PrefillArgs& a, int2* lblk) {
         __syncthreads();
         if (tid == 0) {
             int t = carry;
-            for (int w = 0; w < kWideWaves; ++w) t += wave_tot[w];
+            for (int w = 0; w < NW; ++w) t += wave_tot[w];
             carry = t;
         }
         __syncthreads();
     }
     const int total = carry < kInlineBlocks ? carry : kInlineBlocks;
     // rank, then place (lblk is read before the barrier and written after it)
-    int2 mine = int2{0, 0};
-    int rank = 0;
-    if (tid < total) {
-        const int k = key[tid];
-        mine = lblk[tid];
-        for (int j = 0; j < total; ++j) rank += key[j] < k ? 1 : 0;
+    int2 mine[PER];
+    int rank[PER];
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+        const int i = tid + p * NT;
+        mine[p] = int2{0, 0};
+        rank[p] = 0;
+        if (i < total) {
+            const int k = key[i];
+            mine[p] = lblk[i];
+            for (int j = 0; j < total; ++j) rank[p] += key[j] < k ? 1 : 0;
+        }
     }
     __syncthreads();
-    if (tid < total) lblk[rank] = mine;
+#pragma unroll
+    for (int p = 0; p < PER; ++p)
+        if (tid + p * NT < total) lblk[rank[p]] = mine[p];
     __syncthreads();
     return total;
 }
 
-// Persistent claim loop of the direct-load kernels.
-template <int D, bool FP8>
-__device__ __forceinline__ void wide_items(const PrefillArgs& a, const WideBuffers& buf) {
+// Host-built work list (vkv_prefill_work_list_host): 32 header words (the
+// number of lists nx, then nx item offsets, then nx counts), then the items
+// (s, b * Hkv + kvh) as int2.  A workgroup claims from list blockIdx % nx
+// (workgroups reach the XCDs round robin, so per-XCD lists are possible)
+// through that list's counter, then from the next lists once it is exhausted.
+// The host builds one list (nx = 1), longest first.  Counters: workspace
+// header ints kListClaim0 + 32 x (one 128-byte line each) and kListDone.
+constexpr int kListHeaderWords = 32;
+constexpr int kListMaxXcds = 8;
+constexpr int kListClaim0 = 16;
+constexpr int kListDone = 4;
+__device__ __forceinline__ int list_count(const PrefillArgs& a) {
+    const int n = a.work_list[0];
+    return n < 1 ? 1 : (n > kListMaxXcds ? kListMaxXcds : n);
+}
+__device__ __forceinline__ int claim_listed(const PrefillArgs& a, int& x, int& tried) {
+    const int32_t* wl = a.work_list;
+    const int nx = list_count(a);
+    while (tried < nx) {
+        const int k = atomicAdd(a.list_claim + kListClaim0 + 32 * x, 1);
+        if (k < wl[1 + nx + x]) return wl[1 + x] + k;
+        x = x + 1 < nx ? x + 1 : 0;
+        ++tried;
+    }
+    return -1;
+}
+
+// Persistent claim loop of the direct-load kernels (NT threads): work items
+// from the host-built list, the in-kernel list (small calls) or the list
+// kernel's; item(s, b, kvh) runs one.
+template <int NT, typename Item>
+__device__ __forceinline__ void run_items(const PrefillArgs& a, Item item_fn) {
     __shared__ int claimed;
+    if (a.work_list) {
+        int x = int(blockIdx.x) % list_count(a), tried = 0;  // (thread 0's)
+        for (;;) {
+            if (threadIdx.x == 0) claimed = claim_listed(a, x, tried);
+            __syncthreads();
+            const int it = claimed;
+            __syncthreads();
+            if (it < 0) break;
+            if (it >= a.work_list_items) continue;  // (a list from another call: never read past it)
+            const int2 item = reinterpret_cast<const int2*>(a.work_list + kListHeaderWords)[it];
+            if (unsigned(item.x) < unsigned(a.num_seqs) && item.y >= 0)
+                item_fn(item.x, item.y / a.num_kv_heads, item.y % a.num_kv_heads);
+        }
+        // the last workgroup out returns the counters to zero for the next call
+        if (threadIdx.x == 0 && atomicAdd(a.list_claim + kListDone, 1) == int(gridDim.x) - 1) {
+            for (int i = 0; i < list_count(a); ++i) a.list_claim[kListClaim0 + 32 * i] = 0;
+            a.list_claim[kListDone] = 0;
+        }
+        return;
+    }
     __shared__ int2 lblk[kInlineBlocks];  // inline list: (s, b) of row block i, then in longest-first order
     int* claim = a.inline_list ? a.inline_claim : a.item_count + 1;
     // the first claim travels while the list is built (or its length loaded)
     int first = 0;
     if (threadIdx.x == 0) first = atomicAdd(claim, 1);
-    const int count = a.inline_list ? inline_row_blocks(a, lblk) * a.num_kv_heads : a.item_count[0];
+    const int count = a.inline_list ? inline_row_blocks<NT>(a, lblk) * a.num_kv_heads : a.item_count[0];
     if (threadIdx.x == 0) claimed = first;
     for (;;) {
         __syncthreads();
@@ -985,7 +1059,7 @@ __device__ __forceinline__ void wide_items(const PrefillArgs& a, const WideBuffe
         } else {
             item = a.items[it];
         }
-        prefill_block_wide<D, FP8>(a, item.x, item.y / a.num_kv_heads, item.y % a.num_kv_heads, buf);
+        item_fn(item.x, item.y / a.num_kv_heads, item.y % a.num_kv_heads);
         if (threadIdx.x == 0) claimed = atomicAdd(claim, 1);
     }
     // Every claim of this workgroup has returned (its value decided the exit);
@@ -995,6 +1069,13 @@ __device__ __forceinline__ void wide_items(const PrefillArgs& a, const WideBuffe
         a.inline_claim[0] = 0;
         a.inline_claim[1] = 0;
     }
+}
+
+template <int D, bool FP8>
+__device__ __forceinline__ void wide_items(const PrefillArgs& a, const WideBuffers& buf) {
+    run_items<64 * kWideWaves>(a, [&](int s, int b, int kvh) __attribute__((always_inline)) {
+        prefill_block_wide<D, FP8>(a, s, b, kvh, buf);
+    });
 }
 
 template <int D>
@@ -1010,6 +1091,598 @@ __global__ __launch_bounds__(64 * kWideWaves) void prefill_wide_kernel(PrefillAr
     const WideBuffers buf = {{k0, k1, k2}, {v0, v1, v2}, btc, {nullptr, nullptr, nullptr},
                              {nullptr, nullptr, nullptr}, {nullptr, nullptr, nullptr}};
     wide_items<D, false>(a, buf);
+}
+
+// ---------------------------------------------------------------------------
+// fp16 caches at D = 128, one wave per SIMD: prefill_w64_kernel.
+//
+// The same work items as prefill_wide_kernel<128> (256 (token, head) rows of
+// one sequence and kv head), computed by 4 waves of 64 rows (four 16-row MFMA
+// tiles) instead of 8 waves of 32.  Every K or V operand read from LDS then
+// feeds four MFMAs instead of two, which halves the LDS bytes per FLOP (the
+// operand reads bounded the 8-wave kernel).  A lone wave per SIMD has 512
+// registers: the output and row-sum accumulators live in AGPRs (asm MFMAs,
+// below) and the scores of two steps in VGPRs, so a wave overlaps its own
+// phases: step s's exponentials run on the VALU while step s + 1's Q K^T runs
+// on the matrix pipe, and step s's P V while step s + 2's K operands are read
+// and step s + 1's maxima computed.  K/V tiles reach LDS by direct loads as in
+// the 8-wave kernel, through four stages: with the overlap a wave still reads
+// tile t - 1 after the barrier that publishes tile t + 1, so the loads issued
+// after that barrier (tile t + 3) go to the buffer of tile t - 1, which every
+// wave has left by then.  Tiles whose keys all lie below every row's context
+// run this pipeline; the masked tail tiles run one step at a time.
+constexpr int kW64Waves = 4;
+constexpr int kW64RT = 4;  // 16-row tiles per wave
+constexpr int kW64Stages = 4;
+static_assert(kW64Waves * kW64RT * 16 == Wide<128>::ROWS, "the same items (and work list) as the 8-wave kernel");
+
+struct W64Buffers {
+    char* tiles;  // stage S: K tile at S * 2 * tile bytes, V tile right after it
+    int* btc;
+};
+
+// One 16-byte direct global->LDS load per lane (LDS address lds + 16 lane),
+// in asm: the compiler then does not track these LDS writes, so it neither
+// needs a separate LDS object per stage to tell them from the operand reads
+// nor waits for them (the tile barrier counts them out with s_waitcnt vmcnt).
+// s_nop 0: the wait state between the M0 write and the load reading it.
+__device__ __forceinline__ void dma16(const char* g, const uint32_t lds) {
+    const uint32_t l = __builtin_amdgcn_readfirstlane(lds);  // (wave-uniform; an SGPR operand)
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "s"(l) : "memory", "m0");
+}
+__device__ __forceinline__ uint32_t lds_addr(const char* p) {
+    typedef const __attribute__((address_space(3))) char* lds_cptr;
+    return uint32_t(size_t((lds_cptr)p));
+}
+
+// c_r += A B_r (r = 0..3) on the matrix cores, the accumulators in AGPRs.
+// The compiler's own MFMA selection at one wave per SIMD would put every MFMA
+// result in AGPRs, the scores included, and copy them out for the softmax;
+// asm keeps just these accumulators there.  The compiler inserts no wait
+// states around asm: the leading s_nop covers VALU writes of the B operands
+// (P) just before, and agpr_fence() the AGPR reads that follow.
+__device__ __forceinline__ void mfma4_agpr(float4_t& c0, float4_t& c1, float4_t& c2, float4_t& c3, const half8_t a,
+                                           const half8_t b0, const half8_t b1, const half8_t b2, const half8_t b3) {
+    asm("s_nop 4\n\t"
+        "v_mfma_f32_16x16x32_f16 %0, %4, %5, %0\n\t"
+        "v_mfma_f32_16x16x32_f16 %1, %4, %6, %1\n\t"
+        "v_mfma_f32_16x16x32_f16 %2, %4, %7, %2\n\t"
+        "v_mfma_f32_16x16x32_f16 %3, %4, %8, %3"
+        : "+a"(c0), "+a"(c1), "+a"(c2), "+a"(c3)
+        : "v"(a), "v"(b0), "v"(b1), "v"(b2), "v"(b3));
+}
+
+// Wait states (32) between the asm MFMAs' AGPR writes and any other read of
+// those AGPRs: more than the longest XDL write-to-read distance.  Every
+// accumulator passes through it, so no read can move above it.
+// The accumulators placed in AGPRs once (zero-initialised values would
+// otherwise be re-materialised and copied in at every asm MFMA).
+template <int RT, int DT>
+__device__ __forceinline__ void agpr_pin(float4_t (&o)[RT][DT], float4_t (&l)[RT]) {
+    asm volatile("" : "+a"(l[0]), "+a"(l[1]), "+a"(l[2]), "+a"(l[3]));
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+        asm volatile("" : "+a"(o[r][0]), "+a"(o[r][1]), "+a"(o[r][2]), "+a"(o[r][3]), "+a"(o[r][4]), "+a"(o[r][5]),
+                     "+a"(o[r][6]), "+a"(o[r][7]));
+}
+
+template <int RT, int DT>
+__device__ __forceinline__ void agpr_fence(float4_t (&o)[RT][DT], float4_t (&l)[RT]) {
+    asm volatile("s_nop 15\n\ts_nop 15" : "+a"(l[0]), "+a"(l[1]), "+a"(l[2]), "+a"(l[3]));
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+        asm volatile("" : "+a"(o[r][0]), "+a"(o[r][1]), "+a"(o[r][2]), "+a"(o[r][3]), "+a"(o[r][4]), "+a"(o[r][5]),
+                     "+a"(o[r][6]), "+a"(o[r][7]));
+}
+
+// s_r = A B_r (first k-step: no accumulator) and s_r += A B_r, r = 0..3, for
+// the scores S^T = K Q^T: A = K (VGPRs, from LDS), B = Q (AGPRs, which the
+// MFMAs read directly), s in VGPRs.  Early-clobber outputs: the block writes
+// s_0 before its last MFMA reads A.
+__device__ __forceinline__ void mfma4_first(float4_t& s0, float4_t& s1, float4_t& s2, float4_t& s3, const half8_t a,
+                                            const half8_t b0, const half8_t b1, const half8_t b2, const half8_t b3) {
+    asm("v_mfma_f32_16x16x32_f16 %0, %4, %5, 0\n\t"
+        "v_mfma_f32_16x16x32_f16 %1, %4, %6, 0\n\t"
+        "v_mfma_f32_16x16x32_f16 %2, %4, %7, 0\n\t"
+        "v_mfma_f32_16x16x32_f16 %3, %4, %8, 0"
+        : "=&v"(s0), "=&v"(s1), "=&v"(s2), "=&v"(s3)
+        : "v"(a), "a"(b0), "a"(b1), "a"(b2), "a"(b3));
+}
+__device__ __forceinline__ void mfma4_vacc(float4_t& s0, float4_t& s1, float4_t& s2, float4_t& s3, const half8_t a,
+                                           const half8_t b0, const half8_t b1, const half8_t b2, const half8_t b3) {
+    asm("v_mfma_f32_16x16x32_f16 %0, %4, %5, %0\n\t"
+        "v_mfma_f32_16x16x32_f16 %1, %4, %6, %1\n\t"
+        "v_mfma_f32_16x16x32_f16 %2, %4, %7, %2\n\t"
+        "v_mfma_f32_16x16x32_f16 %3, %4, %8, %3"
+        : "+v"(s0), "+v"(s1), "+v"(s2), "+v"(s3)
+        : "v"(a), "a"(b0), "a"(b1), "a"(b2), "a"(b3));
+}
+
+// Wait states (8, the distance LLVM keeps between this MFMA's result and a
+// VALU read of it) between the asm MFMAs' writes of the scores and their VALU
+// reads, with every score passing through it.
+__device__ __forceinline__ void score_fence(float4_t (&sv)[4][2]) {
+    asm volatile("s_nop 7"
+                 : "+v"(sv[0][0]), "+v"(sv[0][1]), "+v"(sv[1][0]), "+v"(sv[1][1]), "+v"(sv[2][0]), "+v"(sv[2][1]),
+                   "+v"(sv[3][0]), "+v"(sv[3][1]));
+}
+
+// Single MFMAs for hand-placed schedules (each between scheduling barriers):
+// s = A B (no accumulator), s += A B with s in VGPRs and B = Q in AGPRs, and
+// c += A B with c in AGPRs.  No wait states: the schedule keeps every VALU
+// write of an operand at least two instructions ahead of its MFMA.
+__device__ __forceinline__ void mfma_first_v(float4_t& s, const half8_t a, const half8_t b) {
+    asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, 0" : "=&v"(s) : "v"(a), "a"(b));
+}
+__device__ __forceinline__ void mfma_acc_v(float4_t& s, const half8_t a, const half8_t b) {
+    asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+v"(s) : "v"(a), "a"(b));
+}
+__device__ __forceinline__ void mfma_acc_a(float4_t& c, const half8_t a, const half8_t b) {
+    asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+}
+
+// VALU work of the hand-placed slots, also in asm so that it stays where it is
+// written (the compiler orders plain arithmetic freely around scheduling
+// barriers).  w = exp2(x sc - m): v_fma_f32 then v_exp_f32.
+__device__ __forceinline__ float slot_exp2(const float x, const float sc, const float m) {
+    float w;
+    asm volatile("v_fma_f32 %0, %1, %2, -%3\n\tv_exp_f32 %0, %0" : "=&v"(w) : "v"(x), "s"(sc), "v"(m));
+    return w;
+}
+// Two weights rounded to fp16 (nearest even) in one word.  Placed at least
+// two slots after the exps it reads: a trans result (v_exp_f32) needs a wait
+// state before another VALU reads it, and reading it sooner stalls the
+// wave's in-order issue on the exp's latency (measured: a pack right after
+// its exps cost twice as much beside an MFMA).
+__device__ __forceinline__ uint32_t slot_pack(const float lo, const float hi) {
+    uint32_t r;
+    asm volatile("v_cvt_pk_f16_f32 %0, %1, %2" : "=v"(r) : "v"(lo), "v"(hi));
+    return r;
+}
+// max(a, b, c), NaN-propagating like v_maximum3_f32
+__device__ __forceinline__ float slot_max3(const float a, const float b, const float c) {
+    float r;
+    asm volatile("v_maximum3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
+template <int D>
+__device__ __forceinline__ void prefill_block_w64(const PrefillArgs& a, const int s, const int b, const int kvh,
+                                                  const W64Buffers& buf) {
+    using T = DmaTile<D>;
+    constexpr int EB = 2;
+    constexpr int DT = D / 16;  // output dim tiles
+    constexpr int KS = D / 32;  // MFMA k-steps of Q K^T
+    constexpr int RT = kW64RT;
+    constexpr int kRows = kW64Waves * RT * 16;
+    constexpr int NT = 64 * kW64Waves;
+    constexpr int JW = T::INST / kW64Waves;  // direct loads per K (or V) tile and wave
+    constexpr int NLOAD = 2 * JW;            // vector-memory operations per tile and wave
+    static_assert(D == 128 && DT == 8 && RT == 4, "the asm accumulator blocks assume four row tiles, eight dim tiles");
+    static_assert(T::INST % kW64Waves == 0, "the loads of a tile must split evenly over the waves");
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // (scalar: the loads' LDS addresses are)
+    const int col = lane & 15;
+    const int grp = lane >> 4;
+    const int G = a.group;
+    int* btc = buf.btc;
+
+    const int q0 = a.qsl[s];
+    const int qlen = a.qsl[s + 1] - q0;
+    const int nrows = qlen * G;
+    if (qlen < 2 || b * kRows >= nrows) return;  // (the item list holds none of these)
+    const int prior = a.cl[s] - qlen;
+    const int last_row = min(nrows, (b + 1) * kRows) - 1;
+    int kend = prior + last_row / G + 1;  // keys any row of the block may see
+    kend = kend < a.table_tokens ? kend : a.table_tokens;
+    const int ntiles = kend > 0 ? (kend + kBK - 1) / kBK : 0;
+
+    // ---------------- loads of tile t, through block ids held in LDS (as in prefill_block_wide)
+    const int bs_mask = (1 << a.bs_log2) - 1;
+    const uint32_t row_bytes32 = uint32_t(a.num_kv_heads) * D * EB;
+    uint32_t lane_off[JW];
+#pragma unroll
+    for (int j = 0; j < JW; ++j) {
+        const int row = (wave * JW + j) * T::RPI + lane / T::CH;
+        lane_off[j] = uint32_t(kvh) * D * EB + uint32_t(((lane % T::CH) ^ (row % T::CH)) * 16);
+    }
+    const int32_t* table = a.bt + int64_t(s) * a.max_blocks_per_seq;
+    auto load_key = [&](const int t, const int j) __attribute__((always_inline)) {
+        int k = t * kBK + (wave * JW + j) * T::RPI + lane / T::CH;
+        k = k < kend ? k : kend - 1;
+        return k > 0 ? k : 0;
+    };
+    const int nblk = kend > 0 ? ((kend - 1) >> a.bs_log2) + 1 : 1;
+    int win = 0;
+    auto fill_window = [&](const int first) __attribute__((always_inline)) {
+        win = first;
+        const int n = nblk - first < kWideBtc ? nblk - first : kWideBtc;
+        for (int i = tid; i < n; i += NT) {
+            int id = table[first + i];
+            if (a.num_blocks > 0 && unsigned(id) >= unsigned(a.num_blocks)) id = 0;
+            btc[i] = id;
+        }
+    };
+    const uint32_t tiles_lds = lds_addr(buf.tiles);
+    auto kstage = [&](const int st) __attribute__((always_inline)) { return buf.tiles + st * (2 * T::BYTES); };
+    auto vstage = [&](const int st) __attribute__((always_inline)) { return buf.tiles + st * (2 * T::BYTES) + T::BYTES; };
+    // This wave's share of tile t's loads: load j of K (or V) fills LDS bytes
+    // stage base + (JW wave + j) KiB (+ the tile size for V).
+    auto dma_lds = [&](const int st, const int j) __attribute__((always_inline)) {
+        return tiles_lds + uint32_t(st * (2 * T::BYTES) + (wave * JW + j) * 1024);
+    };
+    auto dma_off = [&](const int t, const int j, const int id) __attribute__((always_inline)) {
+        const int k = load_key(t, j);
+        const uint32_t slot = (uint32_t(id) << a.bs_log2) + uint32_t(k & bs_mask);
+        return uint64_t(slot) * row_bytes32 + lane_off[j];
+    };
+    auto dma_id = [&](const int t, const int j) __attribute__((always_inline)) {
+        return btc[(load_key(t, j) >> a.bs_log2) - win];
+    };
+    auto load_tile = [&](const int st, const int t) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < JW; ++j) {
+            const uint64_t off = dma_off(t, j, dma_id(t, j));
+            dma16(a.kc + off, dma_lds(st, j));
+            dma16(a.vc + off, dma_lds(st, j) + T::BYTES);
+        }
+    };
+    // Barrier publishing tile t (its loads landed, tile t + 1's in flight);
+    // the block ids of tile t + 2 are then in the window (every wave has
+    // issued tile t + 1's loads, the last reads of the old window).  The
+    // caller issues the loads of tile t + 2.
+    auto publish_barrier = [&](const int t) __attribute__((always_inline)) {
+        tile_barrier<NLOAD>();
+        const int last = (t + 3) * kBK - 1 < kend - 1 ? (t + 3) * kBK - 1 : kend - 1;
+        if (last > 0 && (last >> a.bs_log2) - win >= kWideBtc) {
+            fill_window(((t + 2) * kBK) >> a.bs_log2);
+            __syncthreads();
+        }
+    };
+
+    fill_window(0);
+    __syncthreads();
+
+
+    // Loads of tiles 0 and 1 (every wave issues its share, also for tiles past
+    // the end, so that the vmcnt counts are exact).
+    load_tile(0, 0);
+    load_tile(1, 1);
+
+    // ---------------- Q (B operand of S^T = K Q^T) and per-row context, loaded
+    // while the first two tiles load.  Row
+    // rho = b * kRows + 16 (RT wave + r) + col is (token rho / G, head rho % G)
+    const bool neg_scale = a.scale_log2 < 0.0f;
+    const float sc = neg_scale ? -a.scale_log2 : a.scale_log2;
+    half8_t qop[RT][KS];
+    int rctx[RT];
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+        const int rho = b * kRows + 16 * RT * wave + 16 * r + col;
+        const bool ok = rho < nrows;
+        const int j = ok ? rho / G : 0;
+        const int h = kvh * G + (ok ? rho - j * G : 0);
+        int c = prior + j + 1;
+        c = c < 0 ? 0 : (c > a.table_tokens ? a.table_tokens : c);
+        rctx[r] = ok ? c : 0;
+        const int64_t qbase = (int64_t(q0) + j) * a.q_stride + int64_t(h) * D;
+#pragma unroll
+        for (int i = 0; i < KS; ++i) {
+            u32x4 w = load16(a.q + (qbase + 32 * i + 8 * grp) * 2);
+            const uint32_t keep = ok ? 0xFFFFFFFFu : 0u;
+            const uint32_t flip = neg_scale ? 0x80008000u : 0u;
+            w = (w ^ u32x4{flip, flip, flip, flip}) & u32x4{keep, keep, keep, keep};
+            qop[r][i] = __builtin_bit_cast(half8_t, w);
+        }
+    }
+
+    const float lazy = kLazy / sc;  // kLazy in raw (unscaled) logit units
+    float m[RT], mlim[RT], msc[RT];
+    float4_t lsum[RT];    // row sums (every element the same), AGPRs
+    float4_t o[RT][DT];   // O^T, AGPRs
+    half8_t kOnes = {1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16};
+    // held in registers from here on: rematerialised by a move right before
+    // an asm MFMA it would lack the VALU-write-to-MFMA-read wait states
+    asm volatile("s_nop 1" : "+v"(kOnes));
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+        m[r] = -INFINITY;
+        mlim[r] = -INFINITY;  // m + lazy
+        msc[r] = 0.0f;        // m * sc, 0 while the row has no key
+        lsum[r] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int t = 0; t < DT; ++t) o[r][t] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    agpr_pin(o, lsum);
+
+    // LDS byte offsets of this lane's operands within a step's K (V) rows, as
+    // in prefill_block_wide.
+    int koff[KS], voff[DT];
+    const int vrow = 4 * grp + (col >> 2);
+#pragma unroll
+    for (int i = 0; i < KS; ++i) koff[i] = T::off(col, 4 * i + grp);
+#pragma unroll
+    for (int t = 0; t < DT; ++t) voff[t] = T::off(vrow, 2 * t + ((col & 3) >> 1)) + 8 * (col & 1);
+
+    auto read_k = [&](const char* kb, half8_t (&kop)[KS][2]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < KS; ++i)
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh)
+                kop[i][hh] = __builtin_bit_cast(half8_t, *reinterpret_cast<const u32x4*>(kb + koff[i] + 16 * hh * T::ROW));
+    };
+    // S^T of a step (asm MFMAs; the scores pass score_fence before any VALU read)
+    auto qk = [&](const half8_t (&kop)[KS][2], float4_t (&sv)[RT][2]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+            mfma4_first(sv[0][hh], sv[1][hh], sv[2][hh], sv[3][hh], kop[0][hh], qop[0][0], qop[1][0], qop[2][0],
+                        qop[3][0]);
+#pragma unroll
+        for (int i = 1; i < KS; ++i)
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh)
+                mfma4_vacc(sv[0][hh], sv[1][hh], sv[2][hh], sv[3][hh], kop[i][hh], qop[0][i], qop[1][i], qop[2][i],
+                           qop[3][i]);
+        score_fence(sv);
+    };
+    auto read_v = [&](const char* vb, half8_t (&vop)[DT]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+            const u32x2 lo = tr_read(vb + voff[t]);
+            const u32x2 hi = tr_read(vb + voff[t] + 16 * T::ROW);
+            vop[t] = __builtin_bit_cast(half8_t, u32x4{lo[0], lo[1], hi[0], hi[1]});
+        }
+    };
+    // causal / context mask: key kbase + 16 hh + 4 grp + e < rctx
+    auto mask = [&](const int kbase, float4_t (&sv)[RT][2]) __attribute__((always_inline)) {
+        bool edge = false;
+#pragma unroll
+        for (int r = 0; r < RT; ++r) edge = edge || kbase + 32 > rctx[r];
+        if (__builtin_amdgcn_ballot_w64(edge)) {
+#pragma unroll
+            for (int r = 0; r < RT; ++r)
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (kbase + 16 * hh + 4 * grp + e >= rctx[r]) sv[r][hh][e] = -INFINITY;
+        }
+    };
+    // This lane's max per row tile; true when some row exceeds its lazy limit
+    auto lane_max = [&](const float4_t (&sv)[RT][2], float (&lmx)[RT]) __attribute__((always_inline)) {
+        bool over = false;
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+            lmx[r] = vmax3(vmax3(sv[r][0][0], sv[r][0][1], sv[r][0][2]), vmax3(sv[r][0][3], sv[r][1][0], sv[r][1][1]),
+                           vmax3(sv[r][1][2], sv[r][1][3], sv[r][1][3]));
+            over = over || lmx[r] > mlim[r];
+        }
+        return over;
+    };
+    // The lazy rescale (rows whose max exceeds m + kLazy reset m to the max
+    // over their four key groups): rare, outside the overlapped regions.
+    auto rescale = [&](const float (&lmx)[RT]) __attribute__((always_inline)) {
+        // every row tile in one block (alpha 1 where the max stays): the code
+        // sits in each step, so it is kept to one copy
+        float alpha[RT];
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+            alpha[r] = 1.0f;
+            if (__builtin_amdgcn_ballot_w64(lmx[r] > mlim[r])) {
+                const float mx = row_group_max(lmx[r]);
+                const float mn = fmaxf(m[r], mx);
+                alpha[r] = mn > m[r] ? __builtin_amdgcn_exp2f((m[r] - mn) * sc) : 1.0f;
+                m[r] = mn;
+                mlim[r] = mn + lazy;
+                msc[r] = (mn == -INFINITY ? 0.0f : mn) * sc;
+            }
+        }
+        agpr_fence(o, lsum);
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+            lsum[r] *= alpha[r];
+#pragma unroll
+            for (int t = 0; t < DT; ++t) o[r][t] *= alpha[r];
+        }
+    };
+    // ---------------- the tiles, pipelined.  Steps whose keys reach past some
+    // row's context are masked: wmin, the smallest context of the wave's rows
+    // (rows past the item have context 0 and are masked everywhere; their
+    // output is not stored), decides on the scalar unit whether a step needs
+    // the per-element test.
+    int wmin;
+    {
+        float mn = 3.0e9f;
+#pragma unroll
+        for (int r = 0; r < RT; ++r)
+            if (b * kRows + 16 * RT * wave + 16 * r + col < nrows) mn = fminf(mn, float(rctx[r]));
+        wmin = __builtin_amdgcn_readfirstlane(int(-group_max<64>(-mn)));
+    }
+    auto mask_if = [&](const int kbase, float4_t (&sv)[RT][2]) __attribute__((always_inline)) {
+        if (kbase + 32 > wmin) mask(kbase, sv);
+    };
+    float4_t sv[RT][2];   // scores of the step being finished
+    half8_t kop[KS][2];   // K operands
+    // Q lives in AGPRs (the asm MFMAs read it there); wait states between its
+    // writes and the first MFMA reads
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+        asm volatile("s_nop 4" : "+a"(qop[r][0]), "+a"(qop[r][1]), "+a"(qop[r][2]), "+a"(qop[r][3]));
+    if (ntiles > 0) {
+        publish_barrier(0);
+        load_tile(2 % kW64Stages, 2);
+        read_k(kstage(0), kop);
+        qk(kop, sv);
+        mask_if(0, sv);
+        float lmx[RT];
+        (void)lane_max(sv, lmx);
+        // the first maximum: the running max starts at -inf, so this is the
+        // rescale with nothing yet to rescale (the accumulators are zero)
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+            const float mx = row_group_max(lmx[r]);
+            m[r] = mx;
+            mlim[r] = mx + lazy;
+            msc[r] = (mx == -INFINITY ? 0.0f : mx) * sc;
+        }
+        read_k(kstage(0) + 32 * T::ROW, kop);
+    }
+    // One step s: at entry the scores of s are computed, masked and rescaled
+    // for, and the K operands of step s + 1 are read.  The step is placed by
+    // hand, slot by slot (scheduling barriers between slots, its VALU work in
+    // asm): one MFMA and a few VALU or LDS instructions per slot, so that the
+    // lone wave of the SIMD issues VALU work while its MFMAs run.
+    //   X: the V operands of s are read; 32 slots of one Q K^T MFMA of step
+    //      s + 1, 24 of them beside one weight exp2(x sc - m sc) of step s
+    //      (row tiles 0-2; pairs packed to fp16 a slot later);
+    //   the scores of s + 1 wait out the MFMA-to-VALU distance and are masked
+    //      where needed; `between` runs here (the barrier publishing the next
+    //      tile, when the next K operands lie in it);
+    //   Y: 36 slots of one P V (or row-sum) MFMA of step s, row tile by row
+    //      tile, beside the K operand reads of step s + 2 (kn2), the weights
+    //      of row tile 3 (done before its MFMAs) and this lane's row maxima
+    //      of step s + 1;
+    //   the rare rescale.
+    // check = false discards the look-ahead (past the item's last tile).
+    // dma: this step issues the loads of tile dt into stage dst, after the
+    // barrier `between` (compile-time: the slots differ).
+    auto pstep = [&](const char* vb, const char* kn2, const int kb_next, const bool check, auto between, auto dma,
+                     const int dt, const int dst) __attribute__((always_inline)) {
+        constexpr bool kDma = decltype(dma)::value;
+        uint32_t pw[RT][4];  // weights of step s, fp16 pairs (the P^T operands)
+        float wexp[RT][8];
+        float4_t svn[RT][2];
+        float lmx[RT];
+        u32x2 vlo[DT], vhi[DT];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+            const int i = j >> 3, hh = (j >> 2) & 1, r = j & 3;
+            if (i == 0) mfma_first_v(svn[r][hh], kop[0][hh], qop[r][0]);
+            else mfma_acc_v(svn[r][hh], kop[i][hh], qop[r][i]);
+            // V operands of step s: one transposed read per slot
+            if (j < 16) {
+                if (j & 1) vhi[j >> 1] = tr_read(vb + voff[j >> 1] + 16 * T::ROW);
+                else vlo[j >> 1] = tr_read(vb + voff[j >> 1]);
+            }
+            // exps n = 3 (j / 4) + j % 4 for j % 4 < 3 (row tile n / 8, slot n % 8),
+            // each odd n's pair packed in the next slot
+            if ((j & 3) < 3) {
+                const int n = 3 * (j >> 2) + (j & 3);
+                wexp[n >> 3][n & 7] = slot_exp2(sv[n >> 3][(n & 7) >> 2][n & 3], sc, msc[n >> 3]);
+            }
+            if (j >= 3 && ((j - 3) & 3) < 3) {  // the pair ending in exp n, three slots later
+                const int n = 3 * ((j - 3) >> 2) + ((j - 3) & 3);
+                if (n & 1) pw[n >> 3][(n & 7) >> 1] = slot_pack(wexp[n >> 3][n & 6], wexp[n >> 3][n & 7]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // pairs whose pack slot falls past the last slot (n + 1 = 23: exp slot 30)
+#pragma unroll
+        for (int n = 0; n < 24; n += 2) {
+            const int jn = 4 * ((n + 1) / 3) + (n + 1) % 3;
+            if (jn + 3 >= 32) pw[n >> 3][(n & 7) >> 1] = slot_pack(wexp[n >> 3][n & 6], wexp[n >> 3][(n & 6) + 1]);
+        }
+        score_fence(svn);
+        if (check) mask_if(kb_next, svn);
+        between();
+        __builtin_amdgcn_sched_barrier(0);
+        half8_t pop[RT], vop[DT];
+#pragma unroll
+        for (int t = 0; t < DT; ++t) vop[t] = __builtin_bit_cast(half8_t, u32x4{vlo[t][0], vlo[t][1], vhi[t][0], vhi[t][1]});
+        int dids[JW];
+#pragma unroll
+        for (int q = 0; q < 36; ++q) {
+            const int r = q / 9, t = q % 9;
+            if (t == 0) pop[r] = __builtin_bit_cast(half8_t, u32x4{pw[r][0], pw[r][1], pw[r][2], pw[r][3]});
+            if (t == 0) mfma_acc_a(lsum[r], kOnes, pop[r]);
+            else mfma_acc_a(o[r][t - 1], vop[t - 1], pop[r]);
+            if (q < 8)
+                kop[q >> 1][q & 1] = __builtin_bit_cast(
+                    half8_t, *reinterpret_cast<const u32x4*>(kn2 + koff[q >> 1] + 16 * (q & 1) * T::ROW));
+            // loads of tile dt: block ids read in slots 8-11, loads issued in 16-23
+            if (kDma && q >= 8 && q < 8 + JW) dids[q - 8] = dma_id(dt, q - 8);
+            if (kDma && q >= 16 && q < 16 + 2 * JW) {
+                const int jj = (q - 16) >> 1;
+                const uint64_t off = dma_off(dt, jj, dids[jj]);
+                if ((q & 1) == 0) dma16(a.kc + off, dma_lds(dst, jj));
+                else dma16(a.vc + off, dma_lds(dst, jj) + T::BYTES);
+            }
+            // row tile 3's weights: exps in slots 0-7, packs three slots after
+            // the pair's second exp, in 4-10 (its MFMAs from slot 27)
+            if (q < 8) wexp[3][q] = slot_exp2(sv[3][q >> 2][q & 3], sc, msc[3]);
+            if (q >= 4 && q < 12 && (q & 1) == 0) pw[3][(q - 4) >> 1] = slot_pack(wexp[3][q - 4], wexp[3][q - 3]);
+            // maxima of step s + 1 (lane-local, one row tile per 4 slots from slot 12)
+            if (q >= 12 && q < 28) {  // (unused when the look-ahead is discarded)
+                const int r2 = (q - 12) >> 2, k = (q - 12) & 3;
+                if (k == 0) lmx[r2] = slot_max3(svn[r2][0][0], svn[r2][0][1], svn[r2][0][2]);
+                if (k == 1) lmx[r2] = slot_max3(lmx[r2], svn[r2][0][3], svn[r2][1][0]);
+                if (k == 2) lmx[r2] = slot_max3(lmx[r2], svn[r2][1][1], svn[r2][1][2]);
+                if (k == 3) lmx[r2] = slot_max3(lmx[r2], svn[r2][1][3], svn[r2][1][3]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (check) {
+            bool over = false;
+#pragma unroll
+            for (int r = 0; r < RT; ++r) over = over || lmx[r] > mlim[r];
+            if (__builtin_amdgcn_ballot_w64(over)) rescale(lmx);
+        }
+#pragma unroll
+        for (int r = 0; r < RT; ++r) sv[r][0] = svn[r][0], sv[r][1] = svn[r][1];
+    };
+    // Tile t in stage t % kW64Stages: step 2t (keys 0-31 of the tile), whose
+    // look-ahead K operands (step 2t + 2) lie in tile t + 1, published by the
+    // barrier between its two halves; then step 2t + 1.  The second step of
+    // the last tile may lie wholly past the context: its keys are all masked
+    // and add nothing.
+    for (int t = 0; t < ntiles; ++t) {
+        const int st = t % kW64Stages, st1 = (t + 1) % kW64Stages;
+        pstep(vstage(st), kstage(st1), t * kBK + 32, true,
+              [&]() __attribute__((always_inline)) { publish_barrier(t + 1); }, std::true_type(), t + 3,
+              (t + 3) % kW64Stages);
+        pstep(vstage(st) + 32 * T::ROW, kstage(st1) + 32 * T::ROW, t * kBK + kBK, t + 1 < ntiles,
+              []() __attribute__((always_inline)) {}, std::false_type(), 0, 0);
+    }
+    wait_vmcnt<0>();  // no load of this item may land in the next item's buffers
+
+    // ---------------- output: lane (row col) holds dims 16 t + 4 grp + e
+    agpr_fence(o, lsum);
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+        const int rho = b * kRows + 16 * RT * wave + 16 * r + col;
+        if (rho >= nrows) continue;
+        const int j = rho / G;
+        const int h = kvh * G + rho - j * G;
+        const float lt = lsum[r][0];
+        const float inv = (rctx[r] > 0 && lt > 0.0f) ? 1.0f / lt : 0.0f;
+        _Float16* orow = a.out + ((int64_t(q0) + j) * a.num_heads + h) * D;
+#pragma unroll
+        for (int t2 = 0; t2 < DT; ++t2) {
+            const half2_t lo = {static_cast<_Float16>(o[r][t2][0] * inv), static_cast<_Float16>(o[r][t2][1] * inv)};
+            const half2_t hi = {static_cast<_Float16>(o[r][t2][2] * inv), static_cast<_Float16>(o[r][t2][3] * inv)};
+            *reinterpret_cast<u32x2*>(orow + 16 * t2 + 4 * grp) =
+                u32x2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
+        }
+    }
+}
+
+template <int D>
+__device__ __forceinline__ void w64_items(const PrefillArgs& a, const W64Buffers& buf) {
+    run_items<64 * kW64Waves>(a, [&](int s, int b, int kvh) __attribute__((always_inline)) {
+        prefill_block_w64<D>(a, s, b, kvh, buf);
+    });
+}
+
+template <int D>
+__global__ __launch_bounds__(64 * kW64Waves) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void prefill_w64_kernel(PrefillArgs a) {
+    __shared__ __attribute__((aligned(1024))) char tiles[kW64Stages * 2 * DmaTile<D>::BYTES];
+    __shared__ int btc[kWideBtc];
+    const W64Buffers buf = {tiles, btc};
+    w64_items<D>(a, buf);
 }
 
 // FP8 caches at D = 128: three stages of code tiles and scales, one fp16 tile.
@@ -1153,7 +1826,8 @@ size_t prefill_items_bytes(const vkv_prefill_params* p) {
     return 256 + size_t(int64_t(p->num_seqs) * max_row_blocks(p) * p->num_kv_heads) * sizeof(int2);
 }
 
-int launch_prefill_mfma(const vkv_prefill_params* p, void* item_space, int32_t* inline_claim, hipStream_t st) {
+int launch_prefill_mfma(const vkv_prefill_params* p, void* item_space, int32_t* header, hipStream_t st) {
+    int32_t* inline_claim = header ? header + kPrefillClaimSlot : nullptr;
     PrefillArgs a;
     a.out = static_cast<_Float16*>(p->output);
     a.q = static_cast<const char*>(p->query);
@@ -1201,9 +1875,13 @@ int launch_prefill_mfma(const vkv_prefill_params* p, void* item_space, int32_t* 
     const int64_t T = p->num_query_tokens;
     const int64_t nseq2 = p->num_seqs < T / 2 ? p->num_seqs : T / 2;
     const int64_t bound = T * row_mult / rpi + nseq2;
-    a.inline_list = wide && inline_claim != nullptr && bound <= kInlineBlocks;
+    // a host-built list (wide kernels only) replaces both in-kernel orderings
+    a.work_list = wide && header != nullptr && p->work_list && p->work_list_words > kListHeaderWords ? p->work_list : nullptr;
+    a.work_list_items = a.work_list ? (p->work_list_words - kListHeaderWords) / 2 : 0;
+    a.list_claim = header;
+    a.inline_list = !a.work_list && wide && inline_claim != nullptr && bound <= kInlineBlocks;
     a.inline_claim = inline_claim;
-    if (!a.inline_list)
+    if (!a.inline_list && !a.work_list)
         hipLaunchKernelGGL(prefill_items_kernel, dim3(1), dim3(256), 0, st, p->query_start_loc, p->context_lens,
                            p->num_seqs, p->num_kv_heads, row_mult, rpi, a.qblocks, a.table_tokens, nbins,
                            items, count);
@@ -1216,11 +1894,13 @@ int launch_prefill_mfma(const vkv_prefill_params* p, void* item_space, int32_t* 
     const int64_t upper = int64_t(p->num_seqs) * a.qblocks * p->num_kv_heads;
     const int64_t per_cu = wide ? 1 : 2;
     const int64_t wgs = int64_t(cus) * per_cu < upper ? int64_t(cus) * per_cu : upper;
-    const int waves = wide ? kWideWaves : (a.heads_per_wg < kMinWaves ? kMinWaves : a.heads_per_wg);
+    const bool w64 = VKV_PREFILL_W64 && p->head_dim == 128 && p->kv_dtype == VKV_DTYPE_F16;
+    const int waves = w64 ? kW64Waves : wide ? kWideWaves : (a.heads_per_wg < kMinWaves ? kMinWaves : a.heads_per_wg);
     const dim3 grid(unsigned(wgs > 0 ? wgs : 1), 1u, unsigned(head_groups));
     const dim3 block(unsigned(64 * waves));
     if (p->head_dim == 128) {
-        if (p->kv_dtype == VKV_DTYPE_F16) hipLaunchKernelGGL((prefill_wide_kernel<128>), grid, block, 0, st, a);
+        if (w64) hipLaunchKernelGGL((prefill_w64_kernel<128>), grid, block, 0, st, a);
+        else if (p->kv_dtype == VKV_DTYPE_F16) hipLaunchKernelGGL((prefill_wide_kernel<128>), grid, block, 0, st, a);
         else hipLaunchKernelGGL(prefill_wide8_kernel, grid, block, 0, st, a);
     } else {
         if (wide) hipLaunchKernelGGL((prefill_wide_kernel<64>), grid, block, 0, st, a);
@@ -1229,4 +1909,53 @@ int launch_prefill_mfma(const vkv_prefill_params* p, void* item_space, int32_t* 
     return 0;
 }
 
+int64_t prefill_work_list_host(const vkv_prefill_params* p, const int32_t* host_qsl, const int32_t* host_cl,
+                               int32_t* out, int64_t capacity) {
+    if (!p || !host_qsl || !host_cl) return -1;
+    if (p->num_seqs <= 0 || !prefill_mfma_supported(p) || !wide_path(p)) return 0;  // no list for this call
+    const int G = p->num_heads / p->num_kv_heads, hkv = p->num_kv_heads;
+    const int rpi = rows_per_item(p);
+    const int64_t qblocks = max_row_blocks(p);
+    int64_t tt = int64_t(p->max_blocks_per_seq) * p->block_size;
+    if (p->max_context_len > 0 && p->max_context_len < tt) tt = p->max_context_len;
+    // items (s, b * Hkv + kvh) in (s, b, kvh) order with their key tiles
+    struct Item {
+        int32_t s, y, tiles;
+    };
+    std::vector<Item> items;
+    for (int32_t s = 0; s < p->num_seqs; ++s) {
+        const int64_t q = int64_t(host_qsl[s + 1]) - host_qsl[s];
+        if (q < 2) continue;
+        const int64_t prior = int64_t(host_cl[s]) - q;
+        int64_t nb = (q * G + rpi - 1) / rpi;
+        nb = nb < qblocks ? nb : qblocks;
+        for (int64_t b = 0; b < nb; ++b) {
+            const int64_t last = ((b + 1) * rpi - 1) / G + 1;
+            int64_t kend = prior + (last < q ? last : q);
+            kend = kend < tt ? kend : tt;
+            const int32_t tiles = int32_t(kend > 0 ? (kend + kBK - 1) / kBK : 0);
+            for (int k = 0; k < hkv; ++k) items.push_back(Item{s, int32_t(b * hkv + k), tiles});
+        }
+    }
+    const int64_t words = kListHeaderWords + 2 * int64_t(items.size());
+    if (!out) return words;
+    if (capacity < words) return -2;
+    // one list, longest first (ties in (s, b, kvh) order): a longest-
+    // processing-time schedule for the persistent workgroups that claim the
+    // items in turn.  (One list per XCD, each group of items of a sequence and
+    // kv head on one XCD, was slower: C3's prefill call 93.5 against 90 us.)
+    std::stable_sort(items.begin(), items.end(), [](const Item& u, const Item& v) { return u.tiles > v.tiles; });
+    std::fill(out, out + kListHeaderWords, 0);
+    out[0] = 1;
+    out[1] = 0;
+    out[2] = int32_t(items.size());
+    int32_t* dst = out + kListHeaderWords;
+    for (const Item& it : items) {
+        *dst++ = it.s;
+        *dst++ = it.y;
+    }
+    return words;
+}
+
 }  // namespace vkv
+

@@ -21,7 +21,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 PKG_ROOT = os.path.dirname(os.path.dirname(_HERE))          # vllm-cpp_amd/
 LIB_PATH = os.path.join(PKG_ROOT, "lib", "libvllm_kv_amd.so")
 
-ABI_VERSION = 3  # vkv_abi_version() of the library this binding's structs match
+ABI_VERSION = 4  # vkv_abi_version() of the library this binding's structs match
 DTYPE_F32, DTYPE_F16, DTYPE_FP8 = 0, 1, 2
 SWAP_OUT, SWAP_IN = 0, 1
 
@@ -38,7 +38,7 @@ EXPORTED = [
     "vkv_paged_prefill",
     "vkv_copy_blocks", "vkv_check_block_pairs_host", "vkv_swap_host_block_bytes",
     "vkv_swap_blocks", "vkv_rope_reshape_and_cache", "vkv_rope_cos_sin_host",
-    "vkv_kv_block_bytes", "vkv_kv_pool_num_blocks", "vkv_release_workspace",
+    "vkv_kv_block_bytes", "vkv_kv_pool_num_blocks", "vkv_release_workspace", "vkv_prefill_work_list_host",
 ]
 
 
@@ -112,6 +112,7 @@ class PrefillParams(ctypes.Structure):
         ("io_dtype", ctypes.c_int32), ("kv_dtype", ctypes.c_int32),
         ("max_context_len", ctypes.c_int32), ("multi_token_only", ctypes.c_int32),
         ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
+        ("work_list", ctypes.c_void_p), ("work_list_words", ctypes.c_int32),
     ]
 
 
@@ -178,6 +179,9 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.vkv_swap_blocks.restype = ctypes.c_int
     lib.vkv_release_workspace.argtypes = [ctypes.c_void_p]
     lib.vkv_release_workspace.restype = ctypes.c_int
+    lib.vkv_prefill_work_list_host.argtypes = [ctypes.POINTER(PrefillParams), ctypes.c_void_p, ctypes.c_void_p,
+                                               ctypes.c_void_p, ctypes.c_int64]
+    lib.vkv_prefill_work_list_host.restype = ctypes.c_int64
     _lib = lib
     return lib
 
@@ -370,17 +374,44 @@ def prefill_params(out, query, key_cache, value_cache, block_tables, context_len
 
 def paged_prefill(out, query, key_cache, value_cache, block_tables, context_lens, query_start_loc,
                   max_query_len, scale, key_scales=None, value_scales=None, max_context_len=0,
-                  workspace=None, stream=None, multi_token_only=False) -> None:
+                  workspace=None, stream=None, multi_token_only=False, work_list=None) -> None:
     """out/query [Tq, H, D]; query_start_loc int32 [S+1]; context_lens counts the step's tokens.
     max_context_len > 0 clamps every row's keys; workspace (optional) as for paged_decode;
     multi_token_only: the caller's promise that no sequence has exactly one query token
-    (skips the decode pass that serves those)."""
+    (skips the decode pass that serves those); work_list: a device int32 copy of
+    prefill_work_list()'s words for this call (optional)."""
     _require_cuda(out, query, key_cache, value_cache, block_tables, context_lens, query_start_loc,
-                  key_scales, value_scales, workspace)
+                  key_scales, value_scales, workspace, work_list)
     p = prefill_params(out, query, key_cache, value_cache, block_tables, context_lens, query_start_loc,
                        max_query_len, scale, key_scales, value_scales, max_context_len, workspace,
                        multi_token_only)
+    if work_list is not None and work_list.numel() > 0:
+        p.work_list = work_list.data_ptr()
+        p.work_list_words = int(work_list.numel())
     check(load().vkv_paged_prefill(ctypes.byref(p), _stream(stream)))
+
+
+def prefill_work_list(out, query, key_cache, value_cache, block_tables, context_lens, query_start_loc,
+                      max_query_len, scale, host_query_start_loc, host_context_lens, key_scales=None,
+                      value_scales=None, max_context_len=0):
+    """vkv_prefill_work_list_host for the call these arguments describe, from host (numpy)
+    copies of its query_start_loc and context_lens: int32 numpy words (empty when the
+    call's shape runs without a list)."""
+    import numpy as np
+    p = prefill_params(out, query, key_cache, value_cache, block_tables, context_lens, query_start_loc,
+                       max_query_len, scale, key_scales, value_scales, max_context_len, None)
+    hq = np.ascontiguousarray(host_query_start_loc, dtype=np.int32)
+    hc = np.ascontiguousarray(host_context_lens, dtype=np.int32)
+    n = int(load().vkv_prefill_work_list_host(ctypes.byref(p), hq.ctypes.data, hc.ctypes.data, None, 0))
+    if n < 0:
+        raise VkvError(n, "vkv_prefill_work_list_host failed")
+    words = np.zeros(n, np.int32)
+    if n:
+        r = int(load().vkv_prefill_work_list_host(ctypes.byref(p), hq.ctypes.data, hc.ctypes.data,
+                                                  words.ctypes.data, n))
+        if r != n:
+            raise VkvError(r, "vkv_prefill_work_list_host failed")
+    return words
 
 
 def prefill_workspace_size(out, query, key_cache, value_cache, block_tables, context_lens, query_start_loc,
