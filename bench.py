@@ -213,6 +213,19 @@ def main():
     log(f"[bench] decode {ms_decode * 1e3:.1f} us (p10 {dec[1] * 1e3:.1f}, p90 {dec[2] * 1e3:.1f}), "
         f"append {ms_append * 1e3:.1f} us")
 
+    # the box's read-only ceiling for this byte set: whole blocks of the
+    # decode's block tables gathered with no math
+    try:
+        nblk = (lay.context_lens.astype(np.int64) + bs - 1) // bs
+        ids = np.concatenate([lay.block_tables[s, :n] for s, n in enumerate(nblk)]).astype(np.int32)
+        ceil_gbs, ceil_shape, ceil_bytes = gather_ceiling(dev, kc, vc, ids, bs * Hkv * D * 2, stream)
+        ceiling = {"gbs": round(ceil_gbs, 1), "bytes": ceil_bytes, "shape": ceil_shape,
+                   "workload": f"read-only gather of the {ids.shape[0]} K and V blocks ({bs * Hkv * D * 2} B each) "
+                               "of the decode's block tables, no math (vllm-cpp_amd/bench/ceilings.hip)"}
+        log(f"[bench] read-only gather ceiling {ceil_gbs:.0f} GB/s ({ceil_shape})")
+    except RuntimeError as e:
+        ceiling = {"gbs": None, "error": str(e)}
+
     kv_bytes = cfg.kv_bytes(2)
     traffic, traffic_note = measured_traffic()
     value = kv_bytes / (ms_step * 1e-3) / 1e9
@@ -251,7 +264,10 @@ def main():
                      "traffic_over_algorithmic": None if traffic is None else round(traffic / kv_bytes, 4),
                      "traffic_source": traffic_note,
                      "kernel": "paged decode (partition + merge kernels), event-timed on the launch stream",
-                     "achieved_note": "algorithmic KV bytes per call / decode call time"},
+                     "achieved_note": "algorithmic KV bytes per call / decode call time",
+                     "measured_ceiling": ceiling["gbs"],
+                     "frac_of_measured_ceiling": None if not ceiling["gbs"] else round(achieved / ceiling["gbs"], 4)},
+        "hbm_read_ceiling": ceiling,
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(kc, vc, q, lay, cfg)
@@ -759,6 +775,136 @@ def suite_stream(dev, steps, warmup):
             "gbs_read_plus_write": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
+CEIL_LIB = os.path.join(ROOT, "vllm-cpp_amd", "lib", "libvkv_ceilings.so")
+MFMA_PEAK_TFLOPS = 2500.0  # MI355X published dense fp16 MFMA rate
+HOST_LINK_GBS = 64.0       # PCIe 5.0 x16, one direction
+
+
+def _ceil_lib():
+    """The measurement-only kernels of vllm-cpp_amd/bench/ceilings.hip."""
+    import ctypes
+    if not os.path.exists(CEIL_LIB):
+        raise RuntimeError(f"{CEIL_LIB} not built: run __graft_entry__.build()")
+    lib = ctypes.CDLL(CEIL_LIB)
+    vp, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
+    sig = {"vkvc_mfma_loop": [vp, i32, i32, vp],
+           "vkvc_read_stream": [vp, i64, vp, i32, i32, vp],
+           "vkvc_read_blocks": [vp, vp, vp, i32, i64, vp, i32, i32, vp],
+           "vkvc_copy": [vp, vp, i64, vp]}
+    for name, args in sig.items():
+        fn = getattr(lib, name)
+        fn.argtypes, fn.restype = args, i32
+    return lib
+
+
+def _ck(rc, what):
+    if rc != 0:
+        raise RuntimeError(f"{what} returned {rc}")
+
+
+def _cus(dev):
+    import torch
+    return torch.cuda.get_device_properties(dev).multi_processor_count
+
+
+def gather_ceiling(dev, k_pool, v_pool, ids, block_bytes, stream, calls=20):
+    """Read-only gather of whole blocks `ids` (int32 numpy) from the K and V
+    pools with no math: the best over launch shapes and load kinds of the
+    median of 5 samples, each the mean of calls/5 launches.  Returns
+    (GB/s, shape note, bytes per launch)."""
+    import torch
+    lib = _ceil_lib()
+    d_ids = torch.from_numpy(ids.astype("int32")).to(dev)
+    cus = _cus(dev)
+    out = torch.empty(cus * 8 * 256, dtype=torch.int32, device=dev)
+    h = stream.cuda_stream
+    nbytes = 2 * int(ids.shape[0]) * block_bytes
+    best = (0.0, "")
+    for mult in (2, 4, 8):
+        for nt in (0, 1):
+            def run():
+                _ck(lib.vkvc_read_blocks(k_pool.data_ptr(), v_pool.data_ptr(), d_ids.data_ptr(), int(ids.shape[0]),
+                                         block_bytes, out.data_ptr(), cus * mult, nt, h), "vkvc_read_blocks")
+            _warm(run, 3, min_ms=20.0)
+            t = _events_ms(run, calls, stream)
+            gbs = nbytes / (t[0] * 1e-3) / 1e9
+            if gbs > best[0]:
+                best = (gbs, f"{cus * mult} workgroups, {'non-temporal' if nt else 'ordinary'} loads")
+    return best[0], best[1], nbytes
+
+
+def suite_ceilings(dev, steps, warmup):
+    """Measured ceilings: dense v_mfma_f32_16x16x32_f16, read-only HBM stream
+    (4 GiB), read-only block gathers of C2 and C5 (the decode's byte sets),
+    pinned-host hipMemcpyAsync of 1 GiB each way."""
+    import numpy as np
+    import torch
+    from vllm_kv_amd import workloads
+    lib = _ceil_lib()
+    stream = torch.cuda.current_stream()
+    h = stream.cuda_stream
+    cus = _cus(dev)
+    rows = {}
+    # matrix cores: 1, 2 and 4 waves per SIMD (256-thread workgroups, one per CU per wave slot)
+    out = torch.empty(cus * 4 * 256, dtype=torch.float32, device=dev)
+    iters = 4000
+    mf = {}
+    for wps in (1, 2, 4):
+        blocks = cus * wps
+        run = lambda: _ck(lib.vkvc_mfma_loop(out.data_ptr(), blocks, iters, h), "vkvc_mfma_loop")
+        _warm(run, 3, min_ms=100.0)
+        t = _events_ms(run, 10, stream)
+        flops = blocks * 4 * iters * 32 * 16384
+        mf[f"{wps}_wave_per_simd"] = round(flops / (t[0] * 1e-3) / 1e12, 1)
+    best = max(mf.values())
+    rows["mfma"] = {"tflops": best, "by_waves_per_simd": mf, "frac_of_spec": round(best / MFMA_PEAK_TFLOPS, 4),
+                    "kernel": f"{iters} x 32 v_mfma_f32_16x16x32_f16 per wave, 8 accumulator chains"}
+    # sequential read-only stream
+    buf = torch.empty(1 << 32, dtype=torch.uint8, device=dev)
+    buf.fill_(1)
+    sink = torch.empty(cus * 32 * 256, dtype=torch.int32, device=dev)
+    rs = {}
+    for mult in (4, 8, 16, 32):
+        for nt in (0, 1):
+            run = lambda: _ck(lib.vkvc_read_stream(buf.data_ptr(), buf.numel(), sink.data_ptr(), cus * mult, nt, h),
+                              "vkvc_read_stream")
+            _warm(run, 2, min_ms=50.0)
+            t = _events_ms(run, 10, stream)
+            rs[f"{cus * mult}wg_{'nt' if nt else 'plain'}"] = round(buf.numel() / (t[0] * 1e-3) / 1e9, 1)
+    best = max(rs.values())
+    rows["read_stream"] = {"gbs": best, "frac_of_spec": round(best / HBM_PEAK_GBS, 4), "bytes": buf.numel(),
+                           "by_shape": rs}
+    del buf, sink
+    torch.cuda.empty_cache()
+    # block gathers of the decode configs' byte sets (whole blocks, every head)
+    for name, cfg, elem in (("gather_c2", workloads.config2(), 2), ("gather_c5", workloads.config5(), 1)):
+        lay = cfg.layout
+        nblk = (lay.context_lens.astype(np.int64) + cfg.block_size - 1) // cfg.block_size
+        ids = np.concatenate([lay.block_tables[s, :n] for s, n in enumerate(nblk)]).astype(np.int32)
+        bb = cfg.block_size * cfg.num_kv_heads * cfg.head_dim * elem
+        pool = torch.empty((2, lay.num_blocks * bb), dtype=torch.uint8, device=dev)
+        pool.fill_(3)
+        gbs, shape, nbytes = gather_ceiling(dev, pool[0], pool[1], ids, bb, stream, calls=50)
+        rows[name] = {"gbs": round(gbs, 1), "frac_of_spec": round(gbs / HBM_PEAK_GBS, 4), "bytes": nbytes,
+                      "blocks": int(ids.shape[0]), "block_bytes": bb, "shape": shape}
+        del pool
+        torch.cuda.empty_cache()
+    # host link: pinned host memory <-> device, hipMemcpyAsync of 1 GiB
+    nb = 1 << 30
+    host = torch.empty(nb, dtype=torch.uint8, pin_memory=True)
+    devb = torch.empty(nb, dtype=torch.uint8, device=dev)
+    for direction, (dst, src) in (("h2d", (devb, host)), ("d2h", (host, devb))):
+        run = lambda: _ck(lib.vkvc_copy(dst.data_ptr(), src.data_ptr(), nb, h), "vkvc_copy")
+        _warm(run, 1, min_ms=50.0)
+        t = _events_ms(run, 10, stream)
+        gbs = nb / (t[0] * 1e-3) / 1e9
+        rows[f"host_{direction}"] = {"gbs": round(gbs, 2), "frac_of_spec": round(gbs / HOST_LINK_GBS, 4),
+                                     "us": round(t[0] * 1e3, 1)}
+    return {"row": "ceilings", "workload": "measurement kernels of vllm-cpp_amd/bench/ceilings.hip",
+            "spec": {"mfma_fp16_tflops": MFMA_PEAK_TFLOPS, "hbm_gbs": HBM_PEAK_GBS, "host_link_gbs": HOST_LINK_GBS},
+            **rows}
+
+
 def suite_c4(dev, steps, warmup):
     """C4: copy_blocks of 4096 (src, dst) pairs over 32 layers x (K, V) of
     [N=8192, bs64, Hkv8, D128] fp16 (random bits), then swap of 2048 blocks to
@@ -876,7 +1022,7 @@ def _decode_beside_swap(dev, planes, host, nsw, out_pairs, in_pairs, swap_bytes,
     return res
 
 
-SUITES = {"stream": suite_stream, "c1": suite_c1, "append": suite_append, "rope": suite_rope, "step": suite_step,
+SUITES = {"ceil": suite_ceilings, "stream": suite_stream, "c1": suite_c1, "append": suite_append, "rope": suite_rope, "step": suite_step,
           "c3": suite_c3,
           "c3p": suite_c3_prefill_only, "c5": suite_c5, "c4": suite_c4}
 
