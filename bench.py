@@ -530,6 +530,7 @@ def suite_c1(dev, steps, warmup):
     _warm(graph.replay, warmup)
     tg = _events_ms(graph.replay, steps, stream)
     graph_equal = bool(torch.equal(out.view(torch.int16), ref_out.view(torch.int16)))
+    native = _native_c1(vkv, nk, nv, kc, vc, slots, out, q, bt, cl, cfg.scale, stream, steps, warmup)
     from oracle import oracle
     hk, hv = kc.cpu().numpy().view(np.uint16), vc.cpu().numpy().view(np.uint16)
     hnk, hnv = nk.cpu().numpy().view(np.uint16), nv.cpu().numpy().view(np.uint16)
@@ -546,8 +547,50 @@ def suite_c1(dev, steps, warmup):
             "step_us_p10_p90": [round(t[1] * 1e3, 2), round(t[2] * 1e3, 2)],
             "note": "launch-bound: three kernels (append, partition, merge) for 0.6 MB of KV",
             "graph_step_us_median": round(tg[0] * 1e3, 2), "graph_output_equals_eager": graph_equal,
+            "native_caller": native,
             "cpu_baseline": {"us_per_step": round(sec * 1e6, 1), "cores": 1, "kind": "port",
                              "sample": f"oracle append + decode of the whole step, {reps} steps"}}
+
+
+STEPLOOP_LIB = os.path.join(ROOT, "vllm-cpp_amd", "lib", "libvkv_steploop.so")
+
+
+def _native_c1(vkv, nk, nv, kc, vc, slots, out, q, bt, cl, scale, stream, steps, warmup):
+    """The same C1 step from a native caller (vllm-cpp_amd/bench/step_loop.cpp):
+    parameter structs built once, the loop in C, eager and as a replayed
+    one-step HIP graph; event-timed on the launch stream."""
+    import ctypes
+    if not os.path.exists(STEPLOOP_LIB):
+        raise RuntimeError(f"{STEPLOOP_LIB} not built: run __graft_entry__.build()")
+    lib = ctypes.CDLL(STEPLOOP_LIB)
+    vp = ctypes.c_void_p
+    lib.vkvb_step_loop.argtypes = [vp, vp, ctypes.c_int, vp]
+    lib.vkvb_graph_create.argtypes = [vp, vp, ctypes.POINTER(vp)]
+    lib.vkvb_graph_launch.argtypes = [vp, ctypes.c_int, vp]
+    lib.vkvb_graph_destroy.argtypes = [vp]
+    ap = vkv.append_params(nk, nv, kc, vc, slots)
+    dp = vkv.decode_params(out, q, kc, vc, bt, cl, scale)
+    h = stream.cuda_stream
+    n = max(steps, 100)
+
+    def eager():
+        _ck(lib.vkvb_step_loop(ctypes.byref(ap), ctypes.byref(dp), n, h), "vkvb_step_loop")
+
+    _warm(eager, warmup, min_ms=100.0)
+    t = _events_ms(eager, 5, stream, groups=5)
+    g = vp()
+    _ck(lib.vkvb_graph_create(ctypes.byref(ap), ctypes.byref(dp), ctypes.byref(g)), "vkvb_graph_create")
+    try:
+        def replay():
+            _ck(lib.vkvb_graph_launch(g, n, h), "vkvb_graph_launch")
+        _warm(replay, warmup, min_ms=100.0)
+        tg = _events_ms(replay, 5, stream, groups=5)
+    finally:
+        lib.vkvb_graph_destroy(g)
+    return {"eager_step_us_median": round(t[0] * 1e3 / n, 2),
+            "eager_step_us_p10_p90": [round(t[1] * 1e3 / n, 2), round(t[2] * 1e3 / n, 2)],
+            "graph_step_us_median": round(tg[0] * 1e3 / n, 2),
+            "sample": f"5 samples of {n} back-to-back steps each"}
 
 
 def suite_c5(dev, steps, warmup):

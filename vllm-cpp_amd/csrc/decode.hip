@@ -111,8 +111,19 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, const int P, co
     static_assert(LPT >= 1 && LPT <= kWave && (kWave % LPT) == 0, "head_dim / dtype mapping");
 
     const int seq = a.row_seq ? a.row_seq[s] : s;
-    const int ctx = row_context(a, s);
     const int t0 = part * P;
+    // Static (small) calls are bound by their chain of dependent loads: the
+    // table entries the partition could use are requested before the context
+    // length is known (P / block_size <= 64; entries past the row's table are
+    // not read), and those past the context are then dropped.
+    const bool early_table = a.static_parts > 0;
+    int my_block = 0;
+    if (early_table) {
+        const int tb = t0 >> a.bs_log2;
+        const int nb_max = a.max_blocks_per_seq - tb < (P >> a.bs_log2) ? a.max_blocks_per_seq - tb : (P >> a.bs_log2);
+        if (lane < nb_max) my_block = a.bt[int64_t(seq) * a.max_blocks_per_seq + tb + lane];
+    }
+    const int ctx = row_context(a, s);
     if (t0 >= ctx) return;
     const int n = (ctx - t0) < P ? (ctx - t0) : P;
 
@@ -125,8 +136,9 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, const int P, co
 
     // Physical block ids of this partition, one per lane (P / block_size <= 64).
     const int nb = (n + bs_mask) >> a.bs_log2;
-    int my_block = 0;
-    if (lane < nb) {
+    if (early_table) {
+        if (lane >= nb || (a.num_blocks > 0 && unsigned(my_block) >= unsigned(a.num_blocks))) my_block = 0;
+    } else if (lane < nb) {
         my_block = a.bt[int64_t(seq) * a.max_blocks_per_seq + (t0 >> a.bs_log2) + lane];
         if (a.num_blocks > 0 && unsigned(my_block) >= unsigned(a.num_blocks)) my_block = 0;
     }
@@ -740,10 +752,13 @@ void decode_partition_kernel(const DecodeArgs a) {
 // workspace (max_parts per row) and their stale contents are masked out.
 // Longer rows continue in batches with a running max.
 // DT = 0: head_dim from the arguments (the generic variant), one thread per
-// element of a block of head_dim rounded up to 64 threads.
-constexpr int kMergeBatch = 8;
-template <typename IO, int DT>
+// element of a block of head_dim rounded up to 64 threads.  B: partitions per
+// batch, chosen by the host (8; up to 64 for small calls split finely, such
+// as C1's 33 partitions of 16 tokens, which then load all their partials in
+// one round).
+template <typename IO, int DT, int B>
 __global__ __launch_bounds__(DT ? DT : 1024) void decode_reduce_kernel(DecodeArgs a) {
+    constexpr int kMergeBatch = B;
     const int s = blockIdx.y;
     const int h = blockIdx.x;
     const int d = threadIdx.x;
@@ -835,13 +850,24 @@ void launch_g(DecodeArgs& args, int grid_x, int grid_y, int grid_z, size_t lds, 
         if (by_lds < per_cu) per_cu = by_lds > 0 ? by_lds : 1;
         per_cu = blocks_per_cu(per_cu);
         const int64_t wgs = int64_t(cus) * per_cu;
-        const int gx = int(wgs < grid_x ? wgs : grid_x);
+        int gx = int(wgs < grid_x ? wgs : grid_x);
+        if (args.static_parts > 0) {
+            // one item per wave, all resident at once, or the claim loop
+            const int64_t groups = (int64_t(args.num_rows) * args.static_parts * args.num_kv_heads +
+                                    kWavesPerBlock - 1) / kWavesPerBlock;
+            if (groups <= wgs) {
+                gx = int(groups);
+                args.num_cands = 1;
+            } else {
+                args.static_parts = 0;
+            }
+        }
         args.wave_slots = (gx > 0 ? gx : 1) * kWavesPerBlock;
         args.level_waves = (gx > 0 ? (gx < cus ? gx : cus) : 1) * kWavesPerBlock;
         // When even the longest possible contexts give at most one wave of
         // default-size items per SIMD, the default stands and the kernels
         // (this one and the merge, which reads these args) skip the choice.
-        if (args.num_cands > 1) {
+        if (args.num_cands > 1 && args.static_parts == 0) {
             const int64_t worst = int64_t(args.num_rows) * ((int64_t(args.max_ctx) + args.P - 1) / args.P) *
                                   args.num_kv_heads;
             if (worst <= args.level_waves) args.num_cands = 1;
@@ -879,17 +905,28 @@ int dispatch_d(int D, int G, DecodeArgs& args, int grid_x, int Hkv, int S, size_
     }
 }
 
-template <typename IO>
-int launch_reduce(int D, const DecodeArgs& args, int H, int S, hipStream_t st) {
+template <typename IO, int B>
+int launch_reduce_b(int D, const DecodeArgs& args, int H, int S, hipStream_t st) {
     switch (D) {
-        case 64: hipLaunchKernelGGL((decode_reduce_kernel<IO, 64>), dim3(H, S), dim3(64), 0, st, args); return 0;
-        case 128: hipLaunchKernelGGL((decode_reduce_kernel<IO, 128>), dim3(H, S), dim3(128), 0, st, args); return 0;
-        case 256: hipLaunchKernelGGL((decode_reduce_kernel<IO, 256>), dim3(H, S), dim3(256), 0, st, args); return 0;
+        case 64: hipLaunchKernelGGL((decode_reduce_kernel<IO, 64, B>), dim3(H, S), dim3(64), 0, st, args); return 0;
+        case 128: hipLaunchKernelGGL((decode_reduce_kernel<IO, 128, B>), dim3(H, S), dim3(128), 0, st, args); return 0;
+        case 256: hipLaunchKernelGGL((decode_reduce_kernel<IO, 256, B>), dim3(H, S), dim3(256), 0, st, args); return 0;
         default:
             if (D < 1 || D > 1024) return VKV_ERR_UNSUPPORTED;
-            hipLaunchKernelGGL((decode_reduce_kernel<IO, 0>), dim3(H, S), dim3((D + 63) / 64 * 64), 0, st, args);
+            hipLaunchKernelGGL((decode_reduce_kernel<IO, 0, B>), dim3(H, S), dim3((D + 63) / 64 * 64), 0, st, args);
             return 0;
     }
+}
+
+template <typename IO>
+int launch_reduce(int D, const DecodeArgs& args, int H, int S, hipStream_t st) {
+    // Small (static) calls split finely load every partial in one round;
+    // the others keep batches of 8 (their rows have few partitions, and
+    // wider batches measured slower at C2's batch).
+    if (args.static_parts == 0 || args.max_parts <= 8) return launch_reduce_b<IO, 8>(D, args, H, S, st);
+    if (args.max_parts <= 16) return launch_reduce_b<IO, 16>(D, args, H, S, st);
+    if (args.max_parts <= 32) return launch_reduce_b<IO, 32>(D, args, H, S, st);
+    return launch_reduce_b<IO, 64>(D, args, H, S, st);
 }
 
 int ilog2(int x) {
@@ -1024,6 +1061,7 @@ int launch_rows(const vkv_decode_params* p, const DecodePlan& plan, void* worksp
     a.level_waves = 0;
     a.scale_log2 = logit_scale_log2(p->scale);
     a.accumulate = p->accumulate;
+    a.static_parts = 0;
 
     const int G = p->num_heads / p->num_kv_heads;
     const int D = p->head_dim;
@@ -1044,6 +1082,11 @@ int launch_rows(const vkv_decode_params* p, const DecodePlan& plan, void* worksp
         const int n = p->num_seqs - r0 < kMaxRowsPerLaunch ? p->num_seqs - r0 : kMaxRowsPerLaunch;
         DecodeArgs c = a;
         c.num_rows = n;
+        // Small plain decode calls (at most one (row, kv head) pair per CU):
+        // a static grid over the partitions of the default size, if its waves
+        // are all resident at once (decided at launch).
+        if (fixed && !qsl && !row_seq && int64_t(n) * p->num_kv_heads <= device_cu_count())
+            c.static_parts = int32_t((int64_t(c.max_ctx) + c.P - 1) / c.P > 0 ? (int64_t(c.max_ctx) + c.P - 1) / c.P : 1);
         if (qsl) {
             // rows are sequences; their query rows (qsl values) stay absolute
             c.qsl = qsl + r0;

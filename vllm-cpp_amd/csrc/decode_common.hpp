@@ -78,6 +78,11 @@ struct DecodeArgs {
     int32_t block_size;
     int32_t io_f32;           // query and output are fp32 (else fp16)
     int32_t vec_loads;        // whole-vector K/V loads (head_dim and cache alignment allow them)
+    // > 0: small call, one item per wave of a grid that covers every
+    // (row, partition < static_parts, sub-item) at partition size P: no
+    // prefix scan, no claims, and items request their block ids together with
+    // the context length.  0: the persistent claim loop.
+    int32_t static_parts;
 };
 
 // The shapes decode.hip's fixed-shape kernels are built for; every other
@@ -242,139 +247,145 @@ __device__ __forceinline__ void run_partitions(const DecodeArgs& a, const int it
     extern __shared__ int prefix[];  // [num_rows + 1] exclusive prefix of partitions per row
     const int lane = threadIdx.x & (kWave - 1);
     const int nrows = a.num_rows;
-
-    // Partitions per row and their exclusive prefix, scanned by the whole
-    // workgroup: each thread sums a contiguous tile of rows, the 256 tile sums
-    // are scanned with DPP wave scans plus one LDS step, then each thread writes
-    // its tile's prefix entries.  A call that leaves the partition size to the
-    // library counts its tile for every candidate size in the same pass and
-    // picks the size first (power-of-two block sizes only).
-    __shared__ int wave_total[kWavesPerBlock];
-    int P = a.P;
-    auto parts_of = [&](int r) {
-        const int ctx = row_context(a, r);
-        return ctx > 0 ? (ctx + P - 1) / P : 0;
-    };
-    const int per = (nrows + kBlockThreads - 1) / kBlockThreads;
-    const int r0 = int(threadIdx.x) * per;
-    int local = 0;
-    if (a.num_cands > 1) {
-        int cnt[kMaxPartitionCandidates];
-#pragma unroll
-        for (int c = 0; c < kMaxPartitionCandidates; ++c) cnt[c] = 0;
-        for (int i = 0; i < per; ++i) {
-            const int ctx = r0 + i < nrows ? row_context(a, r0 + i) : 0;
-            if (ctx > 0) {
-                // candidates are block multiples m * bs: ceil(ctx / (m * bs)) = ceil(nb / m)
-                const int nb = ((ctx - 1) >> a.bs_log2) + 1;
-#pragma unroll
-                for (int c = 0; c < kMaxPartitionCandidates; ++c) {
-                    const int m = a.cands[c] >> a.bs_log2;  // >= 1 (the host pads unused entries)
-                    cnt[c] += (nb + m - 1) / m;
-                }
-            }
-        }
-        P = __builtin_amdgcn_readfirstlane(choose_partition(a, cnt));  // wave-uniform: keep it scalar
-#pragma unroll
-        for (int c = 0; c < kMaxPartitionCandidates; ++c)
-            if (a.cands[c] == P) local = cnt[c];
-        // for the merge kernel (same stream, after this grid)
-        if (blockIdx.x == 0 && threadIdx.x == 0) a.counters[kChosenPartitionSlot] = P;
-    } else {
-        for (int i = 0; i < per; ++i)
-            if (r0 + i < nrows) local += parts_of(r0 + i);
-    }
-    const int incl = wave_incl_scan(local);
+    // Static (small) calls: one item per wave of a grid covering every
+    // (row, partition < static_parts, sub-item), no prefix scan, no claims.
+    const bool stat = a.static_parts > 0;
     const int wave = threadIdx.x / kWave;
-    if (lane == kWave - 1) wave_total[wave] = incl;
-    __syncthreads();
-    int before = 0;
-    for (int w = 0; w < wave; ++w) before += wave_total[w];
-    int run = before + incl - local;
-    for (int i = 0; i < per; ++i) {
-        if (r0 + i < nrows) {
-            prefix[r0 + i] = run;
-            run += parts_of(r0 + i);
-        }
-    }
-    if (threadIdx.x == kBlockThreads - 1) prefix[nrows] = before + incl;
-    __syncthreads();
-    const int num_pairs = prefix[nrows];
-    const int num_items = num_pairs * items_per_pair;
-
-    // Longest-first order (above).  prefix becomes the exclusive prefix of the
-    // rows' full partitions (the last one counts when it is full); the short
-    // final partitions follow in shortlist, their row's partition index being
-    // its full count.
-    const bool lpt = nrows <= kLptMaxRows && num_items > a.wave_slots;
+    int P = a.P;
+    int num_items = nrows * a.static_parts * items_per_pair;
+    bool lpt = false;
     int num_full = 0;
     int* shortlist = prefix + (nrows + 1);  // [nrows]: rows of the short final partitions, longest first
-    int* bins = shortlist + nrows;          // [nrows]: length class of a row's short final partition, -1 none
-    if (lpt) {
-        int full_r[kLptMaxRows / 256 + 1];  // this thread's rows r = tid + 256 j
+    if (!stat) {
+        // Partitions per row and their exclusive prefix, scanned by the whole
+        // workgroup: each thread sums a contiguous tile of rows, the 256 tile sums
+        // are scanned with DPP wave scans plus one LDS step, then each thread writes
+        // its tile's prefix entries.  A call that leaves the partition size to the
+        // library counts its tile for every candidate size in the same pass and
+        // picks the size first (power-of-two block sizes only).
+        __shared__ int wave_total[kWavesPerBlock];
+        auto parts_of = [&](int r) {
+            const int ctx = row_context(a, r);
+            return ctx > 0 ? (ctx + P - 1) / P : 0;
+        };
+        const int per = (nrows + kBlockThreads - 1) / kBlockThreads;
+        const int r0 = int(threadIdx.x) * per;
+        int local = 0;
+        if (a.num_cands > 1) {
+            int cnt[kMaxPartitionCandidates];
 #pragma unroll
-        for (int j = 0; j * 256 < kLptMaxRows; ++j) {
-            const int r = int(threadIdx.x) + 256 * j;
-            full_r[j] = 0;
-            if (r < nrows) {
-                const int np = prefix[r + 1] - prefix[r];
-                const int ctx = np > 0 ? row_context(a, r) : 0;
-                const int last = ctx - (np - 1) * P;  // tokens of the final partition
-                const bool short_last = np > 0 && last < P;
-                full_r[j] = short_last ? np - 1 : np;
-                bins[r] = short_last ? int((int64_t(last) * kLptBins) / P) : -1;
+            for (int c = 0; c < kMaxPartitionCandidates; ++c) cnt[c] = 0;
+            for (int i = 0; i < per; ++i) {
+                const int ctx = r0 + i < nrows ? row_context(a, r0 + i) : 0;
+                if (ctx > 0) {
+                    // candidates are block multiples m * bs: ceil(ctx / (m * bs)) = ceil(nb / m)
+                    const int nb = ((ctx - 1) >> a.bs_log2) + 1;
+#pragma unroll
+                    for (int c = 0; c < kMaxPartitionCandidates; ++c) {
+                        const int m = a.cands[c] >> a.bs_log2;  // >= 1 (the host pads unused entries)
+                        cnt[c] += (nb + m - 1) / m;
+                    }
+                }
             }
-        }
-        __syncthreads();  // every thread has read the partition prefix
-        // the full counts into prefix (exclusive, by a block scan of the
-        // per-thread tiles of contiguous rows)
-        const int per2 = (nrows + kBlockThreads - 1) / kBlockThreads;
+            P = __builtin_amdgcn_readfirstlane(choose_partition(a, cnt));  // wave-uniform: keep it scalar
 #pragma unroll
-        for (int j = 0; j * 256 < kLptMaxRows; ++j) {
-            const int r = int(threadIdx.x) + 256 * j;
-            if (r < nrows) shortlist[r] = full_r[j];  // (shortlist as scratch for the counts)
+            for (int c = 0; c < kMaxPartitionCandidates; ++c)
+                if (a.cands[c] == P) local = cnt[c];
+            // for the merge kernel (same stream, after this grid)
+            if (blockIdx.x == 0 && threadIdx.x == 0) a.counters[kChosenPartitionSlot] = P;
+        } else {
+            for (int i = 0; i < per; ++i)
+                if (r0 + i < nrows) local += parts_of(r0 + i);
         }
-        __syncthreads();
-        const int t0 = int(threadIdx.x) * per2;
-        int tile = 0;
-        for (int i = 0; i < per2; ++i)
-            if (t0 + i < nrows) tile += shortlist[t0 + i];
-        const int incl = wave_incl_scan(tile);
-        if (lane == kWave - 1) wave_total[threadIdx.x / kWave] = incl;
+        const int incl = wave_incl_scan(local);
+        if (lane == kWave - 1) wave_total[wave] = incl;
         __syncthreads();
         int before = 0;
-        for (int w = 0; w < int(threadIdx.x) / kWave; ++w) before += wave_total[w];
-        int run = before + incl - tile;
-        for (int i = 0; i < per2; ++i) {
-            if (t0 + i < nrows) {
-                const int c = shortlist[t0 + i];
-                prefix[t0 + i] = run;
-                run += c;
+        for (int w = 0; w < wave; ++w) before += wave_total[w];
+        int run = before + incl - local;
+        for (int i = 0; i < per; ++i) {
+            if (r0 + i < nrows) {
+                prefix[r0 + i] = run;
+                run += parts_of(r0 + i);
             }
         }
         if (threadIdx.x == kBlockThreads - 1) prefix[nrows] = before + incl;
-        __syncthreads();  // prefix complete; the counts in shortlist are no longer needed
-        num_full = prefix[nrows];
-        // short final partitions by class, longest class first: thread t takes
-        // class kLptBins - 1 - t / 4 over the quarter t % 4 of the rows; the
-        // (class, quarter) counts in thread order give each its offset
-        const int cls = kLptBins - 1 - int(threadIdx.x) / 4;
-        const int qlen = (nrows + 3) / 4;
-        const int q0 = (int(threadIdx.x) & 3) * qlen;
-        const int q1 = q0 + qlen < nrows ? q0 + qlen : nrows;
-        int cnt = 0;
-        for (int r = q0; r < q1; ++r) cnt += bins[r] == cls ? 1 : 0;
-        const int ci2 = wave_incl_scan(cnt);
-        __syncthreads();  // every wave has read wave_total above
-        if (lane == kWave - 1) wave_total[threadIdx.x / kWave] = ci2;
         __syncthreads();
-        int off = ci2 - cnt;
-        for (int w = 0; w < int(threadIdx.x) / kWave; ++w) off += wave_total[w];
-        for (int r = q0; r < q1; ++r)
-            if (bins[r] == cls) shortlist[off++] = r;
-        __syncthreads();
-    }
+        const int num_pairs = prefix[nrows];
+        num_items = num_pairs * items_per_pair;
 
+        // Longest-first order (above).  prefix becomes the exclusive prefix of the
+        // rows' full partitions (the last one counts when it is full); the short
+        // final partitions follow in shortlist, their row's partition index being
+        // its full count.
+        lpt = nrows <= kLptMaxRows && num_items > a.wave_slots;
+        int* bins = shortlist + nrows;          // [nrows]: length class of a row's short final partition, -1 none
+        if (lpt) {
+            int full_r[kLptMaxRows / 256 + 1];  // this thread's rows r = tid + 256 j
+#pragma unroll
+            for (int j = 0; j * 256 < kLptMaxRows; ++j) {
+                const int r = int(threadIdx.x) + 256 * j;
+                full_r[j] = 0;
+                if (r < nrows) {
+                    const int np = prefix[r + 1] - prefix[r];
+                    const int ctx = np > 0 ? row_context(a, r) : 0;
+                    const int last = ctx - (np - 1) * P;  // tokens of the final partition
+                    const bool short_last = np > 0 && last < P;
+                    full_r[j] = short_last ? np - 1 : np;
+                    bins[r] = short_last ? int((int64_t(last) * kLptBins) / P) : -1;
+                }
+            }
+            __syncthreads();  // every thread has read the partition prefix
+            // the full counts into prefix (exclusive, by a block scan of the
+            // per-thread tiles of contiguous rows)
+            const int per2 = (nrows + kBlockThreads - 1) / kBlockThreads;
+#pragma unroll
+            for (int j = 0; j * 256 < kLptMaxRows; ++j) {
+                const int r = int(threadIdx.x) + 256 * j;
+                if (r < nrows) shortlist[r] = full_r[j];  // (shortlist as scratch for the counts)
+            }
+            __syncthreads();
+            const int t0 = int(threadIdx.x) * per2;
+            int tile = 0;
+            for (int i = 0; i < per2; ++i)
+                if (t0 + i < nrows) tile += shortlist[t0 + i];
+            const int incl = wave_incl_scan(tile);
+            if (lane == kWave - 1) wave_total[threadIdx.x / kWave] = incl;
+            __syncthreads();
+            int before = 0;
+            for (int w = 0; w < int(threadIdx.x) / kWave; ++w) before += wave_total[w];
+            int run = before + incl - tile;
+            for (int i = 0; i < per2; ++i) {
+                if (t0 + i < nrows) {
+                    const int c = shortlist[t0 + i];
+                    prefix[t0 + i] = run;
+                    run += c;
+                }
+            }
+            if (threadIdx.x == kBlockThreads - 1) prefix[nrows] = before + incl;
+            __syncthreads();  // prefix complete; the counts in shortlist are no longer needed
+            num_full = prefix[nrows];
+            // short final partitions by class, longest class first: thread t takes
+            // class kLptBins - 1 - t / 4 over the quarter t % 4 of the rows; the
+            // (class, quarter) counts in thread order give each its offset
+            const int cls = kLptBins - 1 - int(threadIdx.x) / 4;
+            const int qlen = (nrows + 3) / 4;
+            const int q0 = (int(threadIdx.x) & 3) * qlen;
+            const int q1 = q0 + qlen < nrows ? q0 + qlen : nrows;
+            int cnt = 0;
+            for (int r = q0; r < q1; ++r) cnt += bins[r] == cls ? 1 : 0;
+            const int ci2 = wave_incl_scan(cnt);
+            __syncthreads();  // every wave has read wave_total above
+            if (lane == kWave - 1) wave_total[threadIdx.x / kWave] = ci2;
+            __syncthreads();
+            int off = ci2 - cnt;
+            for (int w = 0; w < int(threadIdx.x) / kWave; ++w) off += wave_total[w];
+            for (int r = q0; r < q1; ++r)
+                if (bins[r] == cls) shortlist[off++] = r;
+            __syncthreads();
+        }
+
+    }
     // Item groups of 4 consecutive items go to a workgroup, one item per
     // wave.  Round 0 is static: workgroup b takes group b.  Later groups
     // g >= gridDim.x are dealt in 8 interleaved sequences g = gridDim.x + 8k +
@@ -384,7 +395,7 @@ __device__ __forceinline__ void run_partitions(const DecodeArgs& a, const int it
     // one is exhausted, so every group is processed exactly once wherever the
     // workgroups run.
     __shared__ int next_group;
-    const int num_groups = (num_items + kWavesPerBlock - 1) / kWavesPerBlock;
+    const int num_groups = stat ? int(gridDim.x) : (num_items + kWavesPerBlock - 1) / kWavesPerBlock;
     const int g0 = int(gridDim.x);
     int g = blockIdx.x;
     int q = blockIdx.x % kClaimSequences;
@@ -394,10 +405,14 @@ __device__ __forceinline__ void run_partitions(const DecodeArgs& a, const int it
         if (it < num_items) {
             const int pair = it / items_per_pair;
             const int sub = it - pair * items_per_pair;
-            if (lpt && pair >= num_full) {
+            int row, part;
+            if (stat) {
+                row = pair / a.static_parts;
+                part = pair - row * a.static_parts;
+            } else if (lpt && pair >= num_full) {
                 // a short final partition: its index is the row's full count
-                const int row = shortlist[pair - num_full];
-                item(P, row, prefix[row + 1] - prefix[row], sub);
+                row = shortlist[pair - num_full];
+                part = prefix[row + 1] - prefix[row];
             } else {
                 int lo = 0, hi = nrows - 1;  // row = last r with prefix[r] <= pair
                 while (lo < hi) {
@@ -405,8 +420,10 @@ __device__ __forceinline__ void run_partitions(const DecodeArgs& a, const int it
                     if (prefix[mid] <= pair) lo = mid;
                     else hi = mid - 1;
                 }
-                item(P, lo, pair - prefix[lo], sub);
+                row = lo;
+                part = pair - prefix[lo];
             }
+            item(P, row, part, sub);
         }
         if (g0 >= num_groups) break;  // the grid covers every group: nothing to claim
         __syncthreads();

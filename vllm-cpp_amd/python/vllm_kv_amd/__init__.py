@@ -243,15 +243,20 @@ def reshape_and_cache(key, value, key_cache, value_cache, slot_mapping,
     """key/value [T, Hkv, D] (token stride from the tensor); caches [N, bs, Hkv, D];
     slot_mapping int32 [T]; FP8 caches (uint8) need key_scales/value_scales [N, bs, Hkv]."""
     _require_cuda(key, value, key_cache, value_cache, slot_mapping, key_scales, value_scales)
+    p = append_params(key, value, key_cache, value_cache, slot_mapping, key_scales, value_scales)
+    check(load().vkv_reshape_and_cache(ctypes.byref(p), _stream(stream)))
+
+
+def append_params(key, value, key_cache, value_cache, slot_mapping, key_scales=None,
+                  value_scales=None) -> AppendParams:
     T = key.shape[0]
     N, bs, Hkv, D = key_cache.shape
-    p = AppendParams(
+    return AppendParams(
         key=_ptr(key), value=_ptr(value), key_stride=key.stride(0), value_stride=value.stride(0),
         key_cache=_ptr(key_cache), value_cache=_ptr(value_cache),
         key_scales=_ptr(key_scales), value_scales=_ptr(value_scales),
         slot_mapping=_ptr(slot_mapping), num_tokens=T, num_kv_heads=Hkv, head_dim=D,
         block_size=bs, num_blocks=N, src_dtype=_dtype_code(key), cache_dtype=_dtype_code(key_cache))
-    check(load().vkv_reshape_and_cache(ctypes.byref(p), _stream(stream)))
 
 
 def kv_pool_num_blocks(budget_bytes: int, non_kv_bytes: int, num_layers: int, block_size: int,
