@@ -96,7 +96,7 @@ constexpr int kAdaptMaxRows = 4096;
 // One work item: partition `part` of row s (a sequence, or a prefill query
 // row) for kv head kvh, computed by the calling wave alone.  Writes the
 // item's partial (o, max, sum) to the workspace.
-template <typename IO, int KVT, int D, int G>
+template <typename IO, int KVT, int D, int G, bool STATIC = false>
 __device__ __forceinline__ void decode_item(const DecodeArgs& a, const int P, const int s, const int kvh,
                                             const int part, const int lane) {
     constexpr int EB = KvTraits<KVT>::bytes;
@@ -116,9 +116,9 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, const int P, co
     // table entries the partition could use are requested before the context
     // length is known (P / block_size <= 64; entries past the row's table are
     // not read), and those past the context are then dropped.
-    const bool early_table = a.static_parts > 0;
+    constexpr bool early_table = STATIC;
     int my_block = 0;
-    if (early_table) {
+    if constexpr (early_table) {
         const int tb = t0 >> a.bs_log2;
         const int nb_max = a.max_blocks_per_seq - tb < (P >> a.bs_log2) ? a.max_blocks_per_seq - tb : (P >> a.bs_log2);
         if (lane < nb_max) my_block = a.bt[int64_t(seq) * a.max_blocks_per_seq + tb + lane];
@@ -136,7 +136,7 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, const int P, co
 
     // Physical block ids of this partition, one per lane (P / block_size <= 64).
     const int nb = (n + bs_mask) >> a.bs_log2;
-    if (early_table) {
+    if constexpr (early_table) {
         if (lane >= nb || (a.num_blocks > 0 && unsigned(my_block) >= unsigned(a.num_blocks))) my_block = 0;
     } else if (lane < nb) {
         my_block = a.bt[int64_t(seq) * a.max_blocks_per_seq + (t0 >> a.bs_log2) + lane];
@@ -732,16 +732,17 @@ constexpr int min_waves_per_simd() {
     return (MFMA && ((KVT == kF16 && G > kOneChunkAboveG) || (KVT == kFp8 && G > 6))) ? 2 : kMinWavesPerSimd;
 }
 
-template <typename IO, int KVT, int D, int G, bool MFMA>
+// STATIC: the small-call variant (a static grid, static_parts > 0).
+template <typename IO, int KVT, int D, int G, bool MFMA, bool STATIC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(min_waves_per_simd<KVT, G, MFMA>())))
 void decode_partition_kernel(const DecodeArgs a) {
     __shared__ float plds[MFMA ? kWavesPerBlock : 1][MFMA ? 16 * G : 1];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
-    run_partitions(a, a.num_kv_heads, [&](const int P, const int row, const int part, const int kvh)
-                                          __attribute__((always_inline)) {
+    run_partitions<STATIC>(a, a.num_kv_heads, [&](const int P, const int row, const int part, const int kvh)
+                                                  __attribute__((always_inline)) {
         if constexpr (MFMA) decode_item_mfma<G, KVT>(a, P, row, kvh, part, lane, plds[wave]);
-        else decode_item<IO, KVT, D, G>(a, P, row, kvh, part, lane);
+        else decode_item<IO, KVT, D, G, STATIC>(a, P, row, kvh, part, lane);
     });
 }
 
@@ -836,8 +837,10 @@ void launch_g(DecodeArgs& args, int grid_x, int grid_y, int grid_z, size_t lds, 
     // (each workgroup scans the rows once, where a grid of every group pays
     // that scan per group: C5's batch measured 361 us against 382 us).  The
     // resident wave count also feeds the partition choice.
+    // Static small-call variants exist for fp16 queries (the serving case).
+    constexpr bool kStatic = std::is_same<IO, _Float16>::value;
     static std::atomic<int> reg_blocks[2];
-    auto run = [&](auto kernel, int variant) {
+    auto run = [&](auto kernel, auto static_kernel, int variant) {
         const int cus = device_cu_count();
         int per_cu = reg_blocks[variant].load(std::memory_order_relaxed);
         if (per_cu <= 0) {
@@ -851,6 +854,7 @@ void launch_g(DecodeArgs& args, int grid_x, int grid_y, int grid_z, size_t lds, 
         per_cu = blocks_per_cu(per_cu);
         const int64_t wgs = int64_t(cus) * per_cu;
         int gx = int(wgs < grid_x ? wgs : grid_x);
+        if (!kStatic) args.static_parts = 0;
         if (args.static_parts > 0) {
             // one item per wave, all resident at once, or the claim loop
             const int64_t groups = (int64_t(args.num_rows) * args.static_parts * args.num_kv_heads +
@@ -872,10 +876,16 @@ void launch_g(DecodeArgs& args, int grid_x, int grid_y, int grid_z, size_t lds, 
                                   args.num_kv_heads;
             if (worst <= args.level_waves) args.num_cands = 1;
         }
-        hipLaunchKernelGGL(kernel, dim3(gx > 0 ? gx : 1, grid_y, grid_z), dim3(kBlockThreads), lds, st, args);
+        if (args.static_parts > 0)
+            hipLaunchKernelGGL(static_kernel, dim3(gx > 0 ? gx : 1, grid_y, grid_z), dim3(kBlockThreads), lds, st, args);
+        else
+            hipLaunchKernelGGL(kernel, dim3(gx > 0 ? gx : 1, grid_y, grid_z), dim3(kBlockThreads), lds, st, args);
     };
-    if (kMfmaShape && args.bs_log2 >= 4 && args.mfma_enabled) run(decode_partition_kernel<IO, KVT, D, G, kMfmaShape>, 1);
-    else run(decode_partition_kernel<IO, KVT, D, G, false>, 0);
+    if (kMfmaShape && args.bs_log2 >= 4 && args.mfma_enabled)
+        run(decode_partition_kernel<IO, KVT, D, G, kMfmaShape, false>,
+            decode_partition_kernel<IO, KVT, D, G, kMfmaShape, kStatic>, 1);
+    else
+        run(decode_partition_kernel<IO, KVT, D, G, false, false>, decode_partition_kernel<IO, KVT, D, G, false, kStatic>, 0);
 }
 
 
@@ -1085,7 +1095,8 @@ int launch_rows(const vkv_decode_params* p, const DecodePlan& plan, void* worksp
         // Small plain decode calls (at most one (row, kv head) pair per CU):
         // a static grid over the partitions of the default size, if its waves
         // are all resident at once (decided at launch).
-        if (fixed && !qsl && !row_seq && int64_t(n) * p->num_kv_heads <= device_cu_count())
+        if (fixed && !qsl && !row_seq && p->io_dtype == VKV_DTYPE_F16 &&
+            int64_t(n) * p->num_kv_heads <= device_cu_count())
             c.static_parts = int32_t((int64_t(c.max_ctx) + c.P - 1) / c.P > 0 ? (int64_t(c.max_ctx) + c.P - 1) / c.P : 1);
         if (qsl) {
             // rows are sequences; their query rows (qsl values) stay absolute

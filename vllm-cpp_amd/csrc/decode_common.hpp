@@ -242,21 +242,22 @@ inline size_t lpt_lds_bytes(int n) { return n <= kLptMaxRows ? size_t(2) * size_
 // claim item groups dynamically, so all stay busy until the list runs out.
 // Nothing waits on another workgroup.  item(P, row, partition, sub) runs
 // one item on the calling wave.
-template <class Item>
+template <bool STATIC = false, class Item>
 __device__ __forceinline__ void run_partitions(const DecodeArgs& a, const int items_per_pair, Item&& item) {
     extern __shared__ int prefix[];  // [num_rows + 1] exclusive prefix of partitions per row
     const int lane = threadIdx.x & (kWave - 1);
     const int nrows = a.num_rows;
-    // Static (small) calls: one item per wave of a grid covering every
-    // (row, partition < static_parts, sub-item), no prefix scan, no claims.
-    const bool stat = a.static_parts > 0;
+    // STATIC (small calls, static_parts > 0): one item per wave of a grid
+    // covering every (row, partition < static_parts, sub-item), no prefix
+    // scan, no claims.
+    constexpr bool stat = STATIC;
     const int wave = threadIdx.x / kWave;
     int P = a.P;
     int num_items = nrows * a.static_parts * items_per_pair;
     bool lpt = false;
     int num_full = 0;
     int* shortlist = prefix + (nrows + 1);  // [nrows]: rows of the short final partitions, longest first
-    if (!stat) {
+    if constexpr (!stat) {
         // Partitions per row and their exclusive prefix, scanned by the whole
         // workgroup: each thread sums a contiguous tile of rows, the 256 tile sums
         // are scanned with DPP wave scans plus one LDS step, then each thread writes
@@ -405,14 +406,13 @@ __device__ __forceinline__ void run_partitions(const DecodeArgs& a, const int it
         if (it < num_items) {
             const int pair = it / items_per_pair;
             const int sub = it - pair * items_per_pair;
-            int row, part;
-            if (stat) {
-                row = pair / a.static_parts;
-                part = pair - row * a.static_parts;
+            if constexpr (stat) {
+                const int row = pair / a.static_parts;
+                item(P, row, pair - row * a.static_parts, sub);
             } else if (lpt && pair >= num_full) {
                 // a short final partition: its index is the row's full count
-                row = shortlist[pair - num_full];
-                part = prefix[row + 1] - prefix[row];
+                const int row = shortlist[pair - num_full];
+                item(P, row, prefix[row + 1] - prefix[row], sub);
             } else {
                 int lo = 0, hi = nrows - 1;  // row = last r with prefix[r] <= pair
                 while (lo < hi) {
@@ -420,10 +420,8 @@ __device__ __forceinline__ void run_partitions(const DecodeArgs& a, const int it
                     if (prefix[mid] <= pair) lo = mid;
                     else hi = mid - 1;
                 }
-                row = lo;
-                part = pair - prefix[lo];
+                item(P, lo, pair - prefix[lo], sub);
             }
-            item(P, row, part, sub);
         }
         if (g0 >= num_groups) break;  // the grid covers every group: nothing to claim
         __syncthreads();
