@@ -98,6 +98,22 @@ def test_prefill_vs_oracle(vkv, oracle, cuda, kvt, H, Hkv, D, bs, q_lens, prior)
                      f"prefill ({kvt} cache, {'host' if listed else 'in-kernel'} work list)")
 
 
+@pytest.mark.parametrize("bs", [1, 2])
+def test_prefill_small_blocks_vs_oracle(vkv, oracle, cuda, bs):
+    """fp16 D = 128 caches with one- and two-token blocks (a direct load's
+    four key rows then span blocks: per-lane block ids)."""
+    H, Hkv, D = 8, 2, 128
+    lay, ctx, qsl, q, k, v, scale = _case(H, Hkv, D, bs, [40, 1, 9], [10, 3, 0], 41 + bs)
+    import torch
+    ref = oracle.paged_prefill(q.astype(np.float32), k.view(np.uint16), v.view(np.uint16), lay.block_tables,
+                               ctx, qsl, scale)
+    out = torch.zeros(q.shape, dtype=torch.float16, device=cuda)
+    vkv.paged_prefill(out, to_dev(q, cuda), to_dev(k, cuda), to_dev(v, cuda), to_dev(lay.block_tables, cuda),
+                      to_dev(ctx, cuda), to_dev(qsl, cuda), int(np.diff(qsl).max()), scale)
+    torch.cuda.synchronize()
+    assert_close(to_np(out).astype(np.float32), ref, F16_ATOL, F16_RTOL, f"prefill bs{bs}")
+
+
 @pytest.mark.parametrize("H,Hkv,D,bs", [(28, 4, 128, 32), (16, 2, 64, 16)])  # groups 7 and 8
 def test_prefill_fp8_vs_oracle(vkv, oracle, cuda, H, Hkv, D, bs):
     """FP8 cache (quantised by the GPU append): against the oracle on the same codes and scales."""
