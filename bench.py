@@ -833,6 +833,7 @@ def _ceil_lib():
     sig = {"vkvc_mfma_loop": [vp, i32, i32, vp],
            "vkvc_read_stream": [vp, i64, vp, i32, i32, vp],
            "vkvc_read_blocks": [vp, vp, vp, i32, i64, vp, i32, i32, vp],
+           "vkvc_read_heads": [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, i32, vp, vp],
            "vkvc_copy": [vp, vp, i64, vp]}
     for name, args in sig.items():
         fn = getattr(lib, name)
@@ -930,7 +931,27 @@ def suite_ceilings(dev, steps, warmup):
         gbs, shape, nbytes = gather_ceiling(dev, pool[0], pool[1], ids, bb, stream, calls=50)
         rows[name] = {"gbs": round(gbs, 1), "frac_of_spec": round(gbs / HBM_PEAK_GBS, 4), "bytes": nbytes,
                       "blocks": int(ids.shape[0]), "block_bytes": bb, "shape": shape}
-        del pool
+        # the decode's own pattern: per (row, 768-token partition, kv head) wave, that
+        # head's slice of each token row (codes only for FP8), no math
+        P = 768
+        S, MB = lay.block_tables.shape
+        max_parts = int((int(lay.context_lens.max()) + P - 1) // P)
+        hb = cfg.head_dim * elem
+        d_bt = torch.from_numpy(lay.block_tables).to(dev)
+        d_cl = torch.from_numpy(lay.context_lens).to(dev)
+        sink = torch.empty(((S * max_parts * cfg.num_kv_heads + 3) // 4) * 256, dtype=torch.int32, device=dev)
+        run = lambda: _ck(lib.vkvc_read_heads(pool[0].data_ptr(), pool[1].data_ptr(), d_bt.data_ptr(), d_cl.data_ptr(),
+                                              S, MB, cfg.num_kv_heads, cfg.block_size, cfg.num_kv_heads * hb, hb, P,
+                                              max_parts, sink.data_ptr(), h), "vkvc_read_heads")
+        _warm(run, 3, min_ms=50.0)
+        t = _events_ms(run, 50, stream)
+        pbytes = int(lay.context_lens.astype(np.int64).sum()) * cfg.num_kv_heads * hb * 2
+        pg = pbytes / (t[0] * 1e-3) / 1e9
+        rows[name + "_decode_pattern"] = {"gbs": round(pg, 1), "frac_of_spec": round(pg / HBM_PEAK_GBS, 4),
+                                          "bytes": pbytes, "us": round(t[0] * 1e3, 1),
+                                          "pattern": f"(row, {P}-token partition, kv head) per wave, "
+                                                     f"{hb}-byte head slices, non-temporal"}
+        del pool, sink
         torch.cuda.empty_cache()
     # host link: pinned host memory <-> device, hipMemcpyAsync of 1 GiB
     nb = 1 << 30

@@ -11,6 +11,9 @@
 //   vkvc_read_blocks  read-only gather of whole KV blocks (K and V pools of
 //                     one layer) in the order of a block-id list: the decode's
 //                     byte set without its math.
+//   vkvc_read_heads   the decode's read pattern without its math: per (row,
+//                     partition, kv head) wave, that head's slice of every
+//                     token row of the partition, through the block table.
 //   vkvc_copy         hipMemcpyAsync (pinned host <-> device in bench.py's
 //                     host-link rows).
 //
@@ -116,6 +119,53 @@ __global__ __launch_bounds__(kThreads) void read_blocks_kernel(const uint4* __re
     out[int64_t(blockIdx.x) * kThreads + threadIdx.x] = x;
 }
 
+// The decode's own read pattern without its math: items (row, partition of P
+// tokens, kv head), kv head fastest, one per wave (4 per workgroup), each
+// reading its partition's K and V head slices (head_bytes of every token,
+// through the block table) with 16-byte non-temporal loads.  As in the
+// decode, the partition's block ids are loaded once, one per lane (P / bs <=
+// 64), and each lane keeps U loads per pool in flight.
+__global__ __launch_bounds__(kThreads) void read_heads_kernel(const char* __restrict__ k, const char* __restrict__ v,
+                                                              const int32_t* __restrict__ bt,
+                                                              const int32_t* __restrict__ cl, int S, int MB, int Hkv,
+                                                              int bs, int row_bytes, int head_bytes, int P,
+                                                              int max_parts, uint32_t* __restrict__ out) {
+    constexpr int U = 8;
+    const int lane = threadIdx.x & 63;
+    const int64_t item = int64_t(blockIdx.x) * (kThreads / 64) + threadIdx.x / 64;
+    uint32_t x = 0;
+    if (item < int64_t(S) * max_parts * Hkv) {
+        const int h = int(item % Hkv);
+        const int part = int((item / Hkv) % max_parts);
+        const int s = int(item / (int64_t(Hkv) * max_parts));
+        const int ctx = cl[s];
+        const int t0 = part * P;  // a multiple of bs
+        const int n = ctx - t0 < P ? ctx - t0 : P;
+        const int nb = n > 0 ? (n + bs - 1) / bs : 0;
+        const int my_block = lane < nb ? bt[int64_t(s) * MB + t0 / bs + lane] : 0;
+        const int lpt = head_bytes / 16;  // lanes per token
+        const int tpl = 64 / lpt;         // tokens per wave-wide load
+        const int sub = lane % lpt, grp = lane / lpt;
+        for (int c = 0; c < n; c += U * tpl) {
+            uint4 a[U], b[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int rel = c + u * tpl + grp;
+                const int blk = __shfl(my_block, (rel / bs) & 63);
+                a[u] = b[u] = uint4{0, 0, 0, 0};
+                if (rel < n) {
+                    const int64_t off = (int64_t(blk) * bs + rel % bs) * row_bytes + int64_t(h) * head_bytes + sub * 16;
+                    a[u] = load16<true>(reinterpret_cast<const uint4*>(k + off));
+                    b[u] = load16<true>(reinterpret_cast<const uint4*>(v + off));
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) x ^= fold(a[u]) ^ fold(b[u]);
+        }
+    }
+    out[int64_t(blockIdx.x) * kThreads + threadIdx.x] = x;
+}
+
 }  // namespace
 
 extern "C" {
@@ -155,6 +205,25 @@ int vkvc_read_blocks(const void* k, const void* v, const int32_t* ids, int n_ids
         read_blocks_kernel<true><<<blocks, kThreads, 0, stream>>>(kp, vp, ids, n_ids, b16, out);
     else
         read_blocks_kernel<false><<<blocks, kThreads, 0, stream>>>(kp, vp, ids, n_ids, b16, out);
+    return int(hipGetLastError());
+}
+
+// The decode pattern (read_heads_kernel): bt [S][MB] and cl [S] on the
+// device, every table entry a valid block of the pools, cl <= MB * bs; P a
+// multiple of bs with P / bs <= 64; head_bytes a multiple of 16 dividing
+// 1 024; out: ceil(S * max_parts * Hkv / 4) * 256 words.
+int vkvc_read_heads(const void* k, const void* v, const int32_t* bt, const int32_t* cl, int S, int MB, int Hkv,
+                    int bs, int row_bytes, int head_bytes, int P, int max_parts, uint32_t* out, hipStream_t stream) {
+    if (!k || !v || !bt || !cl || !out || S <= 0 || MB <= 0 || Hkv <= 0 || bs <= 0 || P <= 0 || max_parts <= 0 ||
+        head_bytes < 16 || (head_bytes & 15) || 1024 % head_bytes || row_bytes < Hkv * head_bytes || P % bs ||
+        P / bs > 64)
+        return int(hipErrorInvalidValue);
+    const int64_t items = int64_t(S) * max_parts * Hkv;
+    const int64_t blocks = (items + 3) / 4;
+    if (blocks > INT32_MAX) return int(hipErrorInvalidValue);
+    read_heads_kernel<<<int(blocks), kThreads, 0, stream>>>(static_cast<const char*>(k), static_cast<const char*>(v),
+                                                           bt, cl, S, MB, Hkv, bs, row_bytes, head_bytes, P,
+                                                           max_parts, out);
     return int(hipGetLastError());
 }
 
