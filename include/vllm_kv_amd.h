@@ -261,9 +261,11 @@ int vkv_release_workspace(vkv_stream_t stream);
  * capture, serving loops and harnesses that forbid hipMalloc).  Same
  * arguments, kernels and results as vkv_paged_decode, except that workspace /
  * workspace_bytes are ignored: the split-K partials and claim counters live in
- * a fixed 64 MiB device array of the library (one per device, held from the
- * first call on that device until the process ends; the counters are cleared
- * by a kernel at the start of each call).  A call whose
+ * a fixed 64 MiB device array of the library (the counters are cleared by a
+ * kernel at the start of each call).  The array is part of the library's code
+ * object: every process that runs any of this library's kernels on a device
+ * holds those 64 MiB of HBM on it, from the library's first use there until
+ * the process ends, whether or not it ever calls this entry point.  A call whose
  * vkv_paged_decode_workspace_size() exceeds 64 MiB fails with
  * VKV_ERR_WORKSPACE before any launch.  All calls on one device share the
  * array: calls that overlap on one device (other streams, other threads) race
