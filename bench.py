@@ -1089,9 +1089,103 @@ def _decode_beside_swap(dev, planes, host, nsw, out_pairs, in_pairs, swap_bytes,
     return res
 
 
+def suite_shapes(dev, steps, warmup):
+    """Decode at shapes outside the benchmark configurations (the reference's
+    whole shape domain, src/attention/paged_attention.cu:19-38: any head_dim,
+    group size and block size, fp32 tensors), each on C2's 64 sequences
+    (ctx U[512,4096], seed 1), and chunked prefill at head_dim 64 (the C1
+    model's heads on C3's 8 chunks).  One JSON line with a row per shape."""
+    import numpy as np
+    import torch
+    import vllm_kv_amd as vkv
+    from vllm_kv_amd import workloads
+    c2 = workloads.config2()
+    ctx = c2.layout.context_lens
+    S = ctx.shape[0]
+    stream = torch.cuda.current_stream()
+    rows = []
+    # (label, H, Hkv, D, block size, tensor dtype, kernel family)
+    shapes = [("reference API: fp32 q / KV / out", 32, 8, 128, 16, torch.float32, "fixed"),
+              ("head_dim 80", 32, 8, 80, 16, torch.float16, "generic"),
+              ("head_dim 96", 32, 8, 96, 16, torch.float16, "generic"),
+              ("head_dim 112", 32, 8, 112, 16, torch.float16, "generic"),
+              ("group 16 (H32 / Hkv2)", 32, 2, 128, 16, torch.float16, "generic"),
+              ("MQA (H32 / Hkv1)", 32, 1, 128, 16, torch.float16, "generic"),
+              ("block size 12", 32, 8, 128, 12, torch.float16, "generic"),
+              ("block size 24", 32, 8, 128, 24, torch.float16, "generic"),
+              ("fixed shape for comparison (C2: H32 / Hkv8 / D128 / bs16)", 32, 8, 128, 16, torch.float16, "fixed")]
+    for label, H, Hkv, D, bs, dt, fam in shapes:
+        lay = workloads.make_layout(ctx, bs, np.random.default_rng(1))
+        g = torch.Generator(device=dev).manual_seed(1)
+        kc = (torch.randn((lay.num_blocks, bs, Hkv, D), generator=g, device=dev) * c2.sigma).to(dt)
+        vc = (torch.randn((lay.num_blocks, bs, Hkv, D), generator=g, device=dev) * c2.sigma).to(dt)
+        q = (torch.randn((S, H, D), generator=g, device=dev) * c2.sigma).to(dt)
+        bt = torch.from_numpy(lay.block_tables).to(dev)
+        cl = torch.from_numpy(lay.context_lens).to(dev)
+        out = torch.empty_like(q)
+        scale = 1.0 / float(np.sqrt(D))
+
+        def decode():
+            vkv.paged_decode(out, q, kc, vc, bt, cl, scale, stream=stream)
+
+        _warm(decode, warmup, min_ms=100.0)
+        t = _events_ms(decode, steps, stream)
+        kvb = int(ctx.astype(np.int64).sum()) * Hkv * 2 * D * kc.element_size()
+        gbs = kvb / (t[0] * 1e-3) / 1e9
+        rows.append({"shape": label, "H": H, "Hkv": Hkv, "D": D, "block_size": bs,
+                     "dtype": "f32" if dt == torch.float32 else "f16", "kernels": fam,
+                     "us_median": round(t[0] * 1e3, 2), "us_p10_p90": [round(t[1] * 1e3, 2), round(t[2] * 1e3, 2)],
+                     "kv_bytes": kvb, "gbs": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)})
+        log(f"[shapes] {label}: {t[0] * 1e3:.1f} us, {gbs:.0f} GB/s")
+        del kc, vc, q, out
+        torch.cuda.empty_cache()
+    # prefill at head_dim 64: Qwen2.5-0.5B heads (H14 / Hkv2 / D64, bs16) on C3's 8 chunks
+    c3 = workloads.config3()
+    npf = int((c3.q_lens > 1).sum())
+    ql = c3.q_lens[:npf]
+    cl_np = c3.layout.context_lens[:npf]
+    H, Hkv, D, bs = 14, 2, 64, 16
+    lay = workloads.make_layout(cl_np, bs, np.random.default_rng(2))
+    g = torch.Generator(device=dev).manual_seed(2)
+    kc = _rand_half((lay.num_blocks, bs, Hkv, D), g, dev, 0.3)
+    vc = _rand_half((lay.num_blocks, bs, Hkv, D), g, dev, 0.3)
+    qsl_np = np.concatenate([[0], np.cumsum(ql)]).astype(np.int32)
+    q = _rand_half((int(qsl_np[-1]), H, D), g, dev, 0.3)
+    bt = torch.from_numpy(lay.block_tables).to(dev)
+    cl = torch.from_numpy(cl_np).to(dev)
+    qsl = torch.from_numpy(qsl_np).to(dev)
+    out = torch.empty_like(q)
+    scale = 1.0 / float(np.sqrt(D))
+    k8 = torch.empty((lay.num_blocks, bs, Hkv, D), dtype=torch.uint8, device=dev)
+    v8 = torch.empty_like(k8)
+    ks8 = torch.empty((lay.num_blocks, bs, Hkv), dtype=torch.float32, device=dev)
+    vs8 = torch.empty_like(ks8)
+    slots = torch.arange(lay.num_blocks * bs, dtype=torch.int32, device=dev)
+    vkv.reshape_and_cache(kc.reshape(-1, Hkv, D), vc.reshape(-1, Hkv, D), k8, v8, slots, ks8, vs8)
+    keys = sum(int(c3.prior_lens[s]) * int(ql[s]) + int(ql[s]) * (int(ql[s]) + 1) // 2 for s in range(npf))
+    flops = 4.0 * D * H * keys
+    for label, kk, vv, ksc, vsc in (("prefill head_dim 64, fp16 cache", kc, vc, None, None),
+                                    ("prefill head_dim 64, FP8 cache", k8, v8, ks8, vs8)):
+        def attn():
+            vkv.paged_prefill(out, q, kk, vv, bt, cl, qsl, int(ql.max()), scale, key_scales=ksc,
+                              value_scales=vsc, stream=stream, multi_token_only=True)
+
+        _warm(attn, warmup, min_ms=100.0)
+        t = _events_ms(attn, steps, stream)
+        tf = flops / (t[0] * 1e-3) / 1e12
+        rows.append({"shape": label, "H": H, "Hkv": Hkv, "D": D, "block_size": bs, "dtype": "f16",
+                     "us_median": round(t[0] * 1e3, 2), "us_p10_p90": [round(t[1] * 1e3, 2), round(t[2] * 1e3, 2)],
+                     "gflop": round(flops / 1e9, 2), "tflops": round(tf, 1), "frac_of_mfma_peak": round(tf / 2500.0, 4)})
+        log(f"[shapes] {label}: {t[0] * 1e3:.1f} us, {tf:.0f} TFLOP/s")
+    return {"row": "other shapes", "workload": "decode: C2's 64 sequences (ctx U[512,4096], seed 1) at each shape; "
+                                              "prefill: C3's 8 chunks (512 tokens on prior U[0,2048], seed 2) "
+                                              "at H14 / Hkv2 / D64",
+            "rows": rows}
+
+
 SUITES = {"ceil": suite_ceilings, "stream": suite_stream, "c1": suite_c1, "append": suite_append, "rope": suite_rope, "step": suite_step,
           "c3": suite_c3,
-          "c3p": suite_c3_prefill_only, "c5": suite_c5, "c4": suite_c4}
+          "c3p": suite_c3_prefill_only, "c5": suite_c5, "c4": suite_c4, "shapes": suite_shapes}
 
 
 def run_suite(names, steps, warmup):

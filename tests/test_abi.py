@@ -198,7 +198,7 @@ def test_prefill_argument_errors_and_workspace(vkv):
     assert lib.vkv_paged_prefill_workspace_size(ctypes.byref(_prefill_params(vkv, head_dim=0))) == 0
 
 
-@pytest.mark.parametrize("shape", [(28, 4, 128, 32, 1, 1), (32, 8, 128, 16, 1, 2), (16, 2, 64, 16, 1, 1),
+@pytest.mark.parametrize("shape", [(28, 4, 128, 32, 1, 1), (32, 8, 128, 16, 1, 2), (16, 8, 64, 16, 1, 1),
                                    (32, 2, 128, 16, 1, 1)])
 def test_prefill_work_list_host(vkv, shape):
     """vkv_prefill_work_list_host (no GPU): every work item (sequence, row block,
@@ -243,11 +243,15 @@ def test_prefill_work_list_host(vkv, shape):
     assert sorted(got) == sorted(want) and len(got) == len(set(got))
     t = [tiles[it] for it in got]
     assert t == sorted(t, reverse=True)  # longest first
-    # shapes without the list: fp32 queries, FP8 at head_dim 64
+    # shapes without the list: fp32 queries, FP8 at head_dim 64, and fp16 at
+    # head_dim 64 with groups of 4 heads or more (the register-staged kernel)
     p32 = _prefill_params(vkv, io_dtype=0, kv_dtype=0)
     assert lib.vkv_prefill_work_list_host(ctypes.byref(p32), qsl.ctypes.data, ctx.ctypes.data, None, 0) == 0
     p8 = _prefill_params(vkv, head_dim=64, kv_dtype=2)
     assert lib.vkv_prefill_work_list_host(ctypes.byref(p8), qsl.ctypes.data, ctx.ctypes.data, None, 0) == 0
+    p64 = _prefill_params(vkv, num_seqs=q_lens.size, num_query_tokens=int(qsl[-1]), max_query_len=int(q_lens.max()),
+                          num_heads=16, num_kv_heads=4, head_dim=64, block_size=16, max_blocks_per_seq=mb)
+    assert lib.vkv_prefill_work_list_host(ctypes.byref(p64), qsl.ctypes.data, ctx.ctypes.data, None, 0) == 0
     assert lib.vkv_prefill_work_list_host(ctypes.byref(p), None, ctx.ctypes.data, None, 0) == -1
     # a negative length is refused before any launch
     assert lib.vkv_paged_prefill(ctypes.byref(_prefill_params(vkv, work_list_words=-1)), None) == -2

@@ -7,11 +7,12 @@
 // sequence's paged cache, i.e. causal attention over the prior context plus
 // the chunk.  Keys are gathered through the block table like decode.
 //
-// The kernels share the matrix-core layout below: prefill_wide_kernel for fp16
-// caches (work items of (token, head) rows, tiles staged by direct
-// global->LDS loads), prefill_wide8_kernel for FP8 caches at head_dim 128 (the
-// same, with the code tiles converted to fp16 in LDS once per workgroup) and
-// prefill_mfma_kernel for FP8 caches at head_dim 64.  In the last a
+// The kernels share the matrix-core layout below: prefill_w64_kernel (fp16
+// caches at head_dim 128) and prefill_wide_kernel (fp16 caches at head_dim 64
+// with groups below 4 heads): work items of (token, head) rows, tiles staged
+// by direct global->LDS loads; prefill_wide8_kernel for FP8 caches at head_dim
+// 128 (the same, with the code tiles converted to fp16 in LDS once per
+// workgroup); prefill_mfma_kernel for the rest of head_dim 64.  In the last a
 // workgroup owns (sequence, kv head, block of kBQ = 32 query tokens); wave w
 // computes query head kvh * G + w for those 32 tokens as two 16-row MFMA
 // tiles, so the G heads that share a kv head share every K/V tile staged in
@@ -44,6 +45,12 @@
 // 8-wave kernel instead of the one-wave-per-SIMD kernel (an A/B switch).
 #ifndef VKV_PREFILL_W64
 #define VKV_PREFILL_W64 1
+#endif
+// Building with -DVKV_PREFILL_D64_WIDE=1 runs fp16 caches at head_dim 64 on
+// the 8-wave direct-load kernel for every group size (an A/B switch; by
+// default groups of 4 and more take the register-staged kernel).
+#ifndef VKV_PREFILL_D64_WIDE
+#define VKV_PREFILL_D64_WIDE 0
 #endif
 
 namespace vkv {
@@ -1427,14 +1434,6 @@ __device__ __forceinline__ void prefill_block_w64(const PrefillArgs& a, const in
                            qop[3][i]);
         score_fence(sv);
     };
-    auto read_v = [&](const char* vb, half8_t (&vop)[DT]) __attribute__((always_inline)) {
-#pragma unroll
-        for (int t = 0; t < DT; ++t) {
-            const u32x2 lo = tr_read(vb + voff[t]);
-            const u32x2 hi = tr_read(vb + voff[t] + 16 * T::ROW);
-            vop[t] = __builtin_bit_cast(half8_t, u32x4{lo[0], lo[1], hi[0], hi[1]});
-        }
-    };
     // causal / context mask: key kbase + 16 hh + 4 grp + e < rctx
     auto mask = [&](const int kbase, float4_t (&sv)[RT][2]) __attribute__((always_inline)) {
         bool edge = false;
@@ -1804,10 +1803,18 @@ bool prefill_mfma_supported(const vkv_prefill_params* p) {
 
 namespace {
 
-// fp16 caches and FP8 caches at D = 128 run on the direct-load kernels, whose
-// items are Wide<D>::ROWS (token, head) rows; FP8 at D = 64 on
-// prefill_mfma_kernel, whose items are kBQ query tokens (of every head).
-bool wide_path(const vkv_prefill_params* p) { return p->kv_dtype == VKV_DTYPE_F16 || p->head_dim == 128; }
+// D = 128, and fp16 caches at D = 64 with groups below 4 heads, run on the
+// direct-load kernels, whose items are Wide<D>::ROWS (token, head) rows; the
+// rest of D = 64 on prefill_mfma_kernel, whose items are kBQ query tokens of
+// every head of a kv head (a wave per head, at least 4 waves: smaller groups
+// would leave waves idle).  Measured on C3's chunks at D = 64, fp16 cache:
+// groups of 7 73.5 us on the staged kernel against 88.0 on the direct-load
+// one, groups of 4 89.2 against 91.7, groups of 1 138.4 against 101.8.
+bool wide_path(const vkv_prefill_params* p) {
+    if (p->head_dim == 128) return true;
+    const int G = p->num_kv_heads > 0 ? p->num_heads / p->num_kv_heads : 1;
+    return p->kv_dtype == VKV_DTYPE_F16 && (VKV_PREFILL_D64_WIDE || G < kMinWaves);
+}
 int rows_per_item(const vkv_prefill_params* p) {
     if (!wide_path(p)) return kBQ;
     return p->head_dim == 128 ? Wide<128>::ROWS : Wide<64>::ROWS;
@@ -1842,9 +1849,9 @@ int launch_prefill_mfma(const vkv_prefill_params* p, void* item_space, int32_t* 
     a.num_heads = p->num_heads;
     a.num_kv_heads = p->num_kv_heads;
     a.group = p->num_heads / p->num_kv_heads;
-    // fp16 caches and FP8 caches at D = 128: prefill_wide_kernel /
-    // prefill_wide8_kernel, Wide<D>::ROWS (token, head) rows per item; FP8 at
-    // D = 64: prefill_mfma_kernel, up to kMaxWaves heads x kBQ tokens per item
+    // wide_path(): prefill_w64_kernel / prefill_wide_kernel /
+    // prefill_wide8_kernel, Wide<D>::ROWS (token, head) rows per item; else
+    // prefill_mfma_kernel, up to kMaxWaves heads x kBQ tokens per item
     const bool wide = wide_path(p);
     const int head_groups = wide ? 1 : (a.group + kMaxWaves - 1) / kMaxWaves;
     a.heads_per_wg = (a.group + head_groups - 1) / head_groups;
@@ -1904,6 +1911,7 @@ int launch_prefill_mfma(const vkv_prefill_params* p, void* item_space, int32_t* 
         else hipLaunchKernelGGL(prefill_wide8_kernel, grid, block, 0, st, a);
     } else {
         if (wide) hipLaunchKernelGGL((prefill_wide_kernel<64>), grid, block, 0, st, a);
+        else if (p->kv_dtype == VKV_DTYPE_F16) hipLaunchKernelGGL((prefill_mfma_kernel<64, kF16>), grid, block, 0, st, a);
         else hipLaunchKernelGGL((prefill_mfma_kernel<64, kFp8>), grid, block, 0, st, a);
     }
     return 0;
