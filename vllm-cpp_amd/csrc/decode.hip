@@ -918,7 +918,10 @@ int dispatch_d(int D, int G, DecodeArgs& args, int grid_x, int Hkv, int S, size_
 // The same merge at head_dim DT = 128 or 256 with one wave per (sequence,
 // head) and E = DT / 64 consecutive elements per lane: measured C2 0.2-0.4 us
 // and C5 1-2 us faster than a thread per element (at DT = 64 a thread per
-// element is one wave already, and stays).
+// element is one wave already, and stays).  The wave reads the context length
+// first and then loads only the row's own partials: measured C2 0.4-0.8 us and
+// C5 1-1.5 us faster than loading the first B slots beside the context length
+// (their bytes, twice the partials' at C5, cost more than the round trip).
 template <typename IO, int DT, int B>
 __global__ __launch_bounds__(kWave) void decode_reduce_wave_kernel(DecodeArgs a) {
     constexpr int E = DT / kWave;
@@ -933,22 +936,24 @@ __global__ __launch_bounds__(kWave) void decode_reduce_wave_kernel(DecodeArgs a)
     const int64_t slot0 = (int64_t(s) * a.num_kv_heads + kvh) * a.max_parts * G + (h - kvh * G);
     const float* ml = a.part_ml + slot0 * 2;
     const float* o = a.part_o + slot0 * DT + d;
+    if (a.qsl && a.qsl[s + 1] - a.qsl[s] != 1) return;
+    const int ctx = row_context(a, s);
+    const int P = a.num_cands > 1 ? __builtin_amdgcn_readfirstlane(a.counters[kChosenPartitionSlot]) : a.P;
+    const int np = ctx > 0 ? (ctx + P - 1) / P : 0;
+    // partials of batch i0 (slots past np are neither loaded nor read)
     float bm[B], bl[B];
     fE bo[B];
     auto load_batch = [&](int i0) __attribute__((always_inline)) {
 #pragma unroll
         for (int k = 0; k < B; ++k) {
-            const int i = i0 + k < a.max_parts ? i0 + k : a.max_parts - 1;  // in-bounds slot
-            bm[k] = ml[int64_t(i) * G * 2];
-            bl[k] = ml[int64_t(i) * G * 2 + 1];
-            bo[k] = *reinterpret_cast<const fE*>(o + int64_t(i) * G * DT);
+            if (i0 + k < np) {
+                bm[k] = ml[int64_t(i0 + k) * G * 2];
+                bl[k] = ml[int64_t(i0 + k) * G * 2 + 1];
+                bo[k] = *reinterpret_cast<const fE*>(o + int64_t(i0 + k) * G * DT);
+            }
         }
     };
-    if (a.qsl && a.qsl[s + 1] - a.qsl[s] != 1) return;
     load_batch(0);
-    const int ctx = row_context(a, s);
-    const int P = a.num_cands > 1 ? __builtin_amdgcn_readfirstlane(a.counters[kChosenPartitionSlot]) : a.P;
-    const int np = ctx > 0 ? (ctx + P - 1) / P : 0;
     float m = -INFINITY, l = 0.0f;
     float acc[E];
 #pragma unroll
