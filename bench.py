@@ -181,6 +181,12 @@ def main():
         vkv.paged_decode(out, q, kc, vc, bt, cl, cfg.scale, workspace=ws, stream=stream, partition_size=P)
 
     def step():
+        # one decode step of the attention layer: the append of each
+        # sequence's new token fused into the decode launches
+        vkv.paged_decode_append(out, q, kc, vc, bt, cl, cfg.scale, nk, nv, slots, workspace=ws, stream=stream,
+                                partition_size=P)
+
+    def step_two_calls():
         append()
         decode()
 
@@ -205,6 +211,9 @@ def main():
         f"{lay.num_blocks} blocks ({2 * kc.numel() * 2 / 1e9:.2f} GB K+V)")
     ms_step = timed(step, args.steps)
     log(f"[bench] timed {args.steps} steps: {ms_step * 1e3:.1f} us/step")
+    _warm(step_two_calls, 0, min_ms=50.0)
+    ms_step2 = timed(step_two_calls, args.steps)
+    log(f"[bench] the same steps as two calls (append, then decode): {ms_step2 * 1e3:.1f} us/step")
     # the decode call alone: median, p10 and p90 over DECODE_GROUPS samples,
     # each the mean of DECODE_CALLS back-to-back calls
     dec = _events_ms(decode, DECODE_GROUPS * DECODE_CALLS, stream, groups=DECODE_GROUPS)
@@ -245,7 +254,8 @@ def main():
         "dtype": "f16",
         "data": "synthetic",
         "config": {"workload": "C2: Llama-3-8B-shaped paged decode, one layer, H32/Hkv8/D128 fp16, bs16, "
-                               "B=64, ctx U[512,4096], append 1 token + decode per step",
+                               "B=64, ctx U[512,4096], append 1 token + decode per step "
+                               "(vkv_paged_decode_append: the append fused into the decode launches)",
                    "global_batch": S, "context_tokens": int(lay.context_lens.sum()), "seed": cfg.seed},
         "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
         "decode_tokens_per_s": round(S / (ms_step * 1e-3), 1),
@@ -256,6 +266,9 @@ def main():
                          "calls timed with HIP events on the launch stream",
         "warm_steps": warm_steps,
         "warm_ms": round(warm_ms, 1),
+        "step_us_two_calls": round(ms_step2 * 1e3, 2),
+        "step_two_calls_note": "the same step as vkv_reshape_and_cache then vkv_paged_decode (the reference's "
+                               "call pattern), timed after the headline steps",
         "append_us": round(ms_append * 1e3, 2),
         "append_gbs": round(append_bytes / (ms_append * 1e-3) / 1e9, 2),
         "kv_bytes_per_call": kv_bytes,
@@ -509,8 +522,13 @@ def suite_c1(dev, steps, warmup):
         vkv.reshape_and_cache(nk, nv, kc, vc, slots, stream=stream)
         vkv.paged_decode(out, q, kc, vc, bt, cl, cfg.scale, stream=stream)
 
+    def fused_step():
+        vkv.paged_decode_append(out, q, kc, vc, bt, cl, cfg.scale, nk, nv, slots, stream=stream)
+
     _warm(step, warmup)
     t = _events_ms(step, steps, stream)
+    _warm(fused_step, warmup)
+    tf = _events_ms(fused_step, steps, stream)
     kvb = cfg.kv_bytes(2)
     # The same step captured once in a HIP graph and replayed (the launch-bound
     # case graphs are for): the capture stream's library workspace is sized by
@@ -545,7 +563,10 @@ def suite_c1(dev, steps, warmup):
     return {"row": "C1 append + decode", "workload": "Qwen2.5-0.5B shape H14/Hkv2/D64 fp16 bs16, B=4, ctx U[1,512]",
             "kv_bytes": kvb, "step_us_median": round(t[0] * 1e3, 2),
             "step_us_p10_p90": [round(t[1] * 1e3, 2), round(t[2] * 1e3, 2)],
-            "note": "launch-bound: three kernels (append, partition, merge) for 0.6 MB of KV",
+            "fused_step_us_median": round(tf[0] * 1e3, 2),
+            "fused_step_us_p10_p90": [round(tf[1] * 1e3, 2), round(tf[2] * 1e3, 2)],
+            "note": "launch-bound: three kernels (append, partition, merge) for 0.6 MB of KV; "
+                    "vkv_paged_decode_append fuses the append into the decode's two",
             "graph_step_us_median": round(tg[0] * 1e3, 2), "graph_output_equals_eager": graph_equal,
             "native_caller": native,
             "cpu_baseline": {"us_per_step": round(sec * 1e6, 1), "cores": 1, "kind": "port",
@@ -564,33 +585,34 @@ def _native_c1(vkv, nk, nv, kc, vc, slots, out, q, bt, cl, scale, stream, steps,
         raise RuntimeError(f"{STEPLOOP_LIB} not built: run __graft_entry__.build()")
     lib = ctypes.CDLL(STEPLOOP_LIB)
     vp = ctypes.c_void_p
-    lib.vkvb_step_loop.argtypes = [vp, vp, ctypes.c_int, vp]
-    lib.vkvb_graph_create.argtypes = [vp, vp, ctypes.POINTER(vp)]
+    lib.vkvb_step_loop.argtypes = [vp, vp, ctypes.c_int, ctypes.c_int, vp]
+    lib.vkvb_graph_create.argtypes = [vp, vp, ctypes.c_int, ctypes.POINTER(vp)]
     lib.vkvb_graph_launch.argtypes = [vp, ctypes.c_int, vp]
     lib.vkvb_graph_destroy.argtypes = [vp]
     ap = vkv.append_params(nk, nv, kc, vc, slots)
     dp = vkv.decode_params(out, q, kc, vc, bt, cl, scale)
     h = stream.cuda_stream
     n = max(steps, 100)
+    res = {"sample": f"5 samples of {n} back-to-back steps each"}
+    for fused, tag in ((0, "two_calls"), (1, "fused")):
+        def eager():
+            _ck(lib.vkvb_step_loop(ctypes.byref(ap), ctypes.byref(dp), n, fused, h), "vkvb_step_loop")
 
-    def eager():
-        _ck(lib.vkvb_step_loop(ctypes.byref(ap), ctypes.byref(dp), n, h), "vkvb_step_loop")
-
-    _warm(eager, warmup, min_ms=100.0)
-    t = _events_ms(eager, 5, stream, groups=5)
-    g = vp()
-    _ck(lib.vkvb_graph_create(ctypes.byref(ap), ctypes.byref(dp), ctypes.byref(g)), "vkvb_graph_create")
-    try:
-        def replay():
-            _ck(lib.vkvb_graph_launch(g, n, h), "vkvb_graph_launch")
-        _warm(replay, warmup, min_ms=100.0)
-        tg = _events_ms(replay, 5, stream, groups=5)
-    finally:
-        lib.vkvb_graph_destroy(g)
-    return {"eager_step_us_median": round(t[0] * 1e3 / n, 2),
-            "eager_step_us_p10_p90": [round(t[1] * 1e3 / n, 2), round(t[2] * 1e3 / n, 2)],
-            "graph_step_us_median": round(tg[0] * 1e3 / n, 2),
-            "sample": f"5 samples of {n} back-to-back steps each"}
+        _warm(eager, warmup, min_ms=100.0)
+        t = _events_ms(eager, 5, stream, groups=5)
+        g = vp()
+        _ck(lib.vkvb_graph_create(ctypes.byref(ap), ctypes.byref(dp), fused, ctypes.byref(g)), "vkvb_graph_create")
+        try:
+            def replay():
+                _ck(lib.vkvb_graph_launch(g, n, h), "vkvb_graph_launch")
+            _warm(replay, warmup, min_ms=100.0)
+            tg = _events_ms(replay, 5, stream, groups=5)
+        finally:
+            lib.vkvb_graph_destroy(g)
+        res[tag] = {"eager_step_us_median": round(t[0] * 1e3 / n, 2),
+                    "eager_step_us_p10_p90": [round(t[1] * 1e3 / n, 2), round(t[2] * 1e3 / n, 2)],
+                    "graph_step_us_median": round(tg[0] * 1e3 / n, 2)}
+    return res
 
 
 def suite_c5(dev, steps, warmup):
@@ -1109,6 +1131,8 @@ def suite_shapes(dev, steps, warmup):
               ("head_dim 80", 32, 8, 80, 16, torch.float16, "generic"),
               ("head_dim 96", 32, 8, 96, 16, torch.float16, "generic"),
               ("head_dim 112", 32, 8, 112, 16, torch.float16, "generic"),
+              ("head_dim 80, MHA (Phi-2's heads: H32 / Hkv32)", 32, 32, 80, 16, torch.float16, "generic"),
+              ("head_dim 96, MHA (Phi-3-mini's heads: H32 / Hkv32)", 32, 32, 96, 16, torch.float16, "generic"),
               ("group 16 (H32 / Hkv2)", 32, 2, 128, 16, torch.float16, "generic"),
               ("MQA (H32 / Hkv1)", 32, 1, 128, 16, torch.float16, "generic"),
               ("block size 12", 32, 8, 128, 12, torch.float16, "generic"),

@@ -245,6 +245,24 @@ typedef struct vkv_decode_params {
 size_t vkv_paged_decode_workspace_size(const vkv_decode_params* p);
 int vkv_paged_decode(const vkv_decode_params* p, vkv_stream_t stream);
 
+/* One decode step of the attention layer: the append of each sequence's new
+ * token, then the decode, as in the reference's AttentionLayer::forward (the
+ * per-token slot copies, src/layers/attention.cpp:81-101, then
+ * paged_attention_forward, :103-127).  Results, cache contents and errors are
+ * those of vkv_reshape_and_cache(ap) followed by vkv_paged_decode(dp) on the
+ * same stream (workspace as for vkv_paged_decode).  When the two fit together
+ * — token s of ap is sequence s's new token (ap->num_tokens == dp->num_seqs),
+ * both name the same fp16 caches with the same geometry and pool, fp16
+ * source rows 16-byte aligned with token strides a multiple of 8 elements, and
+ * a shape the tuned decode kernels run — the append is fused into the decode
+ * launches (one launch fewer per step): each sequence's last position is read
+ * from its new rows when ap's slot for the token is that position's slot, and
+ * the merge kernel stores the rows.  The fused form assumes what a decode step
+ * guarantees: the slot of an appended token is read in this call only as its
+ * own sequence's last position (a slot of no other sequence's context).
+ * Otherwise the two calls run as they are. */
+int vkv_paged_decode_append(const vkv_append_params* ap, const vkv_decode_params* dp, vkv_stream_t stream);
+
 /* Frees the workspace buffers the library keeps for `stream` on the current
  * device (the ones decode and prefill calls with workspace == NULL use), after
  * synchronising the stream; for hipStreamPerThread, the calling thread's.  No

@@ -86,6 +86,25 @@ def test_workspace_size_formula(vkv):
     assert lib.vkv_paged_decode_workspace_size(ctypes.byref(p)) == 1024 + 64 * 32 * 9 * (128 + 2) * 4
 
 
+def test_decode_append_argument_errors(vkv):
+    """vkv_paged_decode_append checks both parameter blocks first (no GPU)."""
+    lib = vkv.load()
+    dp = _decode_params(vkv)
+    ap = vkv.AppendParams(key=16, value=16, key_cache=16, value_cache=16, slot_mapping=16, num_tokens=2,
+                          num_kv_heads=8, head_dim=128, block_size=16, num_blocks=1000, src_dtype=1, cache_dtype=1)
+    assert lib.vkv_paged_decode_append(None, ctypes.byref(dp), None) == -1
+    assert lib.vkv_paged_decode_append(ctypes.byref(ap), None, None) == -1
+    ap.num_kv_heads = 0
+    assert lib.vkv_paged_decode_append(ctypes.byref(ap), ctypes.byref(dp), None) == -2
+    ap.num_kv_heads = 8
+    dp.num_heads = 30
+    assert lib.vkv_paged_decode_append(ctypes.byref(ap), ctypes.byref(dp), None) == -2
+    # nothing to append and nothing to decode: nothing launched
+    ap.num_tokens = 0
+    dp.num_seqs = 0
+    assert lib.vkv_paged_decode_append(ctypes.byref(ap), ctypes.byref(dp), None) == 0
+
+
 def test_append_argument_errors(vkv):
     lib = vkv.load()
     base = dict(key=16, value=16, key_cache=16, value_cache=16, slot_mapping=16, num_tokens=4, num_kv_heads=8,

@@ -2,8 +2,8 @@
 // launch-bound configurations (bench.py --suite c1) without the Python
 // wrapper's per-call cost.  Measurement code only; links the library.
 //
-//   vkvb_step_loop      n eager steps: vkv_reshape_and_cache then
-//                       vkv_paged_decode, on `stream`.
+//   vkvb_step_loop      n eager steps on `stream`: vkv_reshape_and_cache then
+//                       vkv_paged_decode, or (fused != 0) vkv_paged_decode_append.
 //   vkvb_graph_create   one step captured into a HIP graph (on a side stream
 //                       whose library workspace an eager step sizes first).
 //   vkvb_graph_launch   n launches of that graph on `stream`.
@@ -22,7 +22,8 @@ struct StepGraph {
     hipGraphExec_t exec = nullptr;
 };
 
-int step(const vkv_append_params* ap, const vkv_decode_params* dp, hipStream_t st) {
+int step(const vkv_append_params* ap, const vkv_decode_params* dp, int fused, hipStream_t st) {
+    if (fused) return vkv_paged_decode_append(ap, dp, st);
     int rc = vkv_reshape_and_cache(ap, st);
     return rc ? rc : vkv_paged_decode(dp, st);
 }
@@ -31,24 +32,24 @@ int step(const vkv_append_params* ap, const vkv_decode_params* dp, hipStream_t s
 
 extern "C" {
 
-int vkvb_step_loop(const vkv_append_params* ap, const vkv_decode_params* dp, int n, hipStream_t stream) {
+int vkvb_step_loop(const vkv_append_params* ap, const vkv_decode_params* dp, int n, int fused, hipStream_t stream) {
     for (int i = 0; i < n; ++i) {
-        const int rc = step(ap, dp, stream);
+        const int rc = step(ap, dp, fused, stream);
         if (rc) return rc;
     }
     return 0;
 }
 
-int vkvb_graph_create(const vkv_append_params* ap, const vkv_decode_params* dp, void** handle) {
+int vkvb_graph_create(const vkv_append_params* ap, const vkv_decode_params* dp, int fused, void** handle) {
     if (!handle) return int(hipErrorInvalidValue);
     *handle = nullptr;
     StepGraph* g = new StepGraph;
     int rc = int(hipStreamCreateWithFlags(&g->capture, hipStreamNonBlocking));
-    if (!rc) rc = step(ap, dp, g->capture);  // sizes the capture stream's workspace
+    if (!rc) rc = step(ap, dp, fused, g->capture);  // sizes the capture stream's workspace
     if (!rc) rc = int(hipStreamSynchronize(g->capture));
     if (!rc) rc = int(hipStreamBeginCapture(g->capture, hipStreamCaptureModeThreadLocal));
     if (!rc) {
-        const int step_rc = step(ap, dp, g->capture);
+        const int step_rc = step(ap, dp, fused, g->capture);
         rc = int(hipStreamEndCapture(g->capture, &g->graph));
         if (!rc) rc = step_rc;
     }

@@ -428,6 +428,24 @@ int vkv_paged_decode(const vkv_decode_params* p, vkv_stream_t stream) {
     return after_launch(vkv::launch_decode(p, plan, ws, st), "vkv_paged_decode");
 }
 
+int vkv_paged_decode_append(const vkv_append_params* ap, const vkv_decode_params* dp, vkv_stream_t stream) {
+    int rc = check_append(ap);
+    if (rc != VKV_OK) return rc;
+    rc = check_decode(dp);
+    if (rc != VKV_OK) return rc;
+    if (ap->num_tokens == 0 || dp->num_seqs == 0 || !vkv::decode_append_fusable(ap, dp)) {
+        rc = vkv_reshape_and_cache(ap, stream);
+        return rc != VKV_OK ? rc : vkv_paged_decode(dp, stream);
+    }
+    const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const vkv::DecodePlan plan = vkv::plan_decode(dp);
+    void* ws = dp->workspace;
+    rc = ws ? check_workspace(ws, dp->workspace_bytes, plan.workspace_bytes)
+            : library_workspace(plan.workspace_bytes, st, &ws);
+    if (rc != VKV_OK) return rc;
+    return after_launch(vkv::launch_decode_append(ap, dp, plan, ws, st), "vkv_paged_decode_append");
+}
+
 size_t vkv_paged_prefill_workspace_size(const vkv_prefill_params* p) {
     if (check_prefill(p) != VKV_OK || p->num_seqs == 0 || p->num_query_tokens == 0) return 0;
     return vkv::plan_prefill(p).workspace_bytes;

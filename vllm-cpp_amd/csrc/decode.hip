@@ -396,6 +396,30 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, const int P, co
     {
         ChunkRegs b;
         load_chunk(b, (nc - 1) * CH, std::false_type{});
+        if constexpr (KVT == kF16) {
+            // Fused append: the row's last position reads the new token's
+            // rows when the append targets that position's slot.
+            if (a.fkey && t0 + n == ctx) {
+                const int c = (nc - 1) * CH, pn = n - 1;
+                const int pblk = __builtin_amdgcn_readlane(my_block, (pn >> a.bs_log2) & 63);
+                const int64_t pslot = (int64_t(pblk) << a.bs_log2) + (pn & bs_mask);
+                if (int64_t(a.fslots[s]) == pslot) {
+                    uint32_t kw[LW], vw[LW];
+                    load_lane<KVT>(reinterpret_cast<const char*>(a.fkey + s * a.fkey_stride + kvh * D + sub * EPL), kw);
+                    load_lane<KVT>(reinterpret_cast<const char*>(a.fval + s * a.fval_stride + kvh * D + sub * EPL), vw);
+#pragma unroll
+                    for (int u = 0; u < U; ++u) {
+                        if (c + u * TPL + grp == pn) {
+#pragma unroll
+                            for (int w = 0; w < LW; ++w) {
+                                b.k[u][w] = kw[w];
+                                b.v[u][w] = vw[w];
+                            }
+                        }
+                    }
+                }
+            }
+        }
         if ((n % CH) != 0) compute_chunk(b, std::true_type{}, (nc - 1) * CH);
         else compute_chunk(b, std::false_type{});
     }
@@ -664,6 +688,31 @@ __device__ __forceinline__ void decode_item_mfma(const DecodeArgs& a, const int 
     // time so that the 8 G accumulators per lane fit without spilling.
     const int nc = (n + CH - 1) / CH;
     const bool ragged = (n % CH) != 0;
+    // Fused append (fp16): the row's last position reads the new token's rows
+    // when the append targets that position's slot.  Applied to the last
+    // chunk right after its loads are issued.
+    auto fuse_last = [&](Chunk& ch, const int c) __attribute__((always_inline)) {
+        if constexpr (!FP8) {
+            if (a.fkey && t0 + n == ctx) {
+                const int pn = n - 1;
+                const int pblk = __builtin_amdgcn_readlane(my_block, (pn >> a.bs_log2) & 63);
+                const int64_t pslot = (int64_t(pblk) << a.bs_log2) + (pn & bs_mask);
+                if (int64_t(a.fslots[s]) == pslot) {
+                    const char* kr = reinterpret_cast<const char*>(a.fkey + s * a.fkey_stride + kvh * D);
+                    const char* vr = reinterpret_cast<const char*>(a.fval + s * a.fval_stride + kvh * D);
+                    // K: lane (col, quad) holds token c + col, dims 32 i + 8 quad
+                    if (c + col == pn) {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) ch.k[i] = load16(kr + (32 * i + 8 * quad) * 2);
+                    }
+                    // V: load u holds token c + 4 u + quad, dims 8 col..+7
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+                        if (c + 4 * u + quad == pn) ch.v[u] = load16(vr + 8 * col * 2);
+                }
+            }
+        }
+    };
     int ci = 0;
     if constexpr (FP8 && G > kOneChunkAboveGFp8) {
         for (; ci + 1 < nc; ++ci) {
@@ -687,12 +736,14 @@ __device__ __forceinline__ void decode_item_mfma(const DecodeArgs& a, const int 
         Chunk x, y;
         load_chunk(x, ci * CH);
         load_chunk(y, (ci + 1) * CH);
+        fuse_last(y, (ci + 1) * CH);
         compute_chunk(x, ci * CH, std::false_type{});
         if (ragged) compute_chunk(y, (ci + 1) * CH, std::true_type{});
         else compute_chunk(y, (ci + 1) * CH, std::false_type{});
     } else {
         Chunk x;
         load_chunk(x, ci * CH);
+        fuse_last(x, ci * CH);
         if (ragged) compute_chunk(x, ci * CH, std::true_type{});
         else compute_chunk(x, ci * CH, std::false_type{});
     }
@@ -746,6 +797,34 @@ void decode_partition_kernel(const DecodeArgs a) {
     });
 }
 
+// Fused append: the merge kernel (after every read of the call) stores
+// elements [d, d + E) of row s's new K and V rows for kv head kvh, unless the
+// slot lies outside the pool (the plain append skips those slots too).
+template <int E>
+__device__ __forceinline__ void store_new_token(const DecodeArgs& a, const int s, const int kvh, const int d,
+                                                const int D) {
+    const int64_t slot = a.fslots[s];
+    if (slot < 0 || slot >= a.fnum_slots) return;
+    const int64_t dst = (slot * a.num_kv_heads + kvh) * D + d;
+    const _Float16* kr = a.fkey + s * a.fkey_stride + int64_t(kvh) * D + d;
+    const _Float16* vr = a.fval + s * a.fval_stride + int64_t(kvh) * D + d;
+    _Float16* kc = reinterpret_cast<_Float16*>(const_cast<char*>(a.kc)) + dst;
+    _Float16* vc = reinterpret_cast<_Float16*>(const_cast<char*>(a.vc)) + dst;
+    if constexpr (E % 2 == 0) {
+#pragma unroll
+        for (int e = 0; e < E; e += 2) {
+            *reinterpret_cast<uint32_t*>(kc + e) = *reinterpret_cast<const uint32_t*>(kr + e);
+            *reinterpret_cast<uint32_t*>(vc + e) = *reinterpret_cast<const uint32_t*>(vr + e);
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            kc[e] = kr[e];
+            vc[e] = vr[e];
+        }
+    }
+}
+
 // Merge the partitions of one (sequence, head): one thread per output element.
 // The kernel is latency-bound (a few KiB per workgroup), so the partials of
 // the first kMergeBatch partitions are loaded together with the context length,
@@ -770,6 +849,7 @@ __global__ __launch_bounds__(DT ? DT : 1024) void decode_reduce_kernel(DecodeArg
     if (DT == 0 && d >= D) return;
     const int G = a.num_heads / a.num_kv_heads;
     const int kvh = h / G;
+    if (a.fkey && h == kvh * G) store_new_token<1>(a, s, kvh, d, D);
     const int64_t slot0 = (int64_t(s) * a.num_kv_heads + kvh) * a.max_parts * G + (h - kvh * G);
     const float* ml = a.part_ml + slot0 * 2;
     const float* o = a.part_o + slot0 * D + d;
@@ -933,6 +1013,7 @@ __global__ __launch_bounds__(kWave) void decode_reduce_wave_kernel(DecodeArgs a)
     if (s == 0 && h == 0 && threadIdx.x < kClaimSequences) a.counters[threadIdx.x * kCounterStride] = 0;
     const int G = a.num_heads / a.num_kv_heads;
     const int kvh = h / G;
+    if (a.fkey && h == kvh * G) store_new_token<E>(a, s, kvh, d, DT);
     const int64_t slot0 = (int64_t(s) * a.num_kv_heads + kvh) * a.max_parts * G + (h - kvh * G);
     const float* ml = a.part_ml + slot0 * 2;
     const float* o = a.part_o + slot0 * DT + d;
@@ -1109,7 +1190,7 @@ __global__ __launch_bounds__(kBlockThreads) void prefill_rows_kernel(const int32
 }
 
 int launch_rows(const vkv_decode_params* p, const DecodePlan& plan, void* workspace, const int32_t* row_seq,
-                const int32_t* row_ctx, const int32_t* qsl, hipStream_t st) {
+                const int32_t* row_ctx, const int32_t* qsl, hipStream_t st, const FusedAppend* fa = nullptr) {
     DecodeArgs a;
     a.out = p->output;
     a.q = p->query;
@@ -1146,6 +1227,12 @@ int launch_rows(const vkv_decode_params* p, const DecodePlan& plan, void* worksp
     a.scale_log2 = logit_scale_log2(p->scale);
     a.accumulate = p->accumulate;
     a.static_parts = 0;
+    a.fkey = fa ? fa->key : nullptr;
+    a.fval = fa ? fa->value : nullptr;
+    a.fkey_stride = fa ? fa->key_stride : 0;
+    a.fval_stride = fa ? fa->value_stride : 0;
+    a.fslots = fa ? fa->slots : nullptr;
+    a.fnum_slots = fa ? fa->num_slots : 0;
 
     const int G = p->num_heads / p->num_kv_heads;
     const int D = p->head_dim;
@@ -1188,6 +1275,11 @@ int launch_rows(const vkv_decode_params* p, const DecodePlan& plan, void* worksp
                 c.cl = a.cl + r0;
                 c.bt = a.bt + int64_t(r0) * p->max_blocks_per_seq;
             }
+            if (fa) {
+                c.fkey = a.fkey + int64_t(r0) * a.fkey_stride;
+                c.fval = a.fval + int64_t(r0) * a.fval_stride;
+                c.fslots = a.fslots + r0;
+            }
         }
         // Persistent grid (sized in launch_g from the kernel's occupancy), never
         // more workgroups than item groups.
@@ -1224,6 +1316,33 @@ int launch_rows(const vkv_decode_params* p, const DecodePlan& plan, void* worksp
 
 int launch_decode(const vkv_decode_params* p, const DecodePlan& plan, void* workspace, hipStream_t st) {
     return launch_rows(p, plan, workspace, nullptr, nullptr, nullptr, st);
+}
+
+bool decode_append_fusable(const vkv_append_params* ap, const vkv_decode_params* p) {
+    const int64_t row = int64_t(ap->num_kv_heads) * ap->head_dim;
+    const int64_t ks = ap->key_stride ? ap->key_stride : row;
+    const int64_t vs = ap->value_stride ? ap->value_stride : row;
+    const uintptr_t src = reinterpret_cast<uintptr_t>(ap->key) | reinterpret_cast<uintptr_t>(ap->value);
+    return ap->num_tokens == p->num_seqs && p->num_seqs > 0 && ap->key_cache == p->key_cache &&
+           ap->value_cache == p->value_cache && ap->src_dtype == VKV_DTYPE_F16 && ap->cache_dtype == VKV_DTYPE_F16 &&
+           p->kv_dtype == VKV_DTYPE_F16 && ap->num_kv_heads == p->num_kv_heads && ap->head_dim == p->head_dim &&
+           ap->block_size == p->block_size && ap->num_blocks == p->num_blocks && (src & 15u) == 0 &&
+           ks % 8 == 0 && vs % 8 == 0 &&
+           fixed_decode_shape(p->head_dim, p->num_heads / p->num_kv_heads, p->block_size, p->key_cache,
+                              p->value_cache);
+}
+
+int launch_decode_append(const vkv_append_params* ap, const vkv_decode_params* p, const DecodePlan& plan,
+                         void* workspace, hipStream_t st) {
+    const int64_t row = int64_t(ap->num_kv_heads) * ap->head_dim;
+    FusedAppend fa;
+    fa.key = static_cast<const _Float16*>(ap->key);
+    fa.value = static_cast<const _Float16*>(ap->value);
+    fa.key_stride = ap->key_stride ? ap->key_stride : row;
+    fa.value_stride = ap->value_stride ? ap->value_stride : row;
+    fa.slots = ap->slot_mapping;
+    fa.num_slots = int64_t(ap->num_blocks) * ap->block_size;
+    return launch_rows(p, plan, workspace, nullptr, nullptr, nullptr, st, &fa);
 }
 
 // Decode parameters for the rows of a prefill call: one row per query token

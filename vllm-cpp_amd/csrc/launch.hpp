@@ -36,6 +36,13 @@ struct DecodePlan {
 };
 DecodePlan plan_decode(const vkv_decode_params* p);
 int launch_decode(const vkv_decode_params* p, const DecodePlan& plan, void* workspace, hipStream_t st);
+// An append of one new token per sequence fused into the decode (fp16 source
+// and cache, fixed shapes, the same pool and geometry on both sides): the
+// partition kernel reads each row's last position from the new rows when the
+// append targets that position's slot, and the merge kernel stores the rows.
+bool decode_append_fusable(const vkv_append_params* ap, const vkv_decode_params* p);
+int launch_decode_append(const vkv_append_params* ap, const vkv_decode_params* p, const DecodePlan& plan,
+                         void* workspace, hipStream_t st);
 
 // Causal chunked prefill.  fp16 queries with fp16 or FP8 keys at head_dim 64
 // or 128: sequences with >= 2 query tokens on the matrix-core kernel

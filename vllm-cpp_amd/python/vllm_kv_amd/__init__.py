@@ -33,7 +33,7 @@ ERRORS = {
 # Every symbol the C header declares; tests check the library exports them all.
 EXPORTED = [
     "vkv_last_error", "vkv_abi_version", "vkv_reshape_and_cache", "vkv_slot_mapping_host",
-    "vkv_paged_decode_workspace_size", "vkv_paged_decode", "vkv_paged_decode_noalloc",
+    "vkv_paged_decode_workspace_size", "vkv_paged_decode", "vkv_paged_decode_noalloc", "vkv_paged_decode_append",
     "vkv_paged_prefill_workspace_size",
     "vkv_paged_prefill",
     "vkv_copy_blocks", "vkv_check_block_pairs_host", "vkv_swap_host_block_bytes",
@@ -177,6 +177,8 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
                                     ctypes.c_int32, ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p,
                                     ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]
     lib.vkv_swap_blocks.restype = ctypes.c_int
+    lib.vkv_paged_decode_append.argtypes = [ctypes.POINTER(AppendParams), ctypes.POINTER(DecodeParams), ctypes.c_void_p]
+    lib.vkv_paged_decode_append.restype = ctypes.c_int
     lib.vkv_release_workspace.argtypes = [ctypes.c_void_p]
     lib.vkv_release_workspace.restype = ctypes.c_int
     lib.vkv_prefill_work_list_host.argtypes = [ctypes.POINTER(PrefillParams), ctypes.c_void_p, ctypes.c_void_p,
@@ -338,6 +340,21 @@ def paged_decode(out, query, key_cache, value_cache, block_tables, context_lens,
     p = decode_params(out, query, key_cache, value_cache, block_tables, context_lens, scale,
                       key_scales, value_scales, max_context_len, accumulate, partition_size, workspace)
     check(load().vkv_paged_decode(ctypes.byref(p), _stream(stream)))
+
+
+def paged_decode_append(out, query, key_cache, value_cache, block_tables, context_lens, scale,
+                        key, value, slot_mapping, key_scales=None, value_scales=None,
+                        max_context_len=None, accumulate=False, partition_size=0, workspace=None,
+                        stream=None) -> None:
+    """vkv_paged_decode_append: reshape_and_cache(key, value, ..., slot_mapping) then
+    paged_decode(...), the append fused into the decode when the shapes allow (key/value
+    [num_seqs, Hkv, D], token s being sequence s's new token)."""
+    _require_cuda(out, query, key_cache, value_cache, block_tables, context_lens, key, value, slot_mapping,
+                  key_scales, value_scales, workspace)
+    ap = append_params(key, value, key_cache, value_cache, slot_mapping, key_scales, value_scales)
+    dp = decode_params(out, query, key_cache, value_cache, block_tables, context_lens, scale,
+                       key_scales, value_scales, max_context_len, accumulate, partition_size, workspace)
+    check(load().vkv_paged_decode_append(ctypes.byref(ap), ctypes.byref(dp), _stream(stream)))
 
 
 def paged_decode_noalloc(out, query, key_cache, value_cache, block_tables, context_lens, scale,
