@@ -252,9 +252,10 @@ int vkv_paged_decode(const vkv_decode_params* p, vkv_stream_t stream);
  * those of vkv_reshape_and_cache(ap) followed by vkv_paged_decode(dp) on the
  * same stream (workspace as for vkv_paged_decode).  When the two fit together
  * — token s of ap is sequence s's new token (ap->num_tokens == dp->num_seqs),
- * both name the same fp16 caches with the same geometry and pool, fp16
- * source rows 16-byte aligned with token strides a multiple of 8 elements, and
- * a shape the tuned decode kernels run — the append is fused into the decode
+ * both name the same fp16 or fp32 caches with the same geometry and pool,
+ * source rows of the cache's type, 16-byte aligned with token strides a
+ * multiple of 16 bytes, and a shape the tuned decode kernels run — the append
+ * is fused into the decode
  * launches (one launch fewer per step): each sequence's last position is read
  * from its new rows when ap's slot for the token is that position's slot, and
  * the merge kernel stores the rows.  The fused form assumes what a decode step

@@ -76,6 +76,17 @@ def test_decode_append_matches_two_calls(vkv, cuda, H, Hkv, D, bs, prev):
     _assert_same(vkv, cuda, _case(rng, H, Hkv, D, bs, prev))
 
 
+@pytest.mark.parametrize("H,Hkv,D,bs,prev", [(32, 8, 128, 16, [4, 299, 1000]), (14, 2, 64, 16, [0, 15, 16, 300]),
+                                               (16, 8, 256, 8, [8, 64, 519])])
+def test_decode_append_f32_cache(vkv, cuda, H, Hkv, D, bs, prev):
+    """The reference's own dtype: fp32 query, rows, cache and output (VALU items)."""
+    rng = np.random.default_rng(H + D)
+    lay, k, v, q, nk, nv, slots = _case(rng, H, Hkv, D, bs, prev)
+    case = (lay, k.astype(np.float32), v.astype(np.float32), q.astype(np.float32), nk.astype(np.float32),
+            nv.astype(np.float32), slots)
+    _assert_same(vkv, cuda, case, io=np.float32)
+
+
 def test_decode_append_f32_io_and_accumulate(vkv, cuda):
     """fp32 query / output over the fp16 cache (VALU items), and accumulate = 1."""
     rng = np.random.default_rng(7)

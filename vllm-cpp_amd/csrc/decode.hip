@@ -396,7 +396,7 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, const int P, co
     {
         ChunkRegs b;
         load_chunk(b, (nc - 1) * CH, std::false_type{});
-        if constexpr (KVT == kF16) {
+        if constexpr (KVT == kF16 || KVT == kF32) {
             // Fused append: the row's last position reads the new token's
             // rows when the append targets that position's slot.
             if (a.fkey && t0 + n == ctx) {
@@ -405,8 +405,8 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, const int P, co
                 const int64_t pslot = (int64_t(pblk) << a.bs_log2) + (pn & bs_mask);
                 if (int64_t(a.fslots[s]) == pslot) {
                     uint32_t kw[LW], vw[LW];
-                    load_lane<KVT>(reinterpret_cast<const char*>(a.fkey + s * a.fkey_stride + kvh * D + sub * EPL), kw);
-                    load_lane<KVT>(reinterpret_cast<const char*>(a.fval + s * a.fval_stride + kvh * D + sub * EPL), vw);
+                    load_lane<KVT>(a.fkey + s * a.fkey_stride + (kvh * D + sub * EPL) * EB, kw);
+                    load_lane<KVT>(a.fval + s * a.fval_stride + (kvh * D + sub * EPL) * EB, vw);
 #pragma unroll
                     for (int u = 0; u < U; ++u) {
                         if (c + u * TPL + grp == pn) {
@@ -698,8 +698,8 @@ __device__ __forceinline__ void decode_item_mfma(const DecodeArgs& a, const int 
                 const int pblk = __builtin_amdgcn_readlane(my_block, (pn >> a.bs_log2) & 63);
                 const int64_t pslot = (int64_t(pblk) << a.bs_log2) + (pn & bs_mask);
                 if (int64_t(a.fslots[s]) == pslot) {
-                    const char* kr = reinterpret_cast<const char*>(a.fkey + s * a.fkey_stride + kvh * D);
-                    const char* vr = reinterpret_cast<const char*>(a.fval + s * a.fval_stride + kvh * D);
+                    const char* kr = a.fkey + s * a.fkey_stride + kvh * D * 2;
+                    const char* vr = a.fval + s * a.fval_stride + kvh * D * 2;
                     // K: lane (col, quad) holds token c + col, dims 32 i + 8 quad
                     if (c + col == pn) {
 #pragma unroll
@@ -798,30 +798,34 @@ void decode_partition_kernel(const DecodeArgs a) {
 }
 
 // Fused append: the merge kernel (after every read of the call) stores
-// elements [d, d + E) of row s's new K and V rows for kv head kvh, unless the
-// slot lies outside the pool (the plain append skips those slots too).
+// elements [d, d + E) of row s's new K and V rows for kv head kvh (elements of
+// a.fbytes bytes), unless the slot lies outside the pool (the plain append
+// skips those slots too).
 template <int E>
 __device__ __forceinline__ void store_new_token(const DecodeArgs& a, const int s, const int kvh, const int d,
                                                 const int D) {
     const int64_t slot = a.fslots[s];
     if (slot < 0 || slot >= a.fnum_slots) return;
-    const int64_t dst = (slot * a.num_kv_heads + kvh) * D + d;
-    const _Float16* kr = a.fkey + s * a.fkey_stride + int64_t(kvh) * D + d;
-    const _Float16* vr = a.fval + s * a.fval_stride + int64_t(kvh) * D + d;
-    _Float16* kc = reinterpret_cast<_Float16*>(const_cast<char*>(a.kc)) + dst;
-    _Float16* vc = reinterpret_cast<_Float16*>(const_cast<char*>(a.vc)) + dst;
-    if constexpr (E % 2 == 0) {
+    const int64_t eb = a.fbytes;
+    const int64_t dst = ((slot * a.num_kv_heads + kvh) * D + d) * eb;
+    const char* kr = a.fkey + s * a.fkey_stride + (int64_t(kvh) * D + d) * eb;
+    const char* vr = a.fval + s * a.fval_stride + (int64_t(kvh) * D + d) * eb;
+    char* kc = const_cast<char*>(a.kc) + dst;
+    char* vc = const_cast<char*>(a.vc) + dst;
+    if (E * eb % 4 == 0) {
+        // E fp16 (E even) or E fp32 elements as 32-bit words
+        const int words = int(E * eb / 4);
 #pragma unroll
-        for (int e = 0; e < E; e += 2) {
-            *reinterpret_cast<uint32_t*>(kc + e) = *reinterpret_cast<const uint32_t*>(kr + e);
-            *reinterpret_cast<uint32_t*>(vc + e) = *reinterpret_cast<const uint32_t*>(vr + e);
+        for (int w = 0; w < 2 * E; ++w) {
+            if (w < words) {
+                reinterpret_cast<uint32_t*>(kc)[w] = reinterpret_cast<const uint32_t*>(kr)[w];
+                reinterpret_cast<uint32_t*>(vc)[w] = reinterpret_cast<const uint32_t*>(vr)[w];
+            }
         }
     } else {
-#pragma unroll
-        for (int e = 0; e < E; ++e) {
-            kc[e] = kr[e];
-            vc[e] = vr[e];
-        }
+        // one fp16 element
+        *reinterpret_cast<uint16_t*>(kc) = *reinterpret_cast<const uint16_t*>(kr);
+        *reinterpret_cast<uint16_t*>(vc) = *reinterpret_cast<const uint16_t*>(vr);
     }
 }
 
@@ -1231,6 +1235,7 @@ int launch_rows(const vkv_decode_params* p, const DecodePlan& plan, void* worksp
     a.fval = fa ? fa->value : nullptr;
     a.fkey_stride = fa ? fa->key_stride : 0;
     a.fval_stride = fa ? fa->value_stride : 0;
+    a.fbytes = fa ? fa->elem_bytes : 0;
     a.fslots = fa ? fa->slots : nullptr;
     a.fnum_slots = fa ? fa->num_slots : 0;
 
@@ -1319,27 +1324,32 @@ int launch_decode(const vkv_decode_params* p, const DecodePlan& plan, void* work
 }
 
 bool decode_append_fusable(const vkv_append_params* ap, const vkv_decode_params* p) {
+    const bool f16 = ap->src_dtype == VKV_DTYPE_F16 && ap->cache_dtype == VKV_DTYPE_F16;
+    const bool f32 = ap->src_dtype == VKV_DTYPE_F32 && ap->cache_dtype == VKV_DTYPE_F32;
+    const int64_t eb = f32 ? 4 : 2;
     const int64_t row = int64_t(ap->num_kv_heads) * ap->head_dim;
-    const int64_t ks = ap->key_stride ? ap->key_stride : row;
-    const int64_t vs = ap->value_stride ? ap->value_stride : row;
+    const int64_t ks = (ap->key_stride ? ap->key_stride : row) * eb;
+    const int64_t vs = (ap->value_stride ? ap->value_stride : row) * eb;
     const uintptr_t src = reinterpret_cast<uintptr_t>(ap->key) | reinterpret_cast<uintptr_t>(ap->value);
     return ap->num_tokens == p->num_seqs && p->num_seqs > 0 && ap->key_cache == p->key_cache &&
-           ap->value_cache == p->value_cache && ap->src_dtype == VKV_DTYPE_F16 && ap->cache_dtype == VKV_DTYPE_F16 &&
-           p->kv_dtype == VKV_DTYPE_F16 && ap->num_kv_heads == p->num_kv_heads && ap->head_dim == p->head_dim &&
+           ap->value_cache == p->value_cache && (f16 || f32) && p->kv_dtype == ap->cache_dtype &&
+           ap->num_kv_heads == p->num_kv_heads && ap->head_dim == p->head_dim &&
            ap->block_size == p->block_size && ap->num_blocks == p->num_blocks && (src & 15u) == 0 &&
-           ks % 8 == 0 && vs % 8 == 0 &&
+           ks % 16 == 0 && vs % 16 == 0 &&
            fixed_decode_shape(p->head_dim, p->num_heads / p->num_kv_heads, p->block_size, p->key_cache,
                               p->value_cache);
 }
 
 int launch_decode_append(const vkv_append_params* ap, const vkv_decode_params* p, const DecodePlan& plan,
                          void* workspace, hipStream_t st) {
+    const int eb = ap->cache_dtype == VKV_DTYPE_F32 ? 4 : 2;
     const int64_t row = int64_t(ap->num_kv_heads) * ap->head_dim;
     FusedAppend fa;
-    fa.key = static_cast<const _Float16*>(ap->key);
-    fa.value = static_cast<const _Float16*>(ap->value);
-    fa.key_stride = ap->key_stride ? ap->key_stride : row;
-    fa.value_stride = ap->value_stride ? ap->value_stride : row;
+    fa.key = static_cast<const char*>(ap->key);
+    fa.value = static_cast<const char*>(ap->value);
+    fa.key_stride = (ap->key_stride ? ap->key_stride : row) * eb;
+    fa.value_stride = (ap->value_stride ? ap->value_stride : row) * eb;
+    fa.elem_bytes = eb;
     fa.slots = ap->slot_mapping;
     fa.num_slots = int64_t(ap->num_blocks) * ap->block_size;
     return launch_rows(p, plan, workspace, nullptr, nullptr, nullptr, st, &fa);

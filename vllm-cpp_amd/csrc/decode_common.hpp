@@ -83,26 +83,28 @@ struct DecodeArgs {
     // prefix scan, no claims, and items request their block ids together with
     // the context length.  0: the persistent claim loop.
     int32_t static_parts;
-    // Append fused into the call (fp16 source and cache, fixed shapes): row
-    // s's new token is fkey / fval + s * stride (elements), bound for cache
-    // slot fslots[s].  The partition kernel reads row s's last position from
-    // these rows when that position's slot is fslots[s] (its K/V as the
-    // append would leave them); the merge kernel stores the rows into slots
-    // in [0, fnum_slots).  fkey == NULL: no append.
-    const _Float16* fkey;
-    const _Float16* fval;
+    // Append fused into the call (source rows in the cache's element type,
+    // fp16 or fp32; fixed shapes): row s's new token is fkey / fval + s *
+    // stride (bytes), bound for cache slot fslots[s].  The partition kernel
+    // reads row s's last position from these rows when that position's slot
+    // is fslots[s] (its K/V as the append would leave them); the merge kernel
+    // stores the rows into slots in [0, fnum_slots).  fkey == NULL: no append.
+    const char* fkey;
+    const char* fval;
     int64_t fkey_stride;
     int64_t fval_stride;
+    int32_t fbytes;  // element bytes of the rows and the cache (2 or 4)
     const int32_t* fslots;
     int64_t fnum_slots;
 };
 
 // The new token of an appending decode call (see DecodeArgs::fkey).
 struct FusedAppend {
-    const _Float16* key;
-    const _Float16* value;
-    int64_t key_stride;  // elements
+    const char* key;
+    const char* value;
+    int64_t key_stride;  // bytes
     int64_t value_stride;
+    int32_t elem_bytes;
     const int32_t* slots;
     int64_t num_slots;
 };
