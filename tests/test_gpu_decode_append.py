@@ -163,3 +163,37 @@ def test_decode_append_rows_beyond_one_launch(vkv, cuda):
     rng = np.random.default_rng(19)
     prev = rng.integers(0, 40, 8300).astype(np.int32)
     _assert_same(vkv, cuda, _case(rng, 4, 2, 64, 16, prev))
+
+
+@pytest.mark.parametrize("prev", [[3, 60, 300], [100, 50] + list(range(300, 1060, 20))])  # static grid, claim loop
+def test_decode_append_graph_replays(vkv, cuda, prev):
+    """The fused call captured in a HIP graph replays to the eager result (the
+    append stores the same rows each time), with eager calls on the capture
+    stream's library workspace and synchronisations between the replays."""
+    import torch
+    rng = np.random.default_rng(23)
+    lay, k, v, q, nk, nv, slots = _case(rng, 32, 8, 128, 16, prev)
+    kc, vc = to_dev(k, cuda), to_dev(v, cuda)
+    args = (to_dev(q, cuda), kc, vc, to_dev(lay.block_tables, cuda), to_dev(lay.context_lens, cuda),
+            1.0 / np.sqrt(128), to_dev(nk, cuda), to_dev(nv, cuda), to_dev(slots, cuda))
+    out = torch.zeros(q.shape, dtype=torch.float16, device=cuda)
+    vkv.paged_decode_append(out, *args)
+    torch.cuda.synchronize()
+    ref, kref, vref = out.clone(), kc.clone(), vc.clone()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        vkv.paged_decode_append(torch.empty_like(out), *args, stream=s)  # sizes the capture stream's workspace
+        with torch.cuda.graph(g, stream=s):
+            vkv.paged_decode_append(out, *args, stream=s)
+    torch.cuda.synchronize()
+    for i in range(3):
+        out.fill_(float("nan"))
+        with torch.cuda.stream(s):
+            vkv.paged_decode_append(torch.empty_like(out), *args, stream=s)  # eager work between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(ref.view(torch.int16), out.view(torch.int16)), i
+        assert torch.equal(kref, kc) and torch.equal(vref, vc), i
