@@ -1245,6 +1245,7 @@ int launch_rows(const vkv_decode_params* p, const DecodePlan& plan, void* worksp
     const bool fixed = fixed_decode_shape(D, G, p->block_size, p->key_cache, p->value_cache);
     a.head_dim = D;
     a.block_size = p->block_size;
+    set_block_div(a, p->block_size);
     a.io_f32 = p->io_dtype == VKV_DTYPE_F32;
     {
         const int kv_eb = p->kv_dtype == VKV_DTYPE_F32 ? 4 : (p->kv_dtype == VKV_DTYPE_F16 ? 2 : 1);

@@ -78,6 +78,11 @@ struct DecodeArgs {
     int32_t block_size;
     int32_t io_f32;           // query and output are fp32 (else fp16)
     int32_t vec_loads;        // whole-vector K/V loads (head_dim and cache alignment allow them)
+    // n / block_size for 0 <= n < 2^31 as (n + mulhi(n, bs_div_m)) >> bs_div_s
+    // (bs_div_s = ceil(log2 block_size), bs_div_m = ceil(2^(32 + s) / block_size)
+    // - 2^32: exact for such n, see block_div)
+    uint32_t bs_div_m;
+    int32_t bs_div_s;
     // > 0: small call, one item per wave of a grid that covers every
     // (row, partition < static_parts, sub-item) at partition size P: no
     // prefix scan, no claims, and items request their block ids together with
@@ -120,6 +125,22 @@ inline bool fixed_decode_shape(int head_dim, int group, int block_size, const vo
 // Partition kernel of the generic variant (decode_generic.hip) for one launch
 // of rows; max_pairs bounds the (row, partition) pairs.  0 or VKV_ERR_*.
 int launch_decode_generic(DecodeArgs& a, int kv_dtype, int64_t max_pairs, size_t lds, hipStream_t st);
+
+// n / block_size by the multiplier of DecodeArgs::bs_div_m: with m = 2^32 +
+// bs_div_m = ceil(2^(32+s) / d), n m / 2^(32+s) = n / d + n e / (d 2^(32+s))
+// for e = m d - 2^(32+s) < d, and that last term is below 1 / d for n < 2^31,
+// so the floor is exact (division by invariant integers, Granlund and
+// Montgomery 1994).
+__device__ __forceinline__ int block_div(const DecodeArgs& a, const int n) {
+    return int((uint32_t(n) + __umulhi(uint32_t(n), a.bs_div_m)) >> a.bs_div_s);
+}
+inline void set_block_div(DecodeArgs& a, int block_size) {
+    int s = 0;
+    while ((int64_t(1) << s) < block_size) ++s;
+    const uint64_t m = ((uint64_t(1) << (32 + s)) + uint64_t(block_size) - 1) / uint64_t(block_size);
+    a.bs_div_m = uint32_t(m - (uint64_t(1) << 32));
+    a.bs_div_s = s;
+}
 
 // Keys row r attends (clamped to the table) and the query/output row it uses.
 __device__ __forceinline__ int row_context(const DecodeArgs& a, int r) {

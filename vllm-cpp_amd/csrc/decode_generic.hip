@@ -142,8 +142,9 @@ __device__ __forceinline__ void decode_item_generic(const DecodeArgs& a, const i
             const int tok = c + u * TPL + grp;
             valid[u] = tok < n;
             const int tk = valid[u] ? tok : 0;
-            const int blk = __shfl(my_block, tk / bs, kWave);
-            const int64_t slot = int64_t(blk) * bs + tk % bs;
+            const int bi = block_div(a, tk);
+            const int blk = __shfl(my_block, bi, kWave);
+            const int64_t slot = int64_t(blk) * bs + (tk - bi * bs);
             const char* kr = a.kc + slot * slot_stride + head_off;
             const char* vr = a.vc + slot * slot_stride + head_off;
 #pragma unroll
