@@ -66,9 +66,13 @@ struct GenericShape {
     static_assert(LPT >= 1 && (kWave % LPT) == 0, "lane mapping");
 };
 
-template <int KVT, int DP, int GC>
+// HQ: fp16 queries over an fp16 cache; the logits are packed fp16 dot
+// products (v_dot2_f32_f16, fp32 accumulation) of the query and key halves
+// instead of fp32 products of unpacked keys.
+template <int KVT, int DP, int GC, bool HQ>
 __device__ __forceinline__ void decode_item_generic(const DecodeArgs& a, const int P, const int s, const int kvh,
                                                     const int g0, const int part, const int lane) {
+    static_assert(!HQ || KVT == kF16, "packed query dots need an fp16 cache");
     using Sh = GenericShape<KVT, DP, GC>;
     constexpr int EB = KvTraits<KVT>::bytes;
     constexpr int EPV = Sh::EPV, LW = Sh::LW, LPT = Sh::LPT, NV = Sh::NV, TPL = Sh::TPL, U = Sh::U, CH = Sh::CH;
@@ -115,6 +119,19 @@ __device__ __forceinline__ void decode_item_generic(const DecodeArgs& a, const i
                 }
                 qf[h][j][e] = neg_scale ? -x : x;
             }
+    // HQ: the same query elements as fp16 pairs (exact: the query is fp16)
+    uint32_t qh[HQ ? GC : 1][HQ ? NV : 1][HQ ? LW : 1];
+    if constexpr (HQ) {
+#pragma unroll
+        for (int h = 0; h < GC; ++h)
+#pragma unroll
+            for (int j = 0; j < NV; ++j)
+#pragma unroll
+                for (int w = 0; w < LW; ++w) {
+                    const half2_t p2 = {static_cast<_Float16>(qf[h][j][2 * w]), static_cast<_Float16>(qf[h][j][2 * w + 1])};
+                    qh[h][j][w] = __builtin_bit_cast(uint32_t, p2);
+                }
+    }
     float sc = neg_scale ? -a.scale_log2 : a.scale_log2;
     if constexpr (KVT == kFp8) sc *= kFp8HalfScale;  // unpack_lane yields codes x 2^-8
 
@@ -173,16 +190,25 @@ __device__ __forceinline__ void decode_item_generic(const DecodeArgs& a, const i
         float r[U][GC];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            float kf[NV][EPV];
+            float kf[HQ ? 1 : NV][HQ ? 1 : EPV];
+            if constexpr (!HQ) {
 #pragma unroll
-            for (int j = 0; j < NV; ++j) unpack_lane<KVT>(kw[u][j], kf[j]);
+                for (int j = 0; j < NV; ++j) unpack_lane<KVT>(kw[u][j], kf[j]);
+            }
 #pragma unroll
             for (int h = 0; h < GC; ++h) {
                 float t = 0.0f;
+                if constexpr (HQ) {
 #pragma unroll
-                for (int j = 0; j < NV; ++j)
+                    for (int j = 0; j < NV; ++j)
 #pragma unroll
-                    for (int e = 0; e < EPV; ++e) t = fmaf(qf[h][j][e], kf[j][e], t);
+                        for (int w = 0; w < LW; ++w) t = dot2(as_half2(qh[h][j][w]), as_half2(kw[u][j][w]), t);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < NV; ++j)
+#pragma unroll
+                        for (int e = 0; e < EPV; ++e) t = fmaf(qf[h][j][e], kf[j][e], t);
+                }
                 float y = group_sum<LPT>(t);
                 if constexpr (KVT == kFp8) y *= ks[u];
                 r[u][h] = valid[u] ? y : -INFINITY;
@@ -207,7 +233,38 @@ __device__ __forceinline__ void decode_item_generic(const DecodeArgs& a, const i
             }
             msc[h] = m[h] * sc;
         }
-        // weights (masked tokens weigh exactly 0) and p * V
+        // weights (masked tokens weigh exactly 0) and p * V.  HQ with an even
+        // number of token loads: packed fp16 dot products over token pairs
+        // (weights rounded to fp16, and the row sum over the same rounded
+        // weights), as the fixed-shape kernels do.
+        constexpr bool PAIR = HQ && (U % 2) == 0;
+        if constexpr (PAIR) {
+            const half2_t ones = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
+#pragma unroll
+            for (int u = 0; u < U; u += 2) {
+                half2_t pp[GC];
+#pragma unroll
+                for (int h = 0; h < GC; ++h) {
+                    const float p0 = valid[u] ? __builtin_amdgcn_exp2f(fmaf(r[u][h], sc, -msc[h])) : 0.0f;
+                    const float p1 = valid[u + 1] ? __builtin_amdgcn_exp2f(fmaf(r[u + 1][h], sc, -msc[h])) : 0.0f;
+                    pp[h] = half2_t{static_cast<_Float16>(p0), static_cast<_Float16>(p1)};
+                    l[h] = dot2(pp[h], ones, l[h]);
+                }
+#pragma unroll
+                for (int j = 0; j < NV; ++j)
+#pragma unroll
+                    for (int w = 0; w < LW; ++w) {
+                        // (element 2w of token u, of token u + 1) and (element 2w + 1 of both)
+                        const uint32_t lo = __builtin_amdgcn_perm(vw[u + 1][j][w], vw[u][j][w], 0x05040100u);
+                        const uint32_t hi = __builtin_amdgcn_perm(vw[u + 1][j][w], vw[u][j][w], 0x07060302u);
+#pragma unroll
+                        for (int h = 0; h < GC; ++h) {
+                            acc[h][j][2 * w] = dot2(pp[h], as_half2(lo), acc[h][j][2 * w]);
+                            acc[h][j][2 * w + 1] = dot2(pp[h], as_half2(hi), acc[h][j][2 * w + 1]);
+                        }
+                    }
+            }
+        } else {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             float vf[NV][EPV];
@@ -224,6 +281,7 @@ __device__ __forceinline__ void decode_item_generic(const DecodeArgs& a, const i
 #pragma unroll
                     for (int e = 0; e < EPV; ++e) acc[h][j][e] = fmaf(w, vf[j][e], acc[h][j][e]);
             }
+        }
         }
     }
 
@@ -257,7 +315,7 @@ __device__ __forceinline__ void decode_item_generic(const DecodeArgs& a, const i
     }
 }
 
-template <int KVT, int DP, int GC>
+template <int KVT, int DP, int GC, bool HQ>
 __global__ __launch_bounds__(256) void decode_generic_kernel(const DecodeArgs a) {
     const int lane = threadIdx.x & (kWave - 1);
     const int G = a.num_heads / a.num_kv_heads;
@@ -265,18 +323,18 @@ __global__ __launch_bounds__(256) void decode_generic_kernel(const DecodeArgs a)
     run_partitions(a, a.num_kv_heads * chunks, [&](const int P, const int row, const int part, const int sub)
                                                    __attribute__((always_inline)) {
         const int kvh = sub / chunks;
-        decode_item_generic<KVT, DP, GC>(a, P, row, kvh, (sub - kvh * chunks) * GC, part, lane);
+        decode_item_generic<KVT, DP, GC, HQ>(a, P, row, kvh, (sub - kvh * chunks) * GC, part, lane);
     });
 }
 
 // One workgroup per resident slot (occupancy queried once per variant), never
 // more than there are item groups.
-template <int KVT, int DP, int GC>
-void launch_variant(DecodeArgs& a, int64_t max_pairs, size_t lds, hipStream_t st) {
+template <int KVT, int DP, int GC, bool HQ>
+void launch_variant_q(DecodeArgs& a, int64_t max_pairs, size_t lds, hipStream_t st) {
     static int per_cu_cached = 0;  // benign race: every thread computes the same value
     int per_cu = per_cu_cached;
     if (per_cu <= 0) {
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_generic_kernel<KVT, DP, GC>,
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_generic_kernel<KVT, DP, GC, HQ>,
                                                          kWave * kWavesPerBlock, 0) != hipSuccess || per_cu <= 0)
             per_cu = 1;
         per_cu_cached = per_cu;
@@ -292,8 +350,20 @@ void launch_variant(DecodeArgs& a, int64_t max_pairs, size_t lds, hipStream_t st
     a.wave_slots = int(gx > 0 ? gx : 1) * kWavesPerBlock;
     const int64_t cus = device_cu_count();
     a.level_waves = int(gx > 0 ? (gx < cus ? gx : cus) : 1) * kWavesPerBlock;
-    hipLaunchKernelGGL((decode_generic_kernel<KVT, DP, GC>), dim3(unsigned(gx > 0 ? gx : 1)),
+    hipLaunchKernelGGL((decode_generic_kernel<KVT, DP, GC, HQ>), dim3(unsigned(gx > 0 ? gx : 1)),
                        dim3(kBlockThreads), lds, st, a);
+}
+
+// fp16 queries over an fp16 cache take the packed-dot variant.
+template <int KVT, int DP, int GC>
+void launch_variant(DecodeArgs& a, int64_t max_pairs, size_t lds, hipStream_t st) {
+    if constexpr (KVT == kF16) {
+        if (!a.io_f32) {
+            launch_variant_q<KVT, DP, GC, true>(a, max_pairs, lds, st);
+            return;
+        }
+    }
+    launch_variant_q<KVT, DP, GC, false>(a, max_pairs, lds, st);
 }
 
 template <int KVT, int DP>
