@@ -16,8 +16,13 @@
 // head_dim is not a whole number of vectors (or the caches are not 16-byte
 // aligned) every element is loaded on its own.  Block ids come from a
 // per-lane table of the partition's blocks (a partition holds at most 64
-// blocks) by integer division, so any block size works.  Dots and the online
-// softmax are fp32, as in decode.hip's VALU variant.
+// blocks) by division (a precomputed multiplier, block_div), so any block size
+// works.  Dots and the online softmax are fp32, as in decode.hip's VALU
+// variant; fp16 queries over an fp16 cache take packed fp16 dot products
+// (fp32 accumulation) for the logits and, over token pairs, for p * V, with
+// the weights rounded to fp16 as the fixed-shape kernels round them.  Chunks
+// of up to 2 query heads load 8 tokens per lane (more bytes in flight, for
+// the byte-bound shapes), larger ones 4 (2 above 4 heads).
 #include "common.hpp"
 #include "decode_common.hpp"
 #include "launch.hpp"
@@ -60,7 +65,7 @@ struct GenericShape {
     static constexpr int LPT = DP / EPV < kWave ? DP / EPV : kWave;  // lanes per token
     static constexpr int NV = DP / (LPT * EPV);               // vectors per lane
     static constexpr int TPL = kWave / LPT;                   // tokens per wave-wide load
-    static constexpr int U0 = (GC <= 4 ? 4 : 2) / NV;
+    static constexpr int U0 = (GC <= 2 ? 8 : GC <= 4 ? 4 : 2) / NV;
     static constexpr int U = U0 > 0 ? U0 : 1;                 // token loads per lane per chunk
     static constexpr int CH = U * TPL;                        // tokens per chunk
     static_assert(LPT >= 1 && (kWave % LPT) == 0, "lane mapping");
