@@ -353,15 +353,19 @@ int vkv_paged_prefill(const vkv_prefill_params* p, vkv_stream_t stream);
 /* Host-built work list of the matrix-core prefill kernels.  No counterpart in
  * the reference, whose prefill is one decode per token (src/core/engine.cpp:
  * 157-164).  From host copies of the call's query_start_loc and context_lens
- * and the shape fields of *p, it lists the call's work items (blocks of query
- * rows of one sequence and kv head) longest first, the order in which the
- * kernels' persistent workgroups claim them.  With the words
+ * and the shape fields of *p, it deals the call's work items (blocks of query
+ * rows of one sequence and kv head, with their sequence's query rows and
+ * context) to one list per workgroup of the kernels' persistent grid (one per
+ * CU of the current device, 256 without one), longest first, each to the list
+ * with the least work so far: a workgroup then runs its list without claiming
+ * items and knows its next item while it computes the current one.  With the words
  * copied to device memory and passed as p->work_list / work_list_words, the
  * kernels skip ordering the items themselves: an engine builds it once per
  * step beside its other metadata, for every layer of the step.  The list must
- * come from the same lengths and shape as the call (items past the call's
- * sequences are skipped, so a stale list gives wrong rows but reads nothing out
- * of bounds).  Returns the number of int32 words; writes them when out is not
+ * come from the same lengths and shape as the call (items outside the call's
+ * sequences, kv heads and query rows are skipped, so a stale list gives wrong
+ * rows but reads nothing out of bounds; a grid smaller than the number of
+ * lists runs the extra lists in turn).  Returns the number of int32 words; writes them when out is not
  * NULL and capacity_words suffices (else returns -2); 0 when the call's shape
  * runs without a list (everything but fp16 queries at head_dim 64/128 over fp16
  * caches or FP8 caches at 128); -1 for a NULL argument. */

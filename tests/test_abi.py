@@ -221,8 +221,10 @@ def test_prefill_argument_errors_and_workspace(vkv):
                                    (32, 2, 128, 16, 1, 1)])
 def test_prefill_work_list_host(vkv, shape):
     """vkv_prefill_work_list_host (no GPU): every work item (sequence, row block,
-    kv head) of the call exactly once, longest first; no list for shapes the
-    matrix-core kernels do not run; capacity and argument errors."""
+    kv head) of the call exactly once, with its sequence's query rows and prior
+    context, dealt to one list per workgroup longest first, each to the least
+    loaded list; no list for shapes the matrix-core kernels do not run;
+    capacity and argument errors."""
     import numpy as np
     H, Hkv, D, bs, io, kv = shape
     rng = np.random.default_rng(H + D)
@@ -238,8 +240,7 @@ def test_prefill_work_list_host(vkv, shape):
     n = lib.vkv_prefill_work_list_host(ctypes.byref(p), qsl.ctypes.data, ctx.ctypes.data, None, 0)
     G = H // Hkv
     rows = 256 if D == 128 else 512
-    want = set()
-    tiles = {}
+    want = {}
     for s in range(q_lens.size):
         if q_lens[s] < 2:
             continue
@@ -248,20 +249,35 @@ def test_prefill_work_list_host(vkv, shape):
             last = min(int(q_lens[s]), ((b + 1) * rows - 1) // G + 1)
             t = (int(prior[s]) + last + 63) // 64
             for k in range(Hkv):
-                want.add((s, b * Hkv + k))
-                tiles[(s, b * Hkv + k)] = t
-    assert n == 32 + 2 * len(want)
+                want[(s, b, k)] = (int(qsl[s]), int(q_lens[s]), int(prior[s]), t)
+    # one list per CU (256 on this device, and without a device), at most one per item
+    lists = min(256, len(want))
+    items_word = 32 + (lists + 1 + 3) // 4 * 4
+    assert n == items_word + 8 * len(want)
     words = np.zeros(n, np.int32)
     assert lib.vkv_prefill_work_list_host(ctypes.byref(p), qsl.ctypes.data, ctx.ctypes.data,
                                           words.ctypes.data, n - 1) == -2
     assert lib.vkv_prefill_work_list_host(ctypes.byref(p), qsl.ctypes.data, ctx.ctypes.data,
                                           words.ctypes.data, n) == n
-    assert words[0] == 1 and words[1] == 0 and words[2] == len(want)
-    items = words[32:].reshape(-1, 2)
-    got = [tuple(map(int, it)) for it in items]
-    assert sorted(got) == sorted(want) and len(got) == len(set(got))
-    t = [tiles[it] for it in got]
-    assert t == sorted(t, reverse=True)  # longest first
+    assert words[0] == lists and words[1] == len(want) and words[2] == 2
+    off = words[32:32 + lists + 1]
+    assert off[0] == 0 and off[-1] == len(want) and np.all(np.diff(off) >= 0)
+    items = words[items_word:].reshape(-1, 8)
+    got = {(int(e[0]), int(e[1]), int(e[2])): (int(e[3]), int(e[4]), int(e[5]), int(e[6])) for e in items}
+    assert got == want and len(items) == len(want)
+    # the deal, replayed: longest first (ties in (s, b, kvh) order), each item
+    # to the least loaded list (ties: the lowest), an item costing its key
+    # tiles + 2
+    order = sorted(range(len(items)), key=lambda i: (-items[i, 6], items[i, 0], items[i, 1], items[i, 2]))
+    lst = np.searchsorted(off, np.arange(len(items)), side="right") - 1
+    load = [0] * lists
+    seen = [0] * lists
+    for i in order:
+        w = min(range(lists), key=lambda x: (load[x], x))
+        assert lst[i] == w
+        load[w] += int(items[i, 6]) + 2
+        seen[w] += 1
+    assert seen == list(np.diff(off))
     # shapes without the list: fp32 queries, FP8 at head_dim 64, and fp16 at
     # head_dim 64 with groups of 4 heads or more (the register-staged kernel)
     p32 = _prefill_params(vkv, io_dtype=0, kv_dtype=0)

@@ -35,6 +35,9 @@
 // scale, fp32 -> fp16).  Block ids of the sequence are cached in LDS, 1024 at
 // a time.
 #include <algorithm>
+#include <functional>
+#include <queue>
+#include <utility>
 #include <type_traits>
 #include <vector>
 
@@ -99,11 +102,25 @@ struct PrefillArgs {
     int32_t* inline_claim;
     int32_t rows_per_item;
     int32_t nbins;
-    // host-built work list (vkv_prefill_work_list_host), or nullptr; its claim
-    // counters live in list_claim (the workspace header ints, zero between calls)
+    // host-built schedule (vkv_prefill_work_list_host), or nullptr
     const int32_t* work_list;
-    int32_t work_list_items;  // items the list's words can hold (bounds every index read from it)
-    int32_t* list_claim;
+    int32_t work_list_words;  // its length (bounds every index read from it)
+    int32_t num_query_tokens;
+    // division by the group size G: n / G = (n + mulhi(n, m)) >> s for 0 <= n < 2^31
+    uint32_t group_div_m;
+    int32_t group_div_s;
+};
+
+// The query token of row rho (rows are (token, head) pairs, token-major).
+__device__ __forceinline__ int row_token(const PrefillArgs& a, const int rho) {
+    return int((uint32_t(rho) + __umulhi(uint32_t(rho), a.group_div_m)) >> a.group_div_s);
+}
+
+// One work item: row block b of sequence s at kv head kvh, with the
+// sequence's first query row q0, its query length and its prior context
+// (context length - query length).
+struct PrefillItem {
+    int s, b, kvh, q0, qlen, prior;
 };
 
 template <int D, int KVT>
@@ -585,8 +602,55 @@ __device__ __forceinline__ int row_block_bin(int prior, int q, int b, int row_mu
     return nbins - 1 - int(tiles < nbins - 1 ? tiles : nbins - 1);
 }
 
+// Output rows through LDS.  A wave's RT row tiles of O (accumulator layout:
+// lane (row col) holds dims 16 t + 4 grp + e of row 16 r + col), scaled by
+// inv[r] and rounded to fp16, go to its 16 RT rows x D region ob, then are
+// read back as 16-byte pieces of rows: every store writes whole rows (the
+// accumulator layout stores 8 bytes to each of 16 rows per instruction).
+// Piece q of row R sits at R * 2D + (q ^ (R % P)) * 16, P pieces per row.
+// Rows rho0 + R at or past nrows are not stored.
+template <int D, int RT>
+__device__ __forceinline__ void store_rows_lds(const PrefillArgs& a, char* ob, const float4_t (&o)[RT][D / 16],
+                                               const float (&inv)[RT], const int rho0, const int nrows, const int q0,
+                                               const int kvh, const int lane_in) {
+    constexpr int ROW = D * 2;
+    constexpr int P = ROW / 16;   // 16-byte pieces per row
+    constexpr int RPI = 64 / P;   // rows per wave instruction
+    // (the lane index through an opaque copy: the compiler would otherwise
+    // compute these addresses once before the item loop and hold them in
+    // registers across it)
+    int lane = lane_in;
+    asm volatile("" : "+v"(lane));
+    const int col = lane & 15, grp = lane >> 4;
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+        const int row = 16 * r + col;
+#pragma unroll
+        for (int t = 0; t < D / 16; ++t) {
+            const half2_t lo = {static_cast<_Float16>(o[r][t][0] * inv[r]), static_cast<_Float16>(o[r][t][1] * inv[r])};
+            const half2_t hi = {static_cast<_Float16>(o[r][t][2] * inv[r]), static_cast<_Float16>(o[r][t][3] * inv[r])};
+            const int q = 2 * t + (grp >> 1);
+            *reinterpret_cast<u32x2*>(ob + row * ROW + ((q ^ (row & (P - 1))) << 4) + (grp & 1) * 8) =
+                u32x2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
+        }
+    }
+    // (a wave's LDS accesses complete in order: its own rows need no barrier)
+    const int pq = lane % P;
+#pragma unroll
+    for (int i = 0; i < 16 * RT / RPI; ++i) {
+        const int row = RPI * i + lane / P;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(ob + row * ROW + ((pq ^ (row & (P - 1))) << 4));
+        const int rho = rho0 + row;
+        if (rho < nrows) {
+            const int j = row_token(a, rho);
+            const int h = kvh * a.group + rho - j * a.group;
+            store16(a.out + ((int64_t(q0) + j) * a.num_heads + h) * D + pq * 8, v);
+        }
+    }
+}
+
 template <int D, bool FP8>
-__device__ __forceinline__ void prefill_block_wide(const PrefillArgs& a, const int s, const int b, const int kvh,
+__device__ __forceinline__ void prefill_block_wide(const PrefillArgs& a, const PrefillItem& it,
                                                    const WideBuffers& buf) {
     using T = DmaTile<D>;  // the fp16 tile the MFMAs read
     using L = typename std::conditional<FP8, DmaTile8<D>, DmaTile<D>>::type;  // the tile the loads fill
@@ -608,11 +672,12 @@ __device__ __forceinline__ void prefill_block_wide(const PrefillArgs& a, const i
     const int G = a.group;
     int* btc = buf.btc;
 
-    const int q0 = a.qsl[s];
-    const int qlen = a.qsl[s + 1] - q0;
+    const int s = it.s, b = it.b, kvh = it.kvh;
+    const int q0 = it.q0;
+    const int qlen = it.qlen;
     const int nrows = qlen * G;
     if (qlen < 2 || b * kWideRows >= nrows) return;  // (the item list holds none of these)
-    const int prior = a.cl[s] - qlen;
+    const int prior = it.prior;
     const int last_row = min(nrows, (b + 1) * kWideRows) - 1;
     int kend = prior + last_row / G + 1;  // keys any row of the block may see
     kend = kend < a.table_tokens ? kend : a.table_tokens;
@@ -901,6 +966,32 @@ __device__ __forceinline__ void prefill_block_wide(const PrefillArgs& a, const i
     }
     wait_vmcnt<0>();  // no load of this item may land in the next item's buffers
 
+    if constexpr (D == 128) {
+        // ---------------- output through LDS, 8 KiB per wave: FP8, the six
+        // code buffers and the two fp16 tiles; fp16, the halves of the six
+        // tile buffers
+        static_assert(16 * RT * D * 2 == 8192 && DmaTile8<D>::BYTES == 8192 && T::BYTES == 16384,
+                      "8 KiB of output rows per wave");
+        __syncthreads();  // every wave's loads have landed and no wave reads a tile
+        // (constant indices only: a buffer array indexed by a variable would
+        // be materialised in memory)
+        char* ob;
+        if constexpr (FP8) {
+            ob = wave == 0 ? buf.f8k[0] : wave == 1 ? buf.f8k[1] : wave == 2 ? buf.f8k[2] : wave == 3 ? buf.f8v[0]
+               : wave == 4 ? buf.f8v[1] : wave == 5 ? buf.f8v[2] : wave == 6 ? buf.k[0] : buf.v[0];
+        } else {
+            const int h2 = wave >> 1;
+            ob = (h2 == 0 ? buf.k[0] : h2 == 1 ? buf.k[1] : h2 == 2 ? buf.k[2] : buf.v[0]) + (wave & 1) * 8192;
+        }
+        float inv[RT];
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+            const float lt = lsum[r][0];
+            inv[r] = (rctx[r] > 0 && lt > 0.0f) ? 1.0f / lt : 0.0f;
+        }
+        store_rows_lds<D, RT>(a, ob, o, inv, b * kWideRows + 16 * RT * wave, nrows, q0, kvh, lane);
+        return;
+    }
     // ---------------- output: lane (row col) holds dims 16 t + 4 grp + e
 #pragma unroll
     for (int r = 0; r < RT; ++r) {
@@ -993,31 +1084,30 @@ __device__ int inline_row_blocks(const PrefillArgs& a, int2* lblk) {
     return total;
 }
 
-// Host-built work list (vkv_prefill_work_list_host): 32 header words (the
-// number of lists nx, then nx item offsets, then nx counts), then the items
-// (s, b * Hkv + kvh) as int2.  A workgroup claims from list blockIdx % nx
-// (workgroups reach the XCDs round robin, so per-XCD lists are possible)
-// through that list's counter, then from the next lists once it is exhausted.
-// The host builds one list (nx = 1), longest first.  Counters: workspace
-// header ints kListClaim0 + 32 x (one 128-byte line each) and kListDone.
+// Host-built schedule (vkv_prefill_work_list_host): 32 header words ([0] W
+// lists, one per workgroup of the persistent grid; [1] N items; [2] the
+// format, kListFormat), then W + 1 offsets (list w holds items off[w] ..
+// off[w + 1] - 1) padded to a multiple of 4 words, then the items,
+// kListItemWords each: s, b, kvh, q0, qlen, prior, key tiles, 0.  The host
+// deals the items to the lists longest first, each to the list with the least
+// work so far (a longest-processing-time schedule made before the launch), so
+// a workgroup knows its next item while it computes the current one.
 constexpr int kListHeaderWords = 32;
-constexpr int kListMaxXcds = 8;
-constexpr int kListClaim0 = 16;
-constexpr int kListDone = 4;
-__device__ __forceinline__ int list_count(const PrefillArgs& a) {
-    const int n = a.work_list[0];
-    return n < 1 ? 1 : (n > kListMaxXcds ? kListMaxXcds : n);
+constexpr int kListFormat = 2;
+constexpr int kListItemWords = 8;
+// Cost of an item in the host's schedule: its key tiles plus this many for
+// its start (the chain of loads before its first tile can be computed).
+constexpr int kListItemStartTiles = 5;
+constexpr int kListDefaultCus = 256;  // lists when the builder finds no device
+__host__ __device__ constexpr int64_t list_items_word(int64_t lists) {
+    return kListHeaderWords + ((lists + 1 + 3) & ~int64_t(3));
 }
-__device__ __forceinline__ int claim_listed(const PrefillArgs& a, int& x, int& tried) {
-    const int32_t* wl = a.work_list;
-    const int nx = list_count(a);
-    while (tried < nx) {
-        const int k = atomicAdd(a.list_claim + kListClaim0 + 32 * x, 1);
-        if (k < wl[1 + nx + x]) return wl[1 + x] + k;
-        x = x + 1 < nx ? x + 1 : 0;
-        ++tried;
-    }
-    return -1;
+
+// The sequence fields of item (s, b, kvh), read from the call's arrays.
+__device__ __forceinline__ PrefillItem load_item(const PrefillArgs& a, const int s, const int b, const int kvh) {
+    const int q0 = a.qsl[s];
+    const int qlen = a.qsl[s + 1] - q0;
+    return PrefillItem{s, b, kvh, q0, qlen, a.cl[s] - qlen};
 }
 
 // Persistent claim loop of the direct-load kernels (NT threads): work items
@@ -1027,22 +1117,42 @@ template <int NT, typename Item>
 __device__ __forceinline__ void run_items(const PrefillArgs& a, Item item_fn) {
     __shared__ int claimed;
     if (a.work_list) {
-        int x = int(blockIdx.x) % list_count(a), tried = 0;  // (thread 0's)
-        for (;;) {
-            if (threadIdx.x == 0) claimed = claim_listed(a, x, tried);
-            __syncthreads();
-            const int it = claimed;
-            __syncthreads();
-            if (it < 0) break;
-            if (it >= a.work_list_items) continue;  // (a list from another call: never read past it)
-            const int2 item = reinterpret_cast<const int2*>(a.work_list + kListHeaderWords)[it];
-            if (unsigned(item.x) < unsigned(a.num_seqs) && item.y >= 0)
-                item_fn(item.x, item.y / a.num_kv_heads, item.y % a.num_kv_heads);
-        }
-        // the last workgroup out returns the counters to zero for the next call
-        if (threadIdx.x == 0 && atomicAdd(a.list_claim + kListDone, 1) == int(gridDim.x) - 1) {
-            for (int i = 0; i < list_count(a); ++i) a.list_claim[kListClaim0 + 32 * i] = 0;
-            a.list_claim[kListDone] = 0;
+        // Workgroup w runs list w (and w + grid, ...), no claims.  Every index
+        // read from the list is bounded by its length, and items outside the
+        // call's sequences, kv heads and query rows are skipped, so a list
+        // from another call gives wrong rows but reads nothing out of bounds.
+        const int32_t* wl = a.work_list;
+        const int lists = wl[0], n = wl[1];
+        if (wl[2] != kListFormat || lists < 1 || n < 0 ||
+            list_items_word(lists) + int64_t(n) * kListItemWords > a.work_list_words)
+            return;
+        const int32_t* off = wl + kListHeaderWords;
+        const int32_t* items = wl + list_items_word(lists);
+        for (int w = blockIdx.x; w < lists; w += gridDim.x) {
+            int beg = off[w], end = off[w + 1];
+            beg = beg < 0 ? 0 : (beg > n ? n : beg);
+            end = end < beg ? beg : (end > n ? n : end);
+            if (beg >= end) continue;
+            PrefillItem nx;
+            auto fetch = [&](const int i) __attribute__((always_inline)) {
+                const int32_t* e = items + int64_t(i) * kListItemWords;
+                nx = PrefillItem{e[0], e[1], e[2], e[3], e[4], e[5]};
+            };
+            auto valid = [&](const PrefillItem& it) __attribute__((always_inline)) {
+                return unsigned(it.s) < unsigned(a.num_seqs) && unsigned(it.kvh) < unsigned(a.num_kv_heads) &&
+                       it.b >= 0 && it.q0 >= 0 && it.qlen >= 2 && int64_t(it.q0) + it.qlen <= a.num_query_tokens;
+            };
+            fetch(beg);
+            for (int i = beg; i < end; ++i) {
+                const PrefillItem it = nx;
+                const bool ok = valid(it);
+                // the next item's entry, requested after this one is checked
+                // (waiting for this one then waits for nothing else) and
+                // arriving while this one runs
+                asm volatile("" ::: "memory");
+                if (i + 1 < end) fetch(i + 1);
+                if (ok) item_fn(it);
+            }
         }
         return;
     }
@@ -1066,7 +1176,7 @@ __device__ __forceinline__ void run_items(const PrefillArgs& a, Item item_fn) {
         } else {
             item = a.items[it];
         }
-        item_fn(item.x, item.y / a.num_kv_heads, item.y % a.num_kv_heads);
+        item_fn(load_item(a, item.x, item.y / a.num_kv_heads, item.y % a.num_kv_heads));
         if (threadIdx.x == 0) claimed = atomicAdd(claim, 1);
     }
     // Every claim of this workgroup has returned (its value decided the exit);
@@ -1080,8 +1190,8 @@ __device__ __forceinline__ void run_items(const PrefillArgs& a, Item item_fn) {
 
 template <int D, bool FP8>
 __device__ __forceinline__ void wide_items(const PrefillArgs& a, const WideBuffers& buf) {
-    run_items<64 * kWideWaves>(a, [&](int s, int b, int kvh) __attribute__((always_inline)) {
-        prefill_block_wide<D, FP8>(a, s, b, kvh, buf);
+    run_items<64 * kWideWaves>(a, [&](const PrefillItem& it) __attribute__((always_inline)) {
+        prefill_block_wide<D, FP8>(a, it, buf);
     });
 }
 
@@ -1253,8 +1363,17 @@ __device__ __forceinline__ float slot_max3(const float a, const float b, const f
     return r;
 }
 
+// Keys any row of row block b may see (the rows' largest context), clamped to
+// the table.
+__device__ __forceinline__ int item_kend(const PrefillArgs& a, const PrefillItem& it, const int rows) {
+    const int nrows = it.qlen * a.group;
+    const int last_row = min(nrows, (it.b + 1) * rows) - 1;
+    const int kend = it.prior + last_row / a.group + 1;
+    return kend < a.table_tokens ? kend : a.table_tokens;
+}
+
 template <int D>
-__device__ __forceinline__ void prefill_block_w64(const PrefillArgs& a, const int s, const int b, const int kvh,
+__device__ __forceinline__ void prefill_block_w64(const PrefillArgs& a, const PrefillItem& it,
                                                   const W64Buffers& buf) {
     using T = DmaTile<D>;
     constexpr int EB = 2;
@@ -1276,14 +1395,13 @@ __device__ __forceinline__ void prefill_block_w64(const PrefillArgs& a, const in
     const int G = a.group;
     int* btc = buf.btc;
 
-    const int q0 = a.qsl[s];
-    const int qlen = a.qsl[s + 1] - q0;
+    const int s = it.s, b = it.b, kvh = it.kvh;
+    const int q0 = it.q0;
+    const int qlen = it.qlen;
     const int nrows = qlen * G;
     if (qlen < 2 || b * kRows >= nrows) return;  // (the item list holds none of these)
-    const int prior = a.cl[s] - qlen;
-    const int last_row = min(nrows, (b + 1) * kRows) - 1;
-    int kend = prior + last_row / G + 1;  // keys any row of the block may see
-    kend = kend < a.table_tokens ? kend : a.table_tokens;
+    const int prior = it.prior;
+    const int kend = item_kend(a, it, kRows);  // keys any row of the block may see
     const int ntiles = kend > 0 ? (kend + kBK - 1) / kBK : 0;
 
     // ---------------- loads of tile t, through block ids held in LDS (as in prefill_block_wide)
@@ -1647,31 +1765,23 @@ __device__ __forceinline__ void prefill_block_w64(const PrefillArgs& a, const in
     }
     wait_vmcnt<0>();  // no load of this item may land in the next item's buffers
 
-    // ---------------- output: lane (row col) holds dims 16 t + 4 grp + e
+    // ---------------- output through LDS (16 KiB per wave, in the tile buffers)
+    __syncthreads();  // every wave's loads have landed and no wave reads a tile
     agpr_fence(o, lsum);
+    static_assert(64 * D * EB * kW64Waves <= kW64Stages * 2 * T::BYTES, "the output fits in the tile buffers");
+    float inv[RT];
 #pragma unroll
     for (int r = 0; r < RT; ++r) {
-        const int rho = b * kRows + 16 * RT * wave + 16 * r + col;
-        if (rho >= nrows) continue;
-        const int j = rho / G;
-        const int h = kvh * G + rho - j * G;
         const float lt = lsum[r][0];
-        const float inv = (rctx[r] > 0 && lt > 0.0f) ? 1.0f / lt : 0.0f;
-        _Float16* orow = a.out + ((int64_t(q0) + j) * a.num_heads + h) * D;
-#pragma unroll
-        for (int t2 = 0; t2 < DT; ++t2) {
-            const half2_t lo = {static_cast<_Float16>(o[r][t2][0] * inv), static_cast<_Float16>(o[r][t2][1] * inv)};
-            const half2_t hi = {static_cast<_Float16>(o[r][t2][2] * inv), static_cast<_Float16>(o[r][t2][3] * inv)};
-            *reinterpret_cast<u32x2*>(orow + 16 * t2 + 4 * grp) =
-                u32x2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
-        }
+        inv[r] = (rctx[r] > 0 && lt > 0.0f) ? 1.0f / lt : 0.0f;
     }
+    store_rows_lds<D, RT>(a, buf.tiles + wave * (64 * D * EB), o, inv, b * kRows + 64 * wave, nrows, q0, kvh, lane);
 }
 
 template <int D>
 __device__ __forceinline__ void w64_items(const PrefillArgs& a, const W64Buffers& buf) {
-    run_items<64 * kW64Waves>(a, [&](int s, int b, int kvh) __attribute__((always_inline)) {
-        prefill_block_w64<D>(a, s, b, kvh, buf);
+    run_items<64 * kW64Waves>(a, [&](const PrefillItem& it) __attribute__((always_inline)) {
+        prefill_block_w64<D>(a, it, buf);
     });
 }
 
@@ -1883,9 +1993,16 @@ int launch_prefill_mfma(const vkv_prefill_params* p, void* item_space, int32_t* 
     const int64_t nseq2 = p->num_seqs < T / 2 ? p->num_seqs : T / 2;
     const int64_t bound = T * row_mult / rpi + nseq2;
     // a host-built list (wide kernels only) replaces both in-kernel orderings
-    a.work_list = wide && header != nullptr && p->work_list && p->work_list_words > kListHeaderWords ? p->work_list : nullptr;
-    a.work_list_items = a.work_list ? (p->work_list_words - kListHeaderWords) / 2 : 0;
-    a.list_claim = header;
+    a.work_list = wide && p->work_list && p->work_list_words > kListHeaderWords ? p->work_list : nullptr;
+    a.work_list_words = a.work_list ? p->work_list_words : 0;
+    a.num_query_tokens = int32_t(p->num_query_tokens);
+    {
+        int sh = 0;
+        while ((int64_t(1) << sh) < a.group) ++sh;
+        const uint64_t m = ((uint64_t(1) << (32 + sh)) + uint64_t(a.group) - 1) / uint64_t(a.group);
+        a.group_div_m = uint32_t(m - (uint64_t(1) << 32));
+        a.group_div_s = sh;
+    }
     a.inline_list = !a.work_list && wide && inline_claim != nullptr && bound <= kInlineBlocks;
     a.inline_claim = inline_claim;
     if (!a.inline_list && !a.work_list)
@@ -1926,9 +2043,9 @@ int64_t prefill_work_list_host(const vkv_prefill_params* p, const int32_t* host_
     const int64_t qblocks = max_row_blocks(p);
     int64_t tt = int64_t(p->max_blocks_per_seq) * p->block_size;
     if (p->max_context_len > 0 && p->max_context_len < tt) tt = p->max_context_len;
-    // items (s, b * Hkv + kvh) in (s, b, kvh) order with their key tiles
+    // items in (s, b, kvh) order with their key tiles
     struct Item {
-        int32_t s, y, tiles;
+        int32_t s, b, kvh, q0, qlen, prior, tiles;
     };
     std::vector<Item> items;
     for (int32_t s = 0; s < p->num_seqs; ++s) {
@@ -1942,26 +2059,55 @@ int64_t prefill_work_list_host(const vkv_prefill_params* p, const int32_t* host_
             int64_t kend = prior + (last < q ? last : q);
             kend = kend < tt ? kend : tt;
             const int32_t tiles = int32_t(kend > 0 ? (kend + kBK - 1) / kBK : 0);
-            for (int k = 0; k < hkv; ++k) items.push_back(Item{s, int32_t(b * hkv + k), tiles});
+            for (int k = 0; k < hkv; ++k)
+                items.push_back(Item{s, int32_t(b), k, host_qsl[s], int32_t(q), int32_t(prior), tiles});
         }
     }
-    const int64_t words = kListHeaderWords + 2 * int64_t(items.size());
+    // one list per workgroup of the persistent grid (one per CU)
+    int dev = 0, cus = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess || cus <= 0) {
+        cus = kListDefaultCus;
+        (void)hipGetLastError();  // (no device: the default, and no error left behind)
+    }
+    const int64_t n = int64_t(items.size());
+    const int64_t lists = n < cus ? (n > 0 ? n : 1) : cus;
+    const int64_t words = list_items_word(lists) + kListItemWords * n;
     if (!out) return words;
     if (capacity < words) return -2;
-    // one list, longest first (ties in (s, b, kvh) order): a longest-
-    // processing-time schedule for the persistent workgroups that claim the
-    // items in turn.  (One list per XCD, each group of items of a sequence and
-    // kv head on one XCD, was slower: C3's prefill call 93.5 against 90 us.)
+    // Longest first (ties in (s, b, kvh) order), each item to the list with
+    // the least work so far (ties: the lowest list).
     std::stable_sort(items.begin(), items.end(), [](const Item& u, const Item& v) { return u.tiles > v.tiles; });
-    std::fill(out, out + kListHeaderWords, 0);
-    out[0] = 1;
-    out[1] = 0;
-    out[2] = int32_t(items.size());
-    int32_t* dst = out + kListHeaderWords;
-    for (const Item& it : items) {
-        *dst++ = it.s;
-        *dst++ = it.y;
+    std::vector<std::vector<int32_t>> dealt{static_cast<size_t>(lists)};
+    typedef std::pair<int64_t, int64_t> Load;  // (work, list)
+    std::priority_queue<Load, std::vector<Load>, std::greater<Load>> least;
+    for (int64_t w = 0; w < lists; ++w) least.push(Load(0, w));
+    for (int64_t i = 0; i < n; ++i) {
+        Load l = least.top();
+        least.pop();
+        dealt[size_t(l.second)].push_back(int32_t(i));
+        l.first += items[size_t(i)].tiles + kListItemStartTiles;
+        least.push(l);
     }
+    std::fill(out, out + list_items_word(lists), 0);
+    out[0] = int32_t(lists);
+    out[1] = int32_t(n);
+    out[2] = kListFormat;
+    int32_t* off = out + kListHeaderWords;
+    int32_t* dst = out + list_items_word(lists);
+    int32_t k = 0;
+    for (int64_t w = 0; w < lists; ++w) {
+        off[w] = k;
+        for (const int32_t i : dealt[size_t(w)]) {
+            const Item& it = items[size_t(i)];
+            const int32_t e[kListItemWords] = {it.s, it.b, it.kvh, it.q0, it.qlen, it.prior, it.tiles, 0};
+            std::copy(e, e + kListItemWords, dst);
+            dst += kListItemWords;
+            ++k;
+        }
+    }
+    off[lists] = k;
     return words;
 }
 
