@@ -250,34 +250,39 @@ def test_prefill_work_list_host(vkv, shape):
             t = (int(prior[s]) + last + 63) // 64
             for k in range(Hkv):
                 want[(s, b, k)] = (int(qsl[s]), int(q_lens[s]), int(prior[s]), t)
-    # one list per CU (256 on this device, and without a device), at most one per item
+    # one list per CU (256 on this device, and without a device), at most one
+    # per item; slot k of list w at k W + w, 8 words each, s = -1 past its end
     lists = min(256, len(want))
-    items_word = 32 + (lists + 1 + 3) // 4 * 4
-    assert n == items_word + 8 * len(want)
     words = np.zeros(n, np.int32)
     assert lib.vkv_prefill_work_list_host(ctypes.byref(p), qsl.ctypes.data, ctx.ctypes.data,
                                           words.ctypes.data, n - 1) == -2
     assert lib.vkv_prefill_work_list_host(ctypes.byref(p), qsl.ctypes.data, ctx.ctypes.data,
                                           words.ctypes.data, n) == n
-    assert words[0] == lists and words[1] == len(want) and words[2] == 2
-    off = words[32:32 + lists + 1]
-    assert off[0] == 0 and off[-1] == len(want) and np.all(np.diff(off) >= 0)
-    items = words[items_word:].reshape(-1, 8)
-    got = {(int(e[0]), int(e[1]), int(e[2])): (int(e[3]), int(e[4]), int(e[5]), int(e[6])) for e in items}
-    assert got == want and len(items) == len(want)
+    assert words[0] == lists and words[2] == 3 and words[3] == len(want)
+    L = int(words[1])
+    assert n == 32 + 8 * lists * L
+    slots = words[32:].reshape(L, lists, 8)
+    got = {}
+    per_list = []
+    for w in range(lists):
+        col = [slots[k, w] for k in range(L) if slots[k, w, 0] >= 0]
+        assert all(slots[k, w, 0] == -1 for k in range(len(col), L))  # the list ends once
+        per_list.append(col)
+        for e in col:
+            got[(int(e[0]), int(e[1]), int(e[2]))] = (int(e[3]), int(e[4]), int(e[5]), int(e[6]))
+    assert got == want and sum(len(c) for c in per_list) == len(want)
+    assert L == max(len(c) for c in per_list)
     # the deal, replayed: longest first (ties in (s, b, kvh) order), each item
     # to the least loaded list (ties: the lowest), an item costing its key
-    # tiles + 2
-    order = sorted(range(len(items)), key=lambda i: (-items[i, 6], items[i, 0], items[i, 1], items[i, 2]))
-    lst = np.searchsorted(off, np.arange(len(items)), side="right") - 1
+    # tiles + 5; each list holds its items in the order dealt
+    order = sorted(want, key=lambda k: (-want[k][3], k))
     load = [0] * lists
-    seen = [0] * lists
-    for i in order:
+    dealt = [[] for _ in range(lists)]
+    for key in order:
         w = min(range(lists), key=lambda x: (load[x], x))
-        assert lst[i] == w
-        load[w] += int(items[i, 6]) + 2
-        seen[w] += 1
-    assert seen == list(np.diff(off))
+        load[w] += want[key][3] + 5
+        dealt[w].append(key)
+    assert dealt == [[(int(e[0]), int(e[1]), int(e[2])) for e in c] for c in per_list]
     # shapes without the list: fp32 queries, FP8 at head_dim 64, and fp16 at
     # head_dim 64 with groups of 4 heads or more (the register-staged kernel)
     p32 = _prefill_params(vkv, io_dtype=0, kv_dtype=0)

@@ -1085,23 +1085,21 @@ __device__ int inline_row_blocks(const PrefillArgs& a, int2* lblk) {
 }
 
 // Host-built schedule (vkv_prefill_work_list_host): 32 header words ([0] W
-// lists, one per workgroup of the persistent grid; [1] N items; [2] the
-// format, kListFormat), then W + 1 offsets (list w holds items off[w] ..
-// off[w + 1] - 1) padded to a multiple of 4 words, then the items,
-// kListItemWords each: s, b, kvh, q0, qlen, prior, key tiles, 0.  The host
-// deals the items to the lists longest first, each to the list with the least
-// work so far (a longest-processing-time schedule made before the launch), so
-// a workgroup knows its next item while it computes the current one.
+// lists, one per workgroup of the persistent grid; [1] L slots per list; [2]
+// the format, kListFormat; [3] N items), then W x L slots of kListItemWords
+// words, slot k of list w at k W + w: s, b, kvh, q0, qlen, prior, key tiles, 0
+// (s = -1: the list has ended).  The host deals the items to the lists
+// longest first, each to the list with the least work so far (a
+// longest-processing-time schedule made before the launch), so a workgroup
+// knows its next item while it computes the current one; its first item,
+// slot w, needs no header word and is requested together with the header.
 constexpr int kListHeaderWords = 32;
-constexpr int kListFormat = 2;
+constexpr int kListFormat = 3;
 constexpr int kListItemWords = 8;
 // Cost of an item in the host's schedule: its key tiles plus this many for
 // its start (the chain of loads before its first tile can be computed).
 constexpr int kListItemStartTiles = 5;
 constexpr int kListDefaultCus = 256;  // lists when the builder finds no device
-__host__ __device__ constexpr int64_t list_items_word(int64_t lists) {
-    return kListHeaderWords + ((lists + 1 + 3) & ~int64_t(3));
-}
 
 // The sequence fields of item (s, b, kvh), read from the call's arrays.
 __device__ __forceinline__ PrefillItem load_item(const PrefillArgs& a, const int s, const int b, const int kvh) {
@@ -1122,35 +1120,30 @@ __device__ __forceinline__ void run_items(const PrefillArgs& a, Item item_fn) {
         // call's sequences, kv heads and query rows are skipped, so a list
         // from another call gives wrong rows but reads nothing out of bounds.
         const int32_t* wl = a.work_list;
-        const int lists = wl[0], n = wl[1];
-        if (wl[2] != kListFormat || lists < 1 || n < 0 ||
-            list_items_word(lists) + int64_t(n) * kListItemWords > a.work_list_words)
-            return;
-        const int32_t* off = wl + kListHeaderWords;
-        const int32_t* items = wl + list_items_word(lists);
-        for (int w = blockIdx.x; w < lists; w += gridDim.x) {
-            int beg = off[w], end = off[w + 1];
-            beg = beg < 0 ? 0 : (beg > n ? n : beg);
-            end = end < beg ? beg : (end > n ? n : end);
-            if (beg >= end) continue;
-            PrefillItem nx;
-            auto fetch = [&](const int i) __attribute__((always_inline)) {
-                const int32_t* e = items + int64_t(i) * kListItemWords;
-                nx = PrefillItem{e[0], e[1], e[2], e[3], e[4], e[5]};
-            };
-            auto valid = [&](const PrefillItem& it) __attribute__((always_inline)) {
-                return unsigned(it.s) < unsigned(a.num_seqs) && unsigned(it.kvh) < unsigned(a.num_kv_heads) &&
-                       it.b >= 0 && it.q0 >= 0 && it.qlen >= 2 && int64_t(it.q0) + it.qlen <= a.num_query_tokens;
-            };
-            fetch(beg);
-            for (int i = beg; i < end; ++i) {
+        const int32_t* slots = wl + kListHeaderWords;
+        const int64_t cap = (int64_t(a.work_list_words) - kListHeaderWords) / kListItemWords;
+        PrefillItem nx;
+        auto fetch = [&](const int64_t k) __attribute__((always_inline)) {
+            const int32_t* e = slots + k * kListItemWords;
+            nx = PrefillItem{e[0], e[1], e[2], e[3], e[4], e[5]};
+        };
+        auto valid = [&](const PrefillItem& it) __attribute__((always_inline)) {
+            return unsigned(it.s) < unsigned(a.num_seqs) && unsigned(it.kvh) < unsigned(a.num_kv_heads) &&
+                   it.b >= 0 && it.q0 >= 0 && it.qlen >= 2 && int64_t(it.q0) + it.qlen <= a.num_query_tokens;
+        };
+        for (int w = blockIdx.x; w < cap; w += gridDim.x) {
+            fetch(w);  // (slot 0 of list w, beside the header)
+            const int lists = wl[0], len = wl[1];
+            if (wl[2] != kListFormat || lists < 1 || len < 0 || int64_t(lists) * len > cap || w >= lists) break;
+            for (int k = 0; k < len; ++k) {
                 const PrefillItem it = nx;
+                if (it.s < 0) break;  // (the list has ended)
                 const bool ok = valid(it);
-                // the next item's entry, requested after this one is checked
-                // (waiting for this one then waits for nothing else) and
-                // arriving while this one runs
+                // the next slot, requested after this one is checked (waiting
+                // for this one then waits for nothing else), arrives while
+                // this item runs
                 asm volatile("" ::: "memory");
-                if (i + 1 < end) fetch(i + 1);
+                if (k + 1 < len) fetch(int64_t(k + 1) * lists + w);
                 if (ok) item_fn(it);
             }
         }
@@ -2073,9 +2066,6 @@ int64_t prefill_work_list_host(const vkv_prefill_params* p, const int32_t* host_
     }
     const int64_t n = int64_t(items.size());
     const int64_t lists = n < cus ? (n > 0 ? n : 1) : cus;
-    const int64_t words = list_items_word(lists) + kListItemWords * n;
-    if (!out) return words;
-    if (capacity < words) return -2;
     // Longest first (ties in (s, b, kvh) order), each item to the list with
     // the least work so far (ties: the lowest list).
     std::stable_sort(items.begin(), items.end(), [](const Item& u, const Item& v) { return u.tiles > v.tiles; });
@@ -2090,24 +2080,27 @@ int64_t prefill_work_list_host(const vkv_prefill_params* p, const int32_t* host_
         l.first += items[size_t(i)].tiles + kListItemStartTiles;
         least.push(l);
     }
-    std::fill(out, out + list_items_word(lists), 0);
+    size_t len = 0;
+    for (const auto& d : dealt) len = d.size() > len ? d.size() : len;
+    const int64_t words = kListHeaderWords + int64_t(kListItemWords) * lists * int64_t(len);
+    if (!out) return words;
+    if (capacity < words) return -2;
+    std::fill(out, out + words, 0);
     out[0] = int32_t(lists);
-    out[1] = int32_t(n);
+    out[1] = int32_t(len);
     out[2] = kListFormat;
-    int32_t* off = out + kListHeaderWords;
-    int32_t* dst = out + list_items_word(lists);
-    int32_t k = 0;
-    for (int64_t w = 0; w < lists; ++w) {
-        off[w] = k;
-        for (const int32_t i : dealt[size_t(w)]) {
-            const Item& it = items[size_t(i)];
-            const int32_t e[kListItemWords] = {it.s, it.b, it.kvh, it.q0, it.qlen, it.prior, it.tiles, 0};
-            std::copy(e, e + kListItemWords, dst);
-            dst += kListItemWords;
-            ++k;
+    out[3] = int32_t(n);
+    for (int64_t w = 0; w < lists; ++w)
+        for (size_t k = 0; k < len; ++k) {
+            int32_t* e = out + kListHeaderWords + (int64_t(k) * lists + w) * kListItemWords;
+            if (k < dealt[size_t(w)].size()) {
+                const Item& it = items[size_t(dealt[size_t(w)][k])];
+                const int32_t v[kListItemWords] = {it.s, it.b, it.kvh, it.q0, it.qlen, it.prior, it.tiles, 0};
+                std::copy(v, v + kListItemWords, e);
+            } else {
+                e[0] = -1;  // the list has ended
+            }
         }
-    }
-    off[lists] = k;
     return words;
 }
 
