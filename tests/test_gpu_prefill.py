@@ -98,6 +98,47 @@ def test_prefill_vs_oracle(vkv, oracle, cuda, kvt, H, Hkv, D, bs, q_lens, prior)
                      f"prefill ({kvt} cache, {'host' if listed else 'in-kernel'} work list)")
 
 
+@pytest.mark.parametrize("kvt", ["f16", "fp8"])
+def test_prefill_work_list_relaid(vkv, oracle, cuda, kvt):
+    """A host-built schedule re-laid into more lists than the grid has
+    workgroups (each workgroup then runs its extra lists in turn), with entries
+    the kernels must skip mixed in (a sequence, kv head or row block past the
+    call's, a single-token or out-of-range query span): every row still
+    matches the oracle."""
+    import torch
+    H, Hkv, D, bs, q_lens, prior = 28, 4, 128, 32, [300, 1, 200, 64], [100, 500, 0, 7]
+    lay, ctx, qsl, q, k, v, scale = _case(H, Hkv, D, bs, q_lens, prior, 91)
+    Tq = q.shape[0]
+    (kc, vc, ks, vs), (hk, hv, hks, hvs) = _cache(vkv, cuda, kvt, k, v)
+    ref = oracle.paged_prefill(q.astype(np.float32), hk, hv, lay.block_tables, ctx, qsl, scale,
+                               key_scales=hks, value_scales=hvs, nthreads=_threads())
+    args = (to_dev(q, cuda), kc, vc, to_dev(lay.block_tables, cuda), to_dev(ctx, cuda), to_dev(qsl, cuda),
+            int(max(q_lens)), scale)
+    out = torch.zeros((Tq, H, D), dtype=torch.float16, device=cuda)
+    words = vkv.prefill_work_list(out, *args, qsl, ctx, key_scales=ks, value_scales=vs)
+    lists, L = int(words[0]), int(words[1])
+    slots = words[32:].reshape(L, lists, 8)
+    items = [slots[kk, w].copy() for w in range(lists) for kk in range(L) if slots[kk, w, 0] >= 0]
+    assert len(items) == int(words[3])
+    bad = [[9, 0, 0, 0, 300, 100, 1, 0],                 # sequence past the call's
+           [0, 0, 9, 0, 300, 100, 1, 0],                 # kv head past the call's
+           [0, 1 << 24, 0, 0, 300, 100, 1, 0],           # row block past the sequence's rows
+           [1, 0, 0, 300, 1, 499, 1, 0],                 # a single query token
+           [0, 0, 0, Tq - 10, 300, 100, 1, 0]]           # query rows past the call's
+    entries = items + [np.array(e, np.int32) for e in bad]
+    W2 = 300  # more lists than the device's CUs
+    L2 = (len(entries) + W2 - 1) // W2
+    relaid = np.zeros(32 + 8 * W2 * L2, np.int32)
+    relaid[:4] = [W2, L2, words[2], len(entries)]
+    sl = relaid[32:].reshape(L2, W2, 8)
+    sl[:, :, 0] = -1
+    for n, e in enumerate(entries):
+        sl[n // W2, n % W2] = e
+    vkv.paged_prefill(out, *args, key_scales=ks, value_scales=vs, work_list=to_dev(relaid, cuda))
+    torch.cuda.synchronize()
+    assert_close(to_np(out).astype(np.float32), ref, F16_ATOL, F16_RTOL, f"prefill, re-laid list ({kvt} cache)")
+
+
 @pytest.mark.parametrize("bs", [1, 2])
 def test_prefill_small_blocks_vs_oracle(vkv, oracle, cuda, bs):
     """fp16 D = 128 caches with one- and two-token blocks (a direct load's

@@ -1129,7 +1129,8 @@ __device__ __forceinline__ void run_items(const PrefillArgs& a, Item item_fn) {
         };
         auto valid = [&](const PrefillItem& it) __attribute__((always_inline)) {
             return unsigned(it.s) < unsigned(a.num_seqs) && unsigned(it.kvh) < unsigned(a.num_kv_heads) &&
-                   it.b >= 0 && it.q0 >= 0 && it.qlen >= 2 && int64_t(it.q0) + it.qlen <= a.num_query_tokens;
+                   it.b >= 0 && it.q0 >= 0 && it.qlen >= 2 && int64_t(it.q0) + it.qlen <= a.num_query_tokens &&
+                   int64_t(it.b) * a.rows_per_item < int64_t(it.qlen) * a.group;
         };
         for (int w = blockIdx.x; w < cap; w += gridDim.x) {
             fetch(w);  // (slot 0 of list w, beside the header)
