@@ -383,13 +383,26 @@ def suite_c3(dev, steps, warmup):
     def append():
         vkv.reshape_and_cache(nk, nv, kc, vc, slots, stream=stream)
 
+    # the host-built work list of the prefill rows (an engine builds it once
+    # per step beside its other metadata, for every layer)
+    wl = torch.from_numpy(vkv.prefill_work_list(out, q, kc, vc, bt, cl, qsl, mql, cfg.scale, qsl_np,
+                                                lay.context_lens)).to(dev)
+
     def attn():
+        vkv.paged_prefill(out, q, kc, vc, bt, cl, qsl, mql, cfg.scale, stream=stream, work_list=wl)
+
+    def attn_unlisted():
         vkv.paged_prefill(out, q, kc, vc, bt, cl, qsl, mql, cfg.scale, stream=stream)
 
-    _warm(lambda: (append(), attn()), warmup)
+    _warm(lambda: (append(), attn(), attn_unlisted()), warmup)
     torch.cuda.synchronize()
     t_app = _events_ms(append, steps, stream)
-    t_att = _events_ms(attn, steps, stream)
+    # the two variants alternate, three rounds each (the call's time drifts
+    # with the clocks by more than their difference); the round with the
+    # median time is reported
+    rounds = sorted((_events_ms(attn, steps, stream), _events_ms(attn_unlisted, steps, stream)) for _ in range(3))
+    t_att = sorted(r[0] for r in rounds)[1]
+    t_un = sorted(r[1] for r in rounds)[1]
     npf = int((cfg.q_lens > 1).sum())
     # attended keys per prefill query row: prior + j + 1; FLOPs = 4 D per (query head, key)
     keys = sum(int(cfg.prior_lens[s]) * int(cfg.q_lens[s]) + int(cfg.q_lens[s]) * (int(cfg.q_lens[s]) + 1) // 2
@@ -401,6 +414,8 @@ def suite_c3(dev, steps, warmup):
             "query_tokens": Tq, "append_us_median": round(t_app[0] * 1e3, 2),
             "prefill_call_us_median": round(t_att[0] * 1e3, 2), "prefill_call_us_p10_p90":
             [round(t_att[1] * 1e3, 2), round(t_att[2] * 1e3, 2)],
+            "work_list": "host-built (vkv_prefill_work_list_host), built once before the timed calls",
+            "prefill_call_us_in_kernel_list": round(t_un[0] * 1e3, 2),
             "prefill_rows_gflop": round(flops / 1e9, 2), "decode_rows_kv_bytes": dec_bytes,
             "step_us": round((t_app[0] + t_att[0]) * 1e3, 2)}
 
