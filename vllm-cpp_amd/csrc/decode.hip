@@ -1414,8 +1414,7 @@ int launch_prefill(const vkv_prefill_params* p, const DecodePlan& plan, void* wo
         // CU to keep enough bytes in flight.
         const size_t items_off = plan.workspace_bytes - prefill_items_bytes(p);
         const vkv_decode_params d = prefill_as_decode(p, true);
-        const int rc = launch_prefill_mfma(p, static_cast<char*>(workspace) + items_off,
-                                           static_cast<int32_t*>(workspace), st);
+        const int rc = launch_prefill_mfma(p, static_cast<char*>(workspace) + items_off, st);
         // (the caller's promise of no single-token sequence spares the decode
         // pass: its kernels cost ~9 us even when they find no row)
         if (rc || p->multi_token_only) return rc;

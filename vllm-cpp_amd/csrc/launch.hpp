@@ -54,16 +54,14 @@ int launch_prefill(const vkv_prefill_params* p, const DecodePlan& plan, void* wo
 vkv_decode_params prefill_as_decode(const vkv_prefill_params* p, bool per_sequence);
 bool prefill_mfma_supported(const vkv_prefill_params* p);
 size_t prefill_items_bytes(const vkv_prefill_params* p);
-// header: the workspace header ints (zero between calls): the claim and done
-// counters of the kernels' in-kernel work list (kPrefillClaimSlot) and of a
-// host-built one (ints 4 and 16 + 32 x); the kernels leave them zero.
-int launch_prefill_mfma(const vkv_prefill_params* p, void* item_space, int32_t* header, hipStream_t st);
+// item_space: prefill_items_bytes(p) bytes of workspace for the list kernel's
+// items and counters.
+int launch_prefill_mfma(const vkv_prefill_params* p, void* item_space, hipStream_t st);
 // vkv_prefill_work_list_host
 int64_t prefill_work_list_host(const vkv_prefill_params* p, const int32_t* host_qsl, const int32_t* host_cl,
                                int32_t* out, int64_t capacity);
 // Decode workspace header ints (the claim counters use 0, 32, 64, ...).
 constexpr int kChosenPartitionSlot = 1;  // partition size the partition kernel chose
-constexpr int kPrefillClaimSlot = 2;     // claim and done counters (ints 2, 3) of the fp16 prefill kernel's list
 
 struct PlaneSet {
     char* base[4];

@@ -94,12 +94,9 @@ struct PrefillArgs {
     const int2* items;       // work list (s, b * Hkv + kvh), b the sequence's row block
     int32_t* item_count;     // [0] items, [1 + z] claim counter of head group z (zeroed by the list kernel)
     float scale_log2;
-    // fp16 kernel, calls of at most kInlineBlocks row blocks: every workgroup
-    // orders the blocks itself (no list kernel); inline_claim is the claim
-    // counter and inline_claim[1] counts the workgroups that are done (both
-    // zero at entry; the last workgroup out returns them to zero)
+    // direct-load kernels, calls of at most kInlineBlocks row blocks: every
+    // workgroup orders the blocks itself (no list kernel)
     int32_t inline_list;
-    int32_t* inline_claim;
     int32_t rows_per_item;
     int32_t nbins;
     // host-built schedule (vkv_prefill_work_list_host), or nullptr
@@ -1108,12 +1105,11 @@ __device__ __forceinline__ PrefillItem load_item(const PrefillArgs& a, const int
     return PrefillItem{s, b, kvh, q0, qlen, a.cl[s] - qlen};
 }
 
-// Persistent claim loop of the direct-load kernels (NT threads): work items
-// from the host-built list, the in-kernel list (small calls) or the list
-// kernel's; item(s, b, kvh) runs one.
+// Persistent loop of the direct-load kernels (NT threads): work items from the
+// host-built schedule, the in-kernel list (small calls) or the list kernel's;
+// item_fn(it) runs one.  No item is claimed, so no counter needs resetting.
 template <int NT, typename Item>
 __device__ __forceinline__ void run_items(const PrefillArgs& a, Item item_fn) {
-    __shared__ int claimed;
     if (a.work_list) {
         // Workgroup w runs list w (and w + grid, ...), no claims.  Every index
         // read from the list is bounded by its length, and items outside the
@@ -1150,35 +1146,27 @@ __device__ __forceinline__ void run_items(const PrefillArgs& a, Item item_fn) {
         }
         return;
     }
+    // The in-kernel list (every workgroup orders a small call's row blocks
+    // itself) or the list kernel's, longest first, dealt to the workgroups in
+    // a snake: round r gives item r W + p to workgroup p when r is even and
+    // to W - 1 - p when r is odd (W workgroups, all resident: one per CU), so
+    // the longest items meet the shortest ones, as a longest-processing-time
+    // schedule would put them, with no claims.
     __shared__ int2 lblk[kInlineBlocks];  // inline list: (s, b) of row block i, then in longest-first order
-    int* claim = a.inline_list ? a.inline_claim : a.item_count + 1;
-    // the first claim travels while the list is built (or its length loaded)
-    int first = 0;
-    if (threadIdx.x == 0) first = atomicAdd(claim, 1);
     const int count = a.inline_list ? inline_row_blocks<NT>(a, lblk) * a.num_kv_heads : a.item_count[0];
-    if (threadIdx.x == 0) claimed = first;
-    for (;;) {
-        __syncthreads();
-        const int it = claimed;
-        __syncthreads();
-        if (it >= count) break;
+    const int W = gridDim.x, p = blockIdx.x;
+    for (int r = 0;; ++r) {
+        const int64_t it = int64_t(r) * W + ((r & 1) ? W - 1 - p : p);
+        if (it >= count) break;  // (later rounds are further on)
         // items (row block, kv head), kv head fastest
         int2 item;
         if (a.inline_list) {
             const int2 blk = lblk[it / a.num_kv_heads];
-            item = int2{blk.x, blk.y * a.num_kv_heads + it % a.num_kv_heads};
+            item = int2{blk.x, blk.y * a.num_kv_heads + int(it % a.num_kv_heads)};
         } else {
             item = a.items[it];
         }
         item_fn(load_item(a, item.x, item.y / a.num_kv_heads, item.y % a.num_kv_heads));
-        if (threadIdx.x == 0) claimed = atomicAdd(claim, 1);
-    }
-    // Every claim of this workgroup has returned (its value decided the exit);
-    // the last workgroup to arrive here resets the inline counters for the
-    // next call.  (The list kernel zeroes its counters itself.)
-    if (a.inline_list && threadIdx.x == 0 && atomicAdd(a.inline_claim + 1, 1) == int(gridDim.x) - 1) {
-        a.inline_claim[0] = 0;
-        a.inline_claim[1] = 0;
     }
 }
 
@@ -1937,8 +1925,7 @@ size_t prefill_items_bytes(const vkv_prefill_params* p) {
     return 256 + size_t(int64_t(p->num_seqs) * max_row_blocks(p) * p->num_kv_heads) * sizeof(int2);
 }
 
-int launch_prefill_mfma(const vkv_prefill_params* p, void* item_space, int32_t* header, hipStream_t st) {
-    int32_t* inline_claim = header ? header + kPrefillClaimSlot : nullptr;
+int launch_prefill_mfma(const vkv_prefill_params* p, void* item_space, hipStream_t st) {
     PrefillArgs a;
     a.out = static_cast<_Float16*>(p->output);
     a.q = static_cast<const char*>(p->query);
@@ -1997,8 +1984,7 @@ int launch_prefill_mfma(const vkv_prefill_params* p, void* item_space, int32_t* 
         a.group_div_m = uint32_t(m - (uint64_t(1) << 32));
         a.group_div_s = sh;
     }
-    a.inline_list = !a.work_list && wide && inline_claim != nullptr && bound <= kInlineBlocks;
-    a.inline_claim = inline_claim;
+    a.inline_list = !a.work_list && wide && bound <= kInlineBlocks;
     if (!a.inline_list && !a.work_list)
         hipLaunchKernelGGL(prefill_items_kernel, dim3(1), dim3(256), 0, st, p->query_start_loc, p->context_lens,
                            p->num_seqs, p->num_kv_heads, row_mult, rpi, a.qblocks, a.table_tokens, nbins,
