@@ -201,9 +201,9 @@ int vkv_rope_cos_sin_host(float theta, int32_t head_dim, int32_t max_position, f
  * default; the workspace size covers the smallest), so results may differ in
  * the last bits from an explicit size.
  *
- * Workspace.  A caller workspace must have its first 1024 bytes zeroed before
- * its first use (work counters; every call leaves them zero again, apart from
- * int 1, the partition size the call chose), and calls that may run
+ * Workspace.  A caller workspace holds a 1024-byte header (int 1: the
+ * partition size the call chose; zeroing it before first use, as earlier
+ * versions required, is harmless) and the partials, and calls that may run
  * concurrently need distinct workspaces.  workspace == NULL uses a buffer the
  * library keeps per (device, stream): calls on different streams never share
  * it (hipStreamPerThread: per (device, thread)).  It grows with hipMalloc
@@ -279,9 +279,8 @@ int vkv_release_workspace(vkv_stream_t stream);
  * for callers that cannot allocate device memory (code under HIP graph
  * capture, serving loops and harnesses that forbid hipMalloc).  Same
  * arguments, kernels and results as vkv_paged_decode, except that workspace /
- * workspace_bytes are ignored: the split-K partials and claim counters live in
- * a fixed 64 MiB device array of the library (the counters are cleared by a
- * kernel at the start of each call).  The array is part of the library's code
+ * workspace_bytes are ignored: the split-K partials live in a fixed 64 MiB
+ * device array of the library.  The array is part of the library's code
  * object: every process that runs any of this library's kernels on a device
  * holds those 64 MiB of HBM on it, from the library's first use there until
  * the process ends, whether or not it ever calls this entry point.  A call whose

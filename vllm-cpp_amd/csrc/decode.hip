@@ -846,9 +846,6 @@ __global__ __launch_bounds__(DT ? DT : 1024) void decode_reduce_kernel(DecodeArg
     const int s = blockIdx.y;
     const int h = blockIdx.x;
     const int d = threadIdx.x;
-    // The partition kernel has finished (same stream): return its claim
-    // counters to zero for the next call.
-    if (s == 0 && h == 0 && d < kClaimSequences) a.counters[d * kCounterStride] = 0;
     const int D = DT ? DT : a.head_dim;
     if (DT == 0 && d >= D) return;
     const int G = a.num_heads / a.num_kv_heads;
@@ -1014,7 +1011,6 @@ __global__ __launch_bounds__(kWave) void decode_reduce_wave_kernel(DecodeArgs a)
     const int s = blockIdx.y;
     const int h = blockIdx.x;
     const int d = int(threadIdx.x) * E;
-    if (s == 0 && h == 0 && threadIdx.x < kClaimSequences) a.counters[threadIdx.x * kCounterStride] = 0;
     const int G = a.num_heads / a.num_kv_heads;
     const int kvh = h / G;
     if (a.fkey && h == kvh * G) store_new_token<E>(a, s, kvh, d, DT);

@@ -16,7 +16,7 @@
 #include "launch.hpp"
 #include "vllm_kv_amd.h"
 
-// Split-K partials and claim counters of one call: 64 MiB covers, e.g., 256
+// Split-K partials of one call: 64 MiB covers, e.g., 256
 // sequences x 32 query heads at head_dim 128 with contexts up to ~8k tokens.
 constexpr size_t kScratchBytes = size_t(64) << 20;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
@@ -24,12 +24,8 @@ static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 namespace {
 
 constexpr int kMaxDevices = 64;
-constexpr int kHeaderInts = 256;  // the 1 KiB of claim counters at the start
 std::mutex g_scratch_mutex;
 void* g_scratch[kMaxDevices] = {};
-
-// Zeroes the claim counters (a kernel, not a memset: it may be captured).
-__global__ __launch_bounds__(kHeaderInts) void clear_header_kernel(int* header) { header[threadIdx.x] = 0; }
 
 int scratch_address(void** out) {
     int dev = 0;
@@ -64,7 +60,7 @@ extern "C" int vkv_paged_decode_noalloc(const vkv_decode_params* p, vkv_stream_t
     rc = scratch_address(&ws);
     if (rc != VKV_OK) return rc;
     const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    // The array keeps the last call's contents: the counters start from zero.
-    hipLaunchKernelGGL(clear_header_kernel, dim3(1), dim3(kHeaderInts), 0, st, static_cast<int*>(ws));
+    // (the array keeps the last call's contents; no kernel reads a byte of it
+    // before the same call has written it)
     return vkv::report_launch(vkv::launch_decode(p, plan, ws, st), "vkv_paged_decode_noalloc");
 }
