@@ -201,9 +201,9 @@ int vkv_rope_cos_sin_host(float theta, int32_t head_dim, int32_t max_position, f
  * default; the workspace size covers the smallest), so results may differ in
  * the last bits from an explicit size.
  *
- * Workspace.  A caller workspace holds a 1024-byte header (int 1: the
- * partition size the call chose; zeroing it before first use, as earlier
- * versions required, is harmless) and the partials, and calls that may run
+ * Workspace.  A caller workspace must have its first 1024 bytes zeroed before
+ * its first use (work counters; every call leaves them zero again, apart from
+ * int 1, the partition size the call chose), and calls that may run
  * concurrently need distinct workspaces.  workspace == NULL uses a buffer the
  * library keeps per (device, stream): calls on different streams never share
  * it (hipStreamPerThread: per (device, thread)).  It grows with hipMalloc

@@ -566,8 +566,10 @@ def test_decode_rows_beyond_one_launch(vkv, oracle, cuda):
 def test_decode_more_groups_than_grid(vkv, oracle, cuda, H, Hkv, D):
     """A batch with many more work groups (4 kv-head items each) than the grid,
     which holds one workgroup per resident slot (at most 8 per CU): the groups
-    past the grid are dealt to the workgroups in later rounds.  Sampled
-    sequences against the oracle; a second call must agree bit for bit."""
+    past the grid are dealt to the workgroups in later rounds (matrix-core
+    kernel, D 128) or claimed through the workspace counters (VALU kernel,
+    D 64).  Sampled sequences against the oracle; a second call must agree bit
+    for bit (the counters return to zero)."""
     import torch
     S, bs, P = 2048, 16, 64
     rng = np.random.default_rng(D + H)

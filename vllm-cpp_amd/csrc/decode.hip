@@ -790,7 +790,8 @@ void decode_partition_kernel(const DecodeArgs a) {
     __shared__ float plds[MFMA ? kWavesPerBlock : 1][MFMA ? 16 * G : 1];
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
-    run_partitions<STATIC>(a, a.num_kv_heads, [&](const int P, const int row, const int part, const int kvh)
+    // (matrix-core items are dealt, VALU ones claimed: run_partitions)
+    run_partitions<STATIC, MFMA>(a, a.num_kv_heads, [&](const int P, const int row, const int part, const int kvh)
                                                   __attribute__((always_inline)) {
         if constexpr (MFMA) decode_item_mfma<G, KVT>(a, P, row, kvh, part, lane, plds[wave]);
         else decode_item<IO, KVT, D, G, STATIC>(a, P, row, kvh, part, lane);
@@ -846,6 +847,9 @@ __global__ __launch_bounds__(DT ? DT : 1024) void decode_reduce_kernel(DecodeArg
     const int s = blockIdx.y;
     const int h = blockIdx.x;
     const int d = threadIdx.x;
+    // The partition kernel has finished (same stream): return its claim
+    // counters to zero for the next call.
+    if (s == 0 && h == 0 && d < kClaimSequences) a.counters[d * kCounterStride] = 0;
     const int D = DT ? DT : a.head_dim;
     if (DT == 0 && d >= D) return;
     const int G = a.num_heads / a.num_kv_heads;
@@ -1011,6 +1015,7 @@ __global__ __launch_bounds__(kWave) void decode_reduce_wave_kernel(DecodeArgs a)
     const int s = blockIdx.y;
     const int h = blockIdx.x;
     const int d = int(threadIdx.x) * E;
+    if (s == 0 && h == 0 && threadIdx.x < kClaimSequences) a.counters[threadIdx.x * kCounterStride] = 0;
     const int G = a.num_heads / a.num_kv_heads;
     const int kvh = h / G;
     if (a.fkey && h == kvh * G) store_new_token<E>(a, s, kvh, d, DT);

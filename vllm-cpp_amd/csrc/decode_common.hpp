@@ -17,10 +17,13 @@ namespace dec {
 
 constexpr int kWavesPerBlock = 4;
 static_assert(kWave * kWavesPerBlock == kBlockThreads, "partition kernels launch kBlockThreads threads");
-// Workspace layout: a 1 KiB header (int kChosenPartitionSlot: the partition
-// size the partition kernel chose, for the merge kernel) followed by the
-// partials.
+// Workspace layout: a 1 KiB header holding the work-claim counters (zero
+// between calls: the merge kernel resets them) and int kChosenPartitionSlot
+// (the partition size the partition kernel chose, for the merge kernel),
+// followed by the partials.
 constexpr size_t kWorkspaceHeader = 1024;
+constexpr int kClaimSequences = 8;
+constexpr int kCounterStride = 32;  // ints: one 128-byte line per counter
 constexpr float kLog2e = 1.4426950408889634f;
 // Fixed cost of one item (partial write, merge input, chain start-up) in
 // token-equivalents, for the span estimate of the partition choice.
@@ -64,7 +67,7 @@ struct DecodeArgs {
     float scale_log2;
     int32_t accumulate;
     int32_t num_rows;         // sequences (decode) or query rows (prefill)
-    int* counters;            // the workspace header ints
+    int* counters;            // the workspace header ints (claim counters zero between calls)
     int32_t mfma_enabled;     // use the matrix-core QK^T variant where it applies
     // num_cands > 1: P is the default size, the kernel picks the partition
     // size among cands (ascending) and records it in the workspace header.
@@ -286,7 +289,9 @@ inline size_t lpt_lds_bytes(int n) { return n <= kLptMaxRows ? size_t(2) * size_
 // claim item groups dynamically, so all stay busy until the list runs out.
 // Nothing waits on another workgroup.  item(P, row, partition, sub) runs
 // one item on the calling wave.
-template <bool STATIC = false, class Item>
+// DEAL: items dealt in a snake (no claims); otherwise claimed through the
+// workspace counters.
+template <bool STATIC = false, bool DEAL = false, class Item>
 __device__ __forceinline__ void run_partitions(const DecodeArgs& a, const int items_per_pair, Item&& item) {
     extern __shared__ int prefix[];  // [num_rows + 1] exclusive prefix of partitions per row
     const int lane = threadIdx.x & (kWave - 1);
@@ -432,18 +437,9 @@ __device__ __forceinline__ void run_partitions(const DecodeArgs& a, const int it
 
     }
     // Item groups of 4 consecutive items go to a workgroup, one item per
-    // wave, dealt in a snake over the grid (every workgroup is resident: the
-    // grid holds one per resident slot): round r gives group r W + b to
-    // workgroup b when r is even and to W - 1 - b when r is odd, so in the
-    // longest-first order the later (shorter) groups go first to the
-    // workgroups whose earlier groups were the longest.  Nothing is claimed:
-    // a wave starts its next item as soon as it has finished its own, without
-    // waiting for its workgroup's other waves or for a counter.
+    // wave.
     const int num_groups = stat ? int(gridDim.x) : (num_items + kWavesPerBlock - 1) / kWavesPerBlock;
-    const int W = int(gridDim.x);
-    for (int r = 0;; ++r) {
-        const int g = r * W + ((r & 1) ? W - 1 - int(blockIdx.x) : int(blockIdx.x));
-        if (g >= num_groups) break;  // (later rounds are further on)
+    auto run_group = [&](const int g) __attribute__((always_inline)) {
         const int it = g * kWavesPerBlock + wave;
         if (it < num_items) {
             const int pair = it / items_per_pair;
@@ -465,6 +461,58 @@ __device__ __forceinline__ void run_partitions(const DecodeArgs& a, const int it
                 item(P, lo, pair - prefix[lo], sub);
             }
         }
+    };
+    if constexpr (DEAL) {
+        // Dealt in a snake over the grid (every workgroup is resident: the
+        // grid holds one per resident slot): round r gives group r W + b to
+        // workgroup b when r is even and to W - 1 - b when r is odd, so in the
+        // longest-first order the later (shorter) groups go first to the
+        // workgroups whose earlier groups were the longest.  Nothing is
+        // claimed: a wave starts its next item as soon as it has finished its
+        // own, without waiting for its workgroup's other waves or for a
+        // counter.  (The matrix-core kernels: their items' times follow their
+        // lengths.)
+        const int W = int(gridDim.x);
+        for (int r = 0;; ++r) {
+            const int g = r * W + ((r & 1) ? W - 1 - int(blockIdx.x) : int(blockIdx.x));
+            if (g >= num_groups) break;  // (later rounds are further on)
+            run_group(g);
+        }
+        return;
+    }
+    // Claimed (the VALU kernels, whose items' times vary with what shares
+    // their CU).  Round 0 is static: workgroup b takes group b.  Later groups
+    // g >= gridDim.x are dealt in 8 interleaved sequences g = gridDim.x + 8k +
+    // q, each with its own counter (separate cache lines, so claims on
+    // different sequences do not queue on one address).  A workgroup claims
+    // from sequence blockIdx.x % 8 first and moves on to the next sequence when
+    // one is exhausted, so every group is processed exactly once wherever the
+    // workgroups run.  The merge kernel returns the counters to zero.
+    __shared__ int next_group;
+    const int g0 = int(gridDim.x);
+    int g = blockIdx.x;
+    int q = blockIdx.x % kClaimSequences;
+    int tried = 0;
+    while (g < num_groups) {
+        run_group(g);
+        if (g0 >= num_groups) break;  // the grid covers every group: nothing to claim
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            int next = num_groups;
+            while (tried < kClaimSequences) {
+                const int k = atomicAdd(a.counters + q * kCounterStride, 1);
+                const int cand = g0 + kClaimSequences * k + q;
+                if (cand < num_groups) {
+                    next = cand;
+                    break;
+                }
+                q = (q + 1) % kClaimSequences;  // this sequence is exhausted
+                ++tried;
+            }
+            next_group = next;
+        }
+        __syncthreads();
+        g = next_group;
     }
 }
 

@@ -60,7 +60,8 @@ extern "C" int vkv_paged_decode_noalloc(const vkv_decode_params* p, vkv_stream_t
     rc = scratch_address(&ws);
     if (rc != VKV_OK) return rc;
     const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    // (the array keeps the last call's contents; no kernel reads a byte of it
-    // before the same call has written it)
+    // (the array keeps the last call's contents: its claim counters start
+    // zeroed, as device memory of a code object does, and every call's merge
+    // kernel returns them to zero)
     return vkv::report_launch(vkv::launch_decode(p, plan, ws, st), "vkv_paged_decode_noalloc");
 }
