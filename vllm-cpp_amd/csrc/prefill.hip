@@ -1799,7 +1799,8 @@ __global__ __launch_bounds__(64 * kWideWaves) void prefill_wide8_kernel(PrefillA
 // Work list of the matrix-core kernels, in one workgroup: items (s, b * Hkv +
 // kvh), row block b of every sequence with >= 2 query tokens, ordered by the
 // number of key tiles they stage, most first, so that persistent workgroups
-// claiming them in turn form a longest-processing-time schedule (short items
+// taking them in turn (dealt in a snake by the direct-load kernels, claimed by
+// prefill_mfma_kernel) form a longest-processing-time schedule (short items
 // fill in at the end).  A row block of rows_per_item rows (query tokens
 // times row_mult heads) sees keys 0 .. kend - 1 with kend = prior + its last
 // token + 1; a histogram over the tile counts (one bin per possible count,
