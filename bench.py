@@ -678,18 +678,6 @@ def suite_c5(dev, steps, warmup):
     td = _events_ms(decode, DECODE_GROUPS * DECODE_CALLS, stream, groups=DECODE_GROUPS)
     kvb = cfg.kv_bytes(1, 4)
     gbs = kvb / (td[0] * 1e-3) / 1e9
-
-    # the step: append + decode as two calls, and as one vkv_paged_decode_append
-    # (the new tokens quantised inside the decode's launches), alternating
-    def step_fused():
-        vkv.paged_decode_append(out, q, kc, vc, bt, cl, cfg.scale, nk, nv, slots, key_scales=ks, value_scales=vs,
-                                stream=stream)
-
-    _warm(lambda: (append(), decode(), step_fused()), warmup)
-    rounds = [(_events_ms(lambda: (append(), decode()), steps, stream), _events_ms(step_fused, steps, stream))
-              for _ in range(3)]
-    t_two = sorted(r[0] for r in rounds)[1]
-    t_fused = sorted(r[1] for r in rounds)[1]
     from oracle import oracle
     idx = list(range(16))
     ctx = lay.context_lens[idx]
@@ -712,7 +700,6 @@ def suite_c5(dev, steps, warmup):
             "context_tokens": int(lay.context_lens.astype(np.int64).sum()), "kv_bytes": kvb,
             "decode_us_median": round(td[0] * 1e3, 2), "decode_us_p10_p90": [round(td[1] * 1e3, 2), round(td[2] * 1e3, 2)],
             "append_us_median": round(ta[0] * 1e3, 2),
-            "step_us_two_calls": round(t_two[0] * 1e3, 2), "step_us_fused": round(t_fused[0] * 1e3, 2),
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(gbs / HBM_PEAK_GBS, 4)},
             "cpu_baseline": {"gbs": round(cpu_bytes / sec / 1e9, 3), "cores": thr, "kind": "port",

@@ -252,15 +252,13 @@ int vkv_paged_decode(const vkv_decode_params* p, vkv_stream_t stream);
  * those of vkv_reshape_and_cache(ap) followed by vkv_paged_decode(dp) on the
  * same stream (workspace as for vkv_paged_decode).  When the two fit together
  * — token s of ap is sequence s's new token (ap->num_tokens == dp->num_seqs),
- * both name the same caches with the same geometry and pool — fp16 or fp32
- * with source rows of the cache's type, or FP8 e4m3 (the same scale arrays)
- * with fp16 rows, fp16 queries, head_dim 128 and blocks of at least 16 tokens —
- * source rows 16-byte aligned with token strides a multiple of 16 bytes, and a
- * shape the tuned decode kernels run — the append is fused into the decode
+ * both name the same fp16 or fp32 caches with the same geometry and pool,
+ * source rows of the cache's type, 16-byte aligned with token strides a
+ * multiple of 16 bytes, and a shape the tuned decode kernels run — the append
+ * is fused into the decode
  * launches (one launch fewer per step): each sequence's last position is read
- * from its new rows when ap's slot for the token is that position's slot (FP8:
- * quantised there by the append's rule, the same codes and scale), and the
- * merge kernel stores the rows (FP8: codes and scales).  The fused form assumes what a decode step
+ * from its new rows when ap's slot for the token is that position's slot, and
+ * the merge kernel stores the rows.  The fused form assumes what a decode step
  * guarantees: the slot of an appended token is read in this call only as its
  * own sequence's last position (a slot of no other sequence's context).
  * Otherwise the two calls run as they are. */

@@ -110,89 +110,33 @@ def test_decode_append_slots_elsewhere(vkv, cuda):
     _assert_same(vkv, cuda, (lay, k, v, q, nk, nv, slots))
 
 
-def _run8(vkv, cuda, lay, k, v, q, nk, nv, slots, fused):
-    """The step over an FP8 cache (the pool quantised by the GPU append first):
-    output, codes and scales."""
+def test_decode_append_fp8_cache_runs_both_calls(vkv, cuda):
+    """FP8 caches are not fused: the call is the append then the decode."""
     import torch
+    rng = np.random.default_rng(13)
+    lay, k, v, q, nk, nv, slots = _case(rng, 32, 8, 128, 16, [5, 200, 777])
     N, bs, Hkv, D = k.shape
-    k8 = torch.zeros((N, bs, Hkv, D), dtype=torch.uint8, device=cuda)
-    v8 = torch.zeros_like(k8)
-    ks = torch.zeros((N, bs, Hkv), dtype=torch.float32, device=cuda)
-    vs = torch.zeros_like(ks)
-    all_slots = torch.arange(N * bs, dtype=torch.int32, device=cuda)
-    vkv.reshape_and_cache(to_dev(k, cuda).reshape(-1, Hkv, D), to_dev(v, cuda).reshape(-1, Hkv, D), k8, v8,
-                          all_slots, ks, vs)
-    out = torch.zeros(q.shape, dtype=torch.float16, device=cuda)
-    args = (out, to_dev(q, cuda), k8, v8, to_dev(lay.block_tables, cuda), to_dev(lay.context_lens, cuda),
-            1.0 / np.sqrt(D))
-    nkd, nvd, sd = to_dev(nk, cuda), to_dev(nv, cuda), to_dev(slots, cuda)
-    if fused:
-        vkv.paged_decode_append(*args, nkd, nvd, sd, key_scales=ks, value_scales=vs)
-    else:
-        vkv.reshape_and_cache(nkd, nvd, k8, v8, sd, ks, vs)
-        vkv.paged_decode(*args, key_scales=ks, value_scales=vs)
-    torch.cuda.synchronize()
-    return [t.cpu().numpy() for t in (out, k8, v8, ks, vs)]
-
-
-FP8_CASES = [
-    # (H, Hkv, D, bs, previous context per sequence): kernels reached
-    (32, 8, 128, 16, [5, 200, 777]),                 # group 4, static small-call grid
-    (32, 8, 128, 16, list(range(300, 4000, 37))),    # group 4, rows of many partitions, dealt items
-    (28, 4, 128, 32, [0, 31, 32, 700, 2047]),        # group 7: one chunk at a time; a token opening a block
-    (64, 8, 128, 64, [3, 900, 4000]),                # group 8, blocks of 64
-    (16, 8, 128, 8, [8, 64, 519]),                   # blocks of 8: VALU items, the two calls
-]
-
-
-@pytest.mark.parametrize("H,Hkv,D,bs,prev", FP8_CASES)
-def test_decode_append_fp8_matches_two_calls(vkv, cuda, H, Hkv, D, bs, prev):
-    """FP8 caches: the item that reads a row's new token quantises it as the
-    append would and the merge kernel stores the codes and scales, so output,
-    codes and scales equal the two calls bit for bit (new rows with x8
-    outliers, which set the scales)."""
-    rng = np.random.default_rng(13 + H + bs)
-    lay, k, v, q, nk, nv, slots = _case(rng, H, Hkv, D, bs, prev)
-    nk = nk.copy()
-    nv = nv.copy()
-    nk[..., ::9] *= 8
-    nv[..., 5::11] *= 8
-    a = _run8(vkv, cuda, lay, k, v, q, nk, nv, slots, fused=False)
-    b = _run8(vkv, cuda, lay, k, v, q, nk, nv, slots, fused=True)
-    for x, y, what in zip(a, b, ("output", "key codes", "value codes", "key scales", "value scales")):
-        assert x.tobytes() == y.tobytes(), f"{what} differ from the two-call sequence"
-
-
-def test_decode_append_fp8_slots_elsewhere(vkv, cuda):
-    """FP8: a skipped token (slot -1) and a token bound for an unused slot are
-    stored (or skipped) as the append would."""
-    rng = np.random.default_rng(12)
-    lay, k, v, q, nk, nv, slots = _case(rng, 32, 8, 128, 16, [40, 300, 17, 900], extra_blocks=4)
-    used = set(int(b) for b in lay.block_tables.ravel() if b >= 0)
-    spare = next(b for b in range(lay.num_blocks) if b not in used)
-    slots = slots.copy()
-    slots[0] = -1
-    slots[2] = spare * 16 + 5
-    a = _run8(vkv, cuda, lay, k, v, q, nk, nv, slots, fused=False)
-    b = _run8(vkv, cuda, lay, k, v, q, nk, nv, slots, fused=True)
-    for x, y in zip(a, b):
-        assert x.tobytes() == y.tobytes()
-
-
-def test_decode_append_fp8_is_fused(vkv, cuda):
-    """FP8: as test_decode_append_is_fused, the fused form shows itself by
-    reading an appended slot from the new rows only at its own sequence's
-    last position (the merge stores the codes after every read)."""
-    rng = np.random.default_rng(17)
-    lay, k, v, q, nk, nv, slots = _case(rng, 32, 8, 128, 16, [100, 50] + list(range(300, 1060, 20)))
-    slots = slots.copy()
-    slots[1] = int(lay.block_tables[0, 2]) * 16 + 3  # position 35 of sequence 0
-    a = _run8(vkv, cuda, lay, k, v, q, nk, nv, slots, fused=False)
-    b = _run8(vkv, cuda, lay, k, v, q, nk, nv, slots, fused=True)
-    for x, y in zip(a[1:], b[1:]):
-        assert x.tobytes() == y.tobytes()
-    assert a[0][0].tobytes() != b[0][0].tobytes()          # sequence 0 read the slot before the store
-    assert a[0][1:].tobytes() == b[0][1:].tobytes()
+    res = []
+    for fused in (False, True):
+        k8 = torch.zeros((N, bs, Hkv, D), dtype=torch.uint8, device=cuda)
+        v8 = torch.zeros_like(k8)
+        ks = torch.zeros((N, bs, Hkv), dtype=torch.float32, device=cuda)
+        vs = torch.zeros_like(ks)
+        all_slots = torch.arange(N * bs, dtype=torch.int32, device=cuda)
+        vkv.reshape_and_cache(to_dev(k, cuda).reshape(-1, Hkv, D), to_dev(v, cuda).reshape(-1, Hkv, D), k8, v8,
+                              all_slots, ks, vs)
+        out = torch.zeros(q.shape, dtype=torch.float16, device=cuda)
+        args = (out, to_dev(q, cuda), k8, v8, to_dev(lay.block_tables, cuda), to_dev(lay.context_lens, cuda),
+                1.0 / np.sqrt(D))
+        nkd, nvd, sd = to_dev(nk, cuda), to_dev(nv, cuda), to_dev(slots, cuda)
+        if fused:
+            vkv.paged_decode_append(*args, nkd, nvd, sd, key_scales=ks, value_scales=vs)
+        else:
+            vkv.reshape_and_cache(nkd, nvd, k8, v8, sd, ks, vs)
+            vkv.paged_decode(*args, key_scales=ks, value_scales=vs)
+        torch.cuda.synchronize()
+        res.append([t.cpu().numpy().tobytes() for t in (out, k8, v8, ks, vs)])
+    assert res[0] == res[1]
 
 
 @pytest.mark.parametrize("prev", [[100, 50, 300], [100, 50] + list(range(300, 1060, 20))])  # static grid, claim loop

@@ -100,12 +100,25 @@ __global__ __launch_bounds__(kBlockThreads) void append_rows_kernel(AppendArgs a
     }
 }
 
+// x / s exactly as the correctly rounded fp32 quotient would encode to e4m3.
+// z = x * fl(1/s) is within 2 fp32 ulps of fl(x / s), so the two can only
+// encode differently when an e4m3 rounding midpoint is within that distance of
+// z: normal e4m3 range midpoints are the fp32 values whose 20 mantissa bits
+// below the kept 3 equal 0x80000.  Those cases, the e4m3 subnormal range
+// (|z| < 2^-6, other midpoints) and non-finite values take the IEEE division.
+__device__ __forceinline__ float quotient(float x, float s, float rinv) {
+    const float z = x * rinv;
+    const uint32_t b = as_u32(z) & 0x7FFFFFFFu;
+    const int d = int(b & 0xFFFFFu) - 0x80000;
+    if (b < 0x3C800000u || b >= 0x7F800000u || (d >= -4 && d <= 4)) return x / s;
+    return z;
+}
 
 // Quantise-on-append to e4m3fn.  A group of LPT = head_dim/16 consecutive
 // lanes holds one (token, kv head) vector, 16 elements per lane, for K and V
 // at once (both loaded before either is used); each group's amax comes from a
 // DPP max reduction, every lane forms its 16 quotients x / scale (exact, see
-// fp8_quotient()) and encodes them with gfx950's v_cvt_pk_fp8_f32 (OCP e4m3fn,
+// quotient()) and encodes them with gfx950's v_cvt_pk_fp8_f32 (OCP e4m3fn,
 // round to nearest even).  Quotients are finite and within 448 (1 + 2^-22)
 // unless the input holds inf or NaN; a wave that meets one encodes with the
 // software rule (f32_to_fp8_sat: NaN -> 0x7F, saturation) instead.
@@ -161,7 +174,7 @@ __global__ __launch_bounds__(kBlockThreads) void append_fp8_kernel(AppendArgs a)
             const float rinv = 1.0f / scale[kv];  // correctly rounded
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                x[kv][e] = fp8_quotient(x[kv][e], scale[kv], rinv);
+                x[kv][e] = quotient(x[kv][e], scale[kv], rinv);
                 finite &= (as_u32(x[kv][e]) & 0x7F800000u) != 0x7F800000u;
             }
         }
@@ -228,7 +241,7 @@ __global__ __launch_bounds__(kBlockThreads) void append_elems_kernel(AppendArgs 
                 const float rinv = 1.0f / scale;
                 uint8_t* out = reinterpret_cast<uint8_t*>(dst[kv]) + int64_t(head) * head_dim;
                 for (int d = lane; d < head_dim; d += kWave)
-                    out[d] = uint8_t(f32_to_fp8_sat(fp8_quotient(static_cast<float>(src[kv][d]), scale, rinv)));
+                    out[d] = uint8_t(f32_to_fp8_sat(quotient(static_cast<float>(src[kv][d]), scale, rinv)));
                 if (lane == 0) (kv ? a.value_scales : a.key_scales)[slot * a.num_kv_heads + head] = scale;
             }
         } else {

@@ -223,30 +223,6 @@ __device__ __forceinline__ float fp8_scale_from_amax(float amax) {
     return amax == 0.0f ? 1.0f : amax / 448.0f;
 }
 
-// x / s exactly as the correctly rounded fp32 quotient would encode to e4m3.
-// z = x * fl(1/s) is within 2 fp32 ulps of fl(x / s), so the two can only
-// encode differently when an e4m3 rounding midpoint is within that distance of
-// z: normal e4m3 range midpoints are the fp32 values whose 20 mantissa bits
-// below the kept 3 equal 0x80000.  Those cases, the e4m3 subnormal range
-// (|z| < 2^-6, other midpoints) and non-finite values take the IEEE division.
-__device__ __forceinline__ float fp8_quotient(float x, float s, float rinv) {
-    const float z = x * rinv;
-    const uint32_t b = as_u32(z) & 0x7FFFFFFFu;
-    const int d = int(b & 0xFFFFFu) - 0x80000;
-    if (b < 0x3C800000u || b >= 0x7F800000u || (d >= -4 && d <= 4)) return x / s;
-    return z;
-}
-
-// The e4m3 code of x / s (rinv = the correctly rounded 1 / s): the exact
-// quotient, encoded by gfx950's v_cvt_pk_fp8_f32 (OCP e4m3fn, round to nearest
-// even) when it is finite, else by the software rule (f32_to_fp8_sat); the two
-// agree on every finite quotient, which stays within 448 (1 + 2^-22).
-__device__ __forceinline__ uint32_t fp8_code(float x, float s, float rinv) {
-    const float q = fp8_quotient(x, s, rinv);
-    if ((as_u32(q) & 0x7F800000u) == 0x7F800000u) return f32_to_fp8_sat(q);
-    return uint32_t(__builtin_amdgcn_cvt_pk_fp8_f32(q, q, 0, false)) & 0xFFu;
-}
-
 // Attention logit scale in the log2 domain (scale * log2 e), as the decode
 // and prefill kernels take it.  A scale of magnitude below 2^-100 (zero
 // included) runs as +-2^-100: the reference then weights every key

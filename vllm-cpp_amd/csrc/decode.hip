@@ -688,81 +688,11 @@ __device__ __forceinline__ void decode_item_mfma(const DecodeArgs& a, const int 
     // time so that the 8 G accumulators per lane fit without spilling.
     const int nc = (n + CH - 1) / CH;
     const bool ragged = (n % CH) != 0;
-    // FP8 new token tk of the chunk (0..15): K lanes
-    // (col tk) hold dims 32 quad .. + 31, V lanes (quad tk % 4) dims 8 col ..
-    // + 7 of load tk / 4; scales in lane tk (K) and 16 + tk (V).  amax over the
-    // (token, head) vector, scale = amax / 448, exact quotients: the append's
-    // codes and scales, bit for bit.
-    auto fuse_fp8 = [&](Chunk& ch, const int tk) __attribute__((always_inline)) {
-        const char* kr = a.fkey + s * a.fkey_stride + kvh * D * 2;
-        const char* vr = a.fval + s * a.fval_stride + kvh * D * 2;
-        const bool kl = col == tk, vl = quad == (tk & 3);
-        auto half_at = [](const u32x4& w, const int e) __attribute__((always_inline)) {
-            return f16_bits_to_f32(uint16_t((w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu));
-        };
-        const u32x4 zero = {0u, 0u, 0u, 0u};
-        // K: the amax pass, then the rows again for the codes (a memory
-        // barrier between, so the first pass's registers are not kept)
-        float ak = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const u32x4 w = kl ? load16(kr + (32 * quad + 8 * i) * 2) : zero;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) ak = fmaxf(ak, fabsf(half_at(w, e)));
-        }
-        ak = fmaxf(ak, __shfl_xor(ak, 16, kWave));  // the token's 4 K lanes
-        ak = fmaxf(ak, __shfl_xor(ak, 32, kWave));
-        const float ksc = fp8_scale_from_amax(ak);
-        const float krinv = 1.0f / ksc;  // correctly rounded
-        asm volatile("" ::: "memory");
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const u32x4 w0 = kl ? load16(kr + (32 * quad + 16 * j) * 2) : zero;
-            const u32x4 w1 = kl ? load16(kr + (32 * quad + 16 * j + 8) * 2) : zero;
-#pragma unroll
-            for (int wd = 0; wd < 4; ++wd) {
-                uint32_t packed = 0;
-#pragma unroll
-                for (int b = 0; b < 4; ++b)
-                    packed |= fp8_code(half_at(wd < 2 ? w0 : w1, 4 * (wd & 1) + b), ksc, krinv) << (8 * b);
-                if (kl) ch.k[j][wd] = packed;
-            }
-        }
-        // V: the token's 16 lanes, 8 dims each
-        const u32x4 vw = vl ? load16(vr + 8 * col * 2) : zero;
-        float av = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) av = fmaxf(av, fabsf(half_at(vw, e)));
-        av = group_max<16>(av);
-        const float vsc = fp8_scale_from_amax(av);
-        const float vrinv = 1.0f / vsc;
-        u32x2 vc = {0u, 0u};
-#pragma unroll
-        for (int w = 0; w < 2; ++w)
-#pragma unroll
-            for (int b = 0; b < 4; ++b) vc[w] |= fp8_code(half_at(vw, 4 * w + b), vsc, vrinv) << (8 * b);
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-            if (vl && u == (tk >> 2)) ch.v8[u] = vc;
-        const float ksu = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ksc), tk));
-        const float vsu =
-            __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, vsc), 16 * (tk & 3)));
-        if (lane == tk) ch.sc1 = ksu;
-        if (lane == 16 + tk) ch.sc1 = vsu;
-    };
-    // Fused append: the row's last position reads the new token's rows when
-    // the append targets that position's slot (FP8: quantised here as the
-    // append would, then stored).  Applied to the last chunk right after its
-    // loads are issued.
+    // Fused append (fp16): the row's last position reads the new token's rows
+    // when the append targets that position's slot.  Applied to the last
+    // chunk right after its loads are issued.
     auto fuse_last = [&](Chunk& ch, const int c) __attribute__((always_inline)) {
-        if constexpr (FP8) {
-            if (a.fkey && a.fquant && t0 + n == ctx) {
-                const int pn = n - 1;
-                const int pblk = __builtin_amdgcn_readlane(my_block, (pn >> a.bs_log2) & 63);
-                const int64_t pslot = (int64_t(pblk) << a.bs_log2) + (pn & bs_mask);
-                if (int64_t(a.fslots[s]) == pslot) fuse_fp8(ch, pn - c);
-            }
-        } else {
+        if constexpr (!FP8) {
             if (a.fkey && t0 + n == ctx) {
                 const int pn = n - 1;
                 const int pblk = __builtin_amdgcn_readlane(my_block, (pn >> a.bs_log2) & 63);
@@ -792,7 +722,6 @@ __device__ __forceinline__ void decode_item_mfma(const DecodeArgs& a, const int 
         }
         Chunk x;
         load_chunk(x, ci * CH);
-        fuse_last(x, ci * CH);
         if (ragged) compute_chunk(x, ci * CH, std::true_type{});
         else compute_chunk(x, ci * CH, std::false_type{});
     } else {
@@ -901,34 +830,6 @@ __device__ __forceinline__ void store_new_token(const DecodeArgs& a, const int s
     }
 }
 
-// The FP8 form (fquant): a wave holds row s's head vector for kv head kvh, E
-// elements per lane (D = 64 E); amax over the wave,
-// scale = amax / 448, the exact quotients encoded as the append encodes
-// them: the append's codes and scale, bit for bit.
-template <int E>
-__device__ __forceinline__ void store_new_token_fp8(const DecodeArgs& a, const int s, const int kvh, const int d,
-                                                    const int D) {
-    static_assert(E == 2, "two fp16 elements per lane (head_dim 128)");
-    const int64_t slot = a.fslots[s];
-    if (slot < 0 || slot >= a.fnum_slots) return;  // (uniform: the wave's row)
-    const uint32_t kw = *reinterpret_cast<const uint32_t*>(a.fkey + s * a.fkey_stride + (int64_t(kvh) * D + d) * 2);
-    const uint32_t vw = *reinterpret_cast<const uint32_t*>(a.fval + s * a.fval_stride + (int64_t(kvh) * D + d) * 2);
-    const float k0 = f16_bits_to_f32(uint16_t(kw & 0xFFFFu)), k1 = f16_bits_to_f32(uint16_t(kw >> 16));
-    const float v0 = f16_bits_to_f32(uint16_t(vw & 0xFFFFu)), v1 = f16_bits_to_f32(uint16_t(vw >> 16));
-    const float ksc = fp8_scale_from_amax(group_max<kWave>(fmaxf(fabsf(k0), fabsf(k1))));
-    const float vsc = fp8_scale_from_amax(group_max<kWave>(fmaxf(fabsf(v0), fabsf(v1))));
-    const float krinv = 1.0f / ksc, vrinv = 1.0f / vsc;  // correctly rounded
-    const int64_t dst = (slot * a.num_kv_heads + kvh) * D + d;
-    *reinterpret_cast<uint16_t*>(const_cast<char*>(a.kc) + dst) =
-        uint16_t(fp8_code(k0, ksc, krinv) | (fp8_code(k1, ksc, krinv) << 8));
-    *reinterpret_cast<uint16_t*>(const_cast<char*>(a.vc) + dst) =
-        uint16_t(fp8_code(v0, vsc, vrinv) | (fp8_code(v1, vsc, vrinv) << 8));
-    if (d == 0) {
-        const_cast<float*>(a.ks)[slot * a.num_kv_heads + kvh] = ksc;
-        const_cast<float*>(a.vs)[slot * a.num_kv_heads + kvh] = vsc;
-    }
-}
-
 // Merge the partitions of one (sequence, head): one thread per output element.
 // The kernel is latency-bound (a few KiB per workgroup), so the partials of
 // the first kMergeBatch partitions are loaded together with the context length,
@@ -953,7 +854,7 @@ __global__ __launch_bounds__(DT ? DT : 1024) void decode_reduce_kernel(DecodeArg
     if (DT == 0 && d >= D) return;
     const int G = a.num_heads / a.num_kv_heads;
     const int kvh = h / G;
-    if (a.fkey && !a.fquant && h == kvh * G) store_new_token<1>(a, s, kvh, d, D);
+    if (a.fkey && h == kvh * G) store_new_token<1>(a, s, kvh, d, D);
     const int64_t slot0 = (int64_t(s) * a.num_kv_heads + kvh) * a.max_parts * G + (h - kvh * G);
     const float* ml = a.part_ml + slot0 * 2;
     const float* o = a.part_o + slot0 * D + d;
@@ -1117,10 +1018,7 @@ __global__ __launch_bounds__(kWave) void decode_reduce_wave_kernel(DecodeArgs a)
     if (s == 0 && h == 0 && threadIdx.x < kClaimSequences) a.counters[threadIdx.x * kCounterStride] = 0;
     const int G = a.num_heads / a.num_kv_heads;
     const int kvh = h / G;
-    if (a.fkey && h == kvh * G) {
-        if (!a.fquant) store_new_token<E>(a, s, kvh, d, DT);
-        else if constexpr (E == 2) store_new_token_fp8<E>(a, s, kvh, d, DT);  // (fused FP8: head_dim 128 only)
-    }
+    if (a.fkey && h == kvh * G) store_new_token<E>(a, s, kvh, d, DT);
     const int64_t slot0 = (int64_t(s) * a.num_kv_heads + kvh) * a.max_parts * G + (h - kvh * G);
     const float* ml = a.part_ml + slot0 * 2;
     const float* o = a.part_o + slot0 * DT + d;
@@ -1341,7 +1239,6 @@ int launch_rows(const vkv_decode_params* p, const DecodePlan& plan, void* worksp
     a.fbytes = fa ? fa->elem_bytes : 0;
     a.fslots = fa ? fa->slots : nullptr;
     a.fnum_slots = fa ? fa->num_slots : 0;
-    a.fquant = fa ? fa->quantise : 0;
 
     const int G = p->num_heads / p->num_kv_heads;
     const int D = p->head_dim;
@@ -1431,21 +1328,13 @@ int launch_decode(const vkv_decode_params* p, const DecodePlan& plan, void* work
 bool decode_append_fusable(const vkv_append_params* ap, const vkv_decode_params* p) {
     const bool f16 = ap->src_dtype == VKV_DTYPE_F16 && ap->cache_dtype == VKV_DTYPE_F16;
     const bool f32 = ap->src_dtype == VKV_DTYPE_F32 && ap->cache_dtype == VKV_DTYPE_F32;
-    // FP8 caches: fp16 rows into the matrix-core kernel's items (fp16 queries
-    // at head_dim 128, blocks of 16 tokens or more: launch_g's condition for
-    // that kernel), which quantise the new token themselves; the append's
-    // scale arrays must be the ones the decode reads
-    const bool fp8 = ap->src_dtype == VKV_DTYPE_F16 && ap->cache_dtype == VKV_DTYPE_FP8_E4M3 && VKV_DECODE_MFMA &&
-                     p->io_dtype == VKV_DTYPE_F16 && p->head_dim == 128 && p->block_size >= 16 &&
-                     ap->key_scales != nullptr &&
-                     ap->key_scales == p->key_scales && ap->value_scales == p->value_scales;
     const int64_t eb = f32 ? 4 : 2;
     const int64_t row = int64_t(ap->num_kv_heads) * ap->head_dim;
     const int64_t ks = (ap->key_stride ? ap->key_stride : row) * eb;
     const int64_t vs = (ap->value_stride ? ap->value_stride : row) * eb;
     const uintptr_t src = reinterpret_cast<uintptr_t>(ap->key) | reinterpret_cast<uintptr_t>(ap->value);
     return ap->num_tokens == p->num_seqs && p->num_seqs > 0 && ap->key_cache == p->key_cache &&
-           ap->value_cache == p->value_cache && (f16 || f32 || fp8) && p->kv_dtype == ap->cache_dtype &&
+           ap->value_cache == p->value_cache && (f16 || f32) && p->kv_dtype == ap->cache_dtype &&
            ap->num_kv_heads == p->num_kv_heads && ap->head_dim == p->head_dim &&
            ap->block_size == p->block_size && ap->num_blocks == p->num_blocks && (src & 15u) == 0 &&
            ks % 16 == 0 && vs % 16 == 0 &&
@@ -1455,7 +1344,7 @@ bool decode_append_fusable(const vkv_append_params* ap, const vkv_decode_params*
 
 int launch_decode_append(const vkv_append_params* ap, const vkv_decode_params* p, const DecodePlan& plan,
                          void* workspace, hipStream_t st) {
-    const int eb = ap->src_dtype == VKV_DTYPE_F32 ? 4 : 2;  // (the source rows' element bytes)
+    const int eb = ap->cache_dtype == VKV_DTYPE_F32 ? 4 : 2;
     const int64_t row = int64_t(ap->num_kv_heads) * ap->head_dim;
     FusedAppend fa;
     fa.key = static_cast<const char*>(ap->key);
@@ -1465,7 +1354,6 @@ int launch_decode_append(const vkv_append_params* ap, const vkv_decode_params* p
     fa.elem_bytes = eb;
     fa.slots = ap->slot_mapping;
     fa.num_slots = int64_t(ap->num_blocks) * ap->block_size;
-    fa.quantise = ap->cache_dtype == VKV_DTYPE_FP8_E4M3 ? 1 : 0;
     return launch_rows(p, plan, workspace, nullptr, nullptr, nullptr, st, &fa);
 }
 

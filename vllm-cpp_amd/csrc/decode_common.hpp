@@ -103,12 +103,6 @@ struct DecodeArgs {
     int32_t fbytes;  // element bytes of the rows and the cache (2 or 4)
     const int32_t* fslots;
     int64_t fnum_slots;
-    // FP8 caches (fquant = 1, fp16 rows, head_dim 128, the matrix-core
-    // item): the item that reads row s's new token quantises it as the append
-    // would (per-(token, head) scale, the same codes) and uses those codes and
-    // scales; the merge kernel quantises the rows again and stores codes and
-    // scales.
-    int32_t fquant;
 };
 
 // The new token of an appending decode call (see DecodeArgs::fkey).
@@ -120,7 +114,6 @@ struct FusedAppend {
     int32_t elem_bytes;
     const int32_t* slots;
     int64_t num_slots;
-    int32_t quantise;  // FP8 cache: the kernels quantise the rows
 };
 
 // The shapes decode.hip's fixed-shape kernels are built for; every other
